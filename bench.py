@@ -1,0 +1,224 @@
+#!/usr/bin/env python3
+"""Decode-attention benchmark on one MI355X.
+
+Metric: decode-attention achieved HBM GB/s (% of the 8 TB/s
+peak) + us/call at KV 512 / 8K / 32K.  Workload of `value`: config 2 -- one
+qd_decode_attention call over 16 heads x 128 dims x 8192 fp16 KV rows in the
+reference engine's [pos][16*128] cache layout.
+
+A step is one call of the public C ABI over one layer.  Steps cycle through
+enough layers (>= 1 GiB of K+V) that every call streams its rows from HBM, not
+from the 256 MB Infinity Cache.  The timed loop runs natively
+(libqdiy_bench.so) on torch's current stream between two HIP events; us/call
+= elapsed / steps.  achieved GB/s = algorithmic bytes per call / us per call
+with B(L) = 8192 + 8192*L (Q in, O out, K and V rows read once).
+
+The CPU baseline is the repository's C restatement of the reference kernels
+(oracle/) on the host cores of the same box, on a bounded sample of the same
+workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "llm-inference-diy_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+H, D = 16, 128
+HID = H * D
+PEAK_GBPS = 8000.0
+KV_LENS = (512, 8192, 32768)
+HEADLINE_L = 8192
+METRIC = "decode-attention achieved HBM GB/s (% of peak) + µs/call at KV 512/8K/32K"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode_attention_L8192.json")
+
+
+def algo_bytes(L: int) -> int:
+    return 2 * H * D * 2 + 2 * H * L * D * 2     # Q + O, K + V
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bench_lib():
+    import qdiy
+
+    qdiy.load()
+    path = os.path.join(PKG, "lib", "libqdiy_bench.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built: run python llm-inference-diy_amd/build.py")
+    lib = ctypes.CDLL(path)
+    vp, i, ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
+    lib.qd_bench_decode_attention.argtypes = [vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
+    return lib
+
+
+def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int = 0):
+    import torch
+
+    import qdiy
+
+    layer_bytes = 2 * L * HID * 2
+    n_layers = max(3, math.ceil((1 << 30) / layer_bytes))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(1000 + L)
+    kscale = 0.5 if L == HEADLINE_L else 1.0       # config 2 scales K by 0.5
+    kc = torch.empty(n_layers * L * HID, dtype=torch.float16, device="cuda")
+    vc = torch.empty_like(kc)
+    kc.normal_(0.0, kscale, generator=gen)
+    vc.normal_(0.0, 1.0, generator=gen)
+    q = torch.empty(n_layers * HID, dtype=torch.float16, device="cuda").normal_(generator=gen)
+    out = torch.empty_like(q)
+    ctx = qdiy.Context(num_heads=H, max_seqlen=L)
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+
+    def run(iters, layers):
+        rc = lib.qd_bench_decode_attention(ctx._h, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                           out.data_ptr(), HID, L * HID, layers, L, H, iters,
+                                           variant, splits, sh)
+        if rc != 0:
+            raise RuntimeError(f"bench loop failed: {qdiy.load().qd_last_error().decode()}")
+
+    def timed(iters, layers):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        run(iters, layers)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / iters          # us per call
+
+    run(warmup, n_layers)
+    us_cold = timed(steps, n_layers)
+    run(warmup, 1)
+    us_hot = timed(steps, 1)
+    if not torch.isfinite(out).all():
+        raise RuntimeError("non-finite attention output")
+    plan = ctx.plan(L)
+    ctx.close()
+    del kc, vc
+    torch.cuda.empty_cache()
+    gbps = algo_bytes(L) / (us_cold * 1e-6) / 1e9
+    res = {"L": L, "us_cold": us_cold, "us_hot": us_hot, "gbps": gbps,
+           "gbps_hot": algo_bytes(L) / (us_hot * 1e-6) / 1e9, "frac": gbps / PEAK_GBPS,
+           "layers": n_layers, "plan": f"{plan[0]}x{plan[1]}"}
+    log(f"[bench] L={L}: {us_cold:.2f} us/call cold ({gbps:.0f} GB/s, {100 * gbps / PEAK_GBPS:.1f}% "
+        f"of 8 TB/s), {us_hot:.2f} us hot, plan {res['plan']}, {n_layers} layers rotated")
+    return res
+
+
+def cpu_baseline(L: int, seconds: float):
+    """Times the C oracle (restatement of the reference kernels) on host cores."""
+    import numpy as np
+
+    from oracle import oracle
+
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((H, D), dtype=np.float32).astype(np.float16)
+    kc = (rng.standard_normal(L * HID, dtype=np.float32) * 0.5).astype(np.float16)
+    vc = rng.standard_normal(L * HID, dtype=np.float32).astype(np.float16)
+    try:
+        ncores = len(os.sched_getaffinity(0))
+    except AttributeError:
+        ncores = os.cpu_count() or 1
+    threads = max(1, min(16, ncores))
+
+    def rate(nthreads, budget):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            oracle.decode_attention(q, kc, vc, L, H, HID, D, oracle.ENGINE, nthreads)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return el / n, n
+
+    t1, n1 = rate(1, seconds * 0.4)
+    tn, nn = rate(threads, seconds * 0.6)
+    log(f"[bench] CPU oracle L={L}: {t1 * 1e6:.0f} us/call on 1 thread, {tn * 1e6:.0f} us/call on "
+        f"{threads} threads ({ncores} cores visible)")
+    return {"value": algo_bytes(L) / tn / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{nn} calls at L={L} on {threads} threads + {n1} on 1 thread, "
+                      f"16 heads x 128, fp16 N(0,1) (K x0.5), engine dispatch (split 256-row chunks)",
+            "us_per_call": tn * 1e6, "us_per_call_1thread": t1 * 1e6,
+            "gbps_1thread": algo_bytes(L) / t1 / 1e9, "cores_visible": ncores}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--kv", type=int, nargs="*", default=list(KV_LENS))
+    ap.add_argument("--variant", choices=["auto", "fused", "split"], default="auto")
+    ap.add_argument("--splits", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        return 2
+    if int(os.environ.get("RANK", "0")) != 0:
+        return 0
+
+    import torch
+
+    torch.cuda.set_device(0)
+    lib = bench_lib()
+    variant = {"auto": 0, "fused": 1, "split": 2}[args.variant]
+    kv = sorted(set(args.kv) | {HEADLINE_L})
+    res = {L: measure(lib, L, args.steps, args.warmup, variant, args.splits) for L in kv}
+    head = res[HEADLINE_L]
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
+    cpu = None if args.no_cpu else cpu_baseline(HEADLINE_L, args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(head["gbps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["us_cold"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"decode_attention_L{HEADLINE_L}",
+            "heads": H, "head_dim": D, "kv_len": HEADLINE_L,
+            "io": "fp16 Q/K/V/O, fp32 accumulate",
+            "cache_layout": "[pos][16*128] (reference engine layout)",
+            "cache": "cold: each step reads a different layer; >= 1 GiB rotated",
+            "plan": head["plan"],
+            "us_per_call": {str(L): round(r["us_cold"], 3) for L, r in res.items()},
+            "gbps": {str(L): round(r["gbps"], 1) for L, r in res.items()},
+            "pct_of_peak": {str(L): round(100 * r["frac"], 1) for L, r in res.items()},
+            "us_per_call_hot": {str(L): round(r["us_hot"], 3) for L, r in res.items()},
+        },
+        "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,137 @@
+/*
+ * qdiy/attn.h -- C ABI of the MI355X (gfx950) q=1 decode-attention hot path.
+ *
+ * Drop-in replacement for the decode-attention section of the reference
+ * engine's per-layer step (SeaTheDestiny/LLM-inference-DIY,
+ * framework_src/qwen_infer.cu:629-678):
+ *
+ *   add_bias_kernel<<<24,256>>>(d_qkv, qkv_b, 3H)                  (:631)
+ *   fused_qkv_rope_cache_kernel<<<16,64>>>(d_qkv, Kc_l, Vc_l, pos)   (:634-642)
+ *   for h in 0..15: fd_v5_fused_kernel | fd_v5_split_stage1_kernel +
+ *                   fd_opt_stage2_kernel on head h                   (:646-678)
+ *
+ * becomes two calls per layer:
+ *
+ *   qd_qkv_bias_rope_cache(ctx, d_qkv, qkv_b, Kc_l, Vc_l, pos, ...)
+ *   qd_decode_attention(ctx, d_qkv, Kc_l, Vc_l, d_qkv_out, pos + 1, ...)
+ *
+ * Conventions
+ *   - fp16 buffers are IEEE binary16 bit patterns (uint16_t), device memory.
+ *   - KV cache element (pos, head, d) of one layer lives at
+ *       base + pos*kv_row_stride + head*kv_head_stride + d      (elements)
+ *     The reference engine layout [max_seqlen][num_heads*128] is
+ *     kv_row_stride = num_heads*128, kv_head_stride = 128 (qwen_infer.cu:75-76,
+ *     :636-637, :654-661).
+ *   - q and out are [num_heads][128] contiguous (the Q third of d_qkv and
+ *     d_qkv_out, qwen_infer.cu:659,662).
+ *   - Every call is asynchronous on `stream` and never synchronises the host.
+ *     Launch errors are returned at once; execution errors surface on the
+ *     caller's next synchronisation.
+ *   - Status codes replace the reference's print-and-continue
+ *     (qwen_infer.cu:679-683).  No call ever exits the process.
+ *   - A context owns device scratch (split partials, merge counters, RoPE
+ *     table).  Calls that share a context must be ordered on one stream, the
+ *     way the reference's per-head launches share d_fd_partial on the default
+ *     stream (qwen_infer.cu:672-676).
+ */
+#ifndef QDIY_ATTN_H
+#define QDIY_ATTN_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QD_HEAD_DIM 128
+
+enum qd_status {
+  QD_OK = 0,
+  QD_EINVAL = 1,   /* an argument is out of range, misaligned or NULL */
+  QD_EHIP = 2,     /* a HIP runtime call failed; see qd_last_error() */
+  QD_ENOMEM = 3    /* device or host allocation failed */
+};
+
+typedef struct qd_cfg {
+  int num_heads;            /* heads per layer (16 for Qwen-1.8B)            */
+  int head_dim;             /* must be 128 (qwen_infer.cu:641,649)           */
+  int max_seqlen;           /* cache rows per layer; bounds pos and seqlen   */
+  long long kv_row_stride;  /* elements between positions (num_heads*128)    */
+  long long kv_head_stride; /* elements between heads in a position (128)    */
+  float rope_base;          /* 10000.0f (fused_qkv_rope_cache.cuh:36)        */
+} qd_cfg;
+
+typedef struct qd_ctx qd_ctx;
+
+/* Creates a context on the current HIP device: validates cfg, allocates the
+ * split scratch and builds the [max_seqlen][64] RoPE cos/sin table on the host
+ * (fp32 powf/cosf/sinf, the formula of fused_qkv_rope_cache.cuh:36-38) and
+ * uploads it.  Mirrors the engine-owned d_fd_partial/d_fd_lse allocation
+ * (qwen_infer.cu:264-266).  Synchronous. */
+int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx);
+
+/* Frees everything qd_ctx_create allocated.  NULL is accepted. */
+int qd_ctx_destroy(qd_ctx* ctx);
+
+/* QKV bias + rotate-half RoPE + KV-cache append for one token at `pos`.
+ * Replaces add_bias_kernel (bias.cuh:6-11, call qwen_infer.cu:631) followed by
+ * fused_qkv_rope_cache_kernel (fused_qkv_rope_cache.cuh:6-55, call
+ * qwen_infer.cu:634-642) in one launch, with the same double rounding:
+ *   qkv[j] = half(float(qkv[j]) + float(bias[j]))   for all 3*H*128 j
+ *   Q part of qkv rotated in place; rotated K and biased V written to cache
+ *   row pos of k_layer / v_layer.  The K/V thirds of qkv keep the biased,
+ *   unrotated values, exactly as after the reference's two launches.
+ * bias == NULL skips the add (the caller already added it).
+ * qkv: [3*num_heads*128]; k_layer/v_layer: this layer's cache base.
+ * Requires 0 <= pos < max_seqlen, num_heads/head_dim equal to the cfg's. */
+int qd_qkv_bias_rope_cache(qd_ctx* ctx, uint16_t* qkv, const uint16_t* bias,
+                           uint16_t* k_layer, uint16_t* v_layer, int pos,
+                           int max_seqlen, int num_heads, int head_dim,
+                           hipStream_t stream);
+
+/* q=1 attention of all heads over cache rows [0, seqlen):
+ *   out[h] = half( softmax_j( q[h].K[j,h] / sqrt(128) ) . V[j,h] )
+ * in fp32 with fp16 inputs and output.  Picks the single-workgroup-per-head
+ * (fused) or the split-KV kernel and its split count from seqlen.  Replaces
+ * the 16 per-head launches of qwen_infer.cu:646-678 with one launch.
+ * Requires 1 <= seqlen <= max_seqlen; q, out, k_layer, v_layer 16-byte
+ * aligned; kv strides multiples of 8 elements. */
+int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
+                        const uint16_t* v_layer, uint16_t* out, int seqlen,
+                        int num_heads, int head_dim, hipStream_t stream);
+
+/* Explicit single-workgroup-per-head variant (fd_v5_fused_kernel,
+ * flash_decode_q1_opt.cuh:434-537): one workgroup scans all seqlen rows of a
+ * head and merges its wavefront partials in LDS.  Any seqlen. */
+int qd_decode_attention_fused(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
+                              const uint16_t* v_layer, uint16_t* out, int seqlen,
+                              int num_heads, int head_dim, hipStream_t stream);
+
+/* Explicit split-KV variant (fd_v5_split_stage1_kernel + fd_opt_stage2_kernel,
+ * flash_decode_q1_opt.cuh:548-724): num_splits workgroups per head write fp32
+ * partials; the last workgroup of each head to finish merges them with the
+ * log-sum-exp rule in the same launch.  num_splits <= 0 picks the count;
+ * otherwise 1 <= num_splits <= qd_max_splits(). */
+int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
+                              const uint16_t* v_layer, uint16_t* out, int seqlen,
+                              int num_heads, int head_dim, int num_splits,
+                              hipStream_t stream);
+
+/* Launch plan qd_decode_attention would use for seqlen: *variant is 0 for
+ * fused, 1 for split; *num_splits the split count (1 for fused). */
+int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* num_splits);
+
+/* Largest split count a context supports. */
+int qd_max_splits(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* qd_last_error(void);
+
+/* Library version, e.g. "0.1.0". */
+const char* qd_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QDIY_ATTN_H */

@@ -1,0 +1,64 @@
+"""Builds the gfx950 library llm-inference-diy_amd/lib/libqdiy.so with hipcc.
+
+Usage: python llm-inference-diy_amd/build.py [--verbose]
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
+LIB_DIR = os.path.join(PKG, "lib")
+LIB = os.path.join(LIB_DIR, "libqdiy.so")
+BENCH_LIB = os.path.join(LIB_DIR, "libqdiy_bench.so")
+
+SOURCES = ["qd_capi.cpp", "qd_attention.hip", "qd_rope_cache.hip"]
+ARCH = "gfx950"
+
+# Packed-fp32 VALU forms are disabled for all device code: plain float code is
+# compiled to scalar v_fma/v_mul/v_add only.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if cand and (os.path.sep not in cand or os.path.exists(cand)):
+            return cand
+    raise RuntimeError("hipcc not found")
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature and says so; that is harmless
+    noise = "is not a recognized feature for this target"
+    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln]
+    if res.returncode != 0:
+        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
+    if verbose and msgs:
+        print("\n".join(msgs))
+
+
+def build(verbose: bool = False) -> str:
+    """Builds libqdiy.so (kernels + C ABI) and libqdiy_bench.so (bench loop)."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB + ".tmp"
+    _run([hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
+          "-Wall", "-Wno-unused-result", *DEVICE_FLAGS, "-I", INCLUDE, "-I", CSRC,
+          "-Wl,-soname,libqdiy.so", "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]], verbose)
+    os.replace(tmp, LIB)
+    tmp = BENCH_LIB + ".tmp"
+    _run([hipcc(), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-I", INCLUDE,
+          "-o", tmp, os.path.join(CSRC, "qd_bench.cpp"), "-L", LIB_DIR, "-lqdiy",
+          "-Wl,-rpath,$ORIGIN"], verbose)
+    os.replace(tmp, BENCH_LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="--verbose" in sys.argv))

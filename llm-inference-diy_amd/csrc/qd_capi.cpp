@@ -1,0 +1,270 @@
+// C ABI of the decode-attention hot path: context lifetime, argument checks,
+// launch planning.  Declared in include/qdiy/attn.h.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "qd_internal.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(QD_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Number of workgroups the split planner aims for: four 256-thread
+// workgroups per CU on MI355X's 256 CUs keeps every CU streaming.
+constexpr int kTargetWorkgroups = 1024;
+// Each split scans at least this many rows so the merge stays a small share.
+constexpr int kMinRowsPerSplit = 64;
+// Up to this many rows the fused (one workgroup per head) kernel is used.
+constexpr int kFusedMaxRows = 64;
+
+qd::AttnPlan plan_split(int seqlen, int num_heads, int requested) {
+  int splits = requested;
+  if (splits <= 0) {
+    int target = kTargetWorkgroups / num_heads;
+    if (target < 1) target = 1;
+    int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
+    splits = target < by_rows ? target : by_rows;
+  }
+  if (splits < 1) splits = 1;
+  if (splits > qd::kMaxSplits) splits = qd::kMaxSplits;
+  int rows = (seqlen + splits - 1) / splits;
+  rows = (rows + 3) & ~3;                      // one load instruction covers 4 rows
+  qd::AttnPlan plan;
+  plan.variant = 1;
+  plan.rows_per_split = rows;
+  plan.splits = (seqlen + rows - 1) / rows;    // no empty workgroups
+  plan.rows_per_tile = rows >= 128 ? 8 : (rows >= 64 ? 4 : 2);
+  return plan;
+}
+
+qd::AttnPlan plan_fused(int seqlen) {
+  qd::AttnPlan plan;
+  plan.variant = 0;
+  plan.splits = 1;
+  plan.rows_per_split = seqlen;
+  plan.rows_per_tile = 4;
+  return plan;
+}
+
+int check_attention_args(const qd_ctx* ctx, const uint16_t* q, const uint16_t* k,
+                         const uint16_t* v, const uint16_t* out, int seqlen, int num_heads,
+                         int head_dim) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  if (!q || !k || !v || !out) return fail(QD_EINVAL, "q, k_layer, v_layer and out must be non-NULL");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return fail(QD_EINVAL, "q, k_layer, v_layer and out must be 16-byte aligned");
+  if (head_dim != QD_HEAD_DIM || head_dim != ctx->cfg.head_dim)
+    return fail(QD_EINVAL, "head_dim %d unsupported (must be %d)", head_dim, QD_HEAD_DIM);
+  if (num_heads != ctx->cfg.num_heads)
+    return fail(QD_EINVAL, "num_heads %d differs from the context's %d", num_heads, ctx->cfg.num_heads);
+  if (seqlen < 1 || seqlen > ctx->cfg.max_seqlen)
+    return fail(QD_EINVAL, "seqlen %d outside [1, %d]", seqlen, ctx->cfg.max_seqlen);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
+    return fail(QD_EINVAL, "current device %d is not the context's device %d", dev, ctx->device);
+  return QD_OK;
+}
+
+qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                           uint16_t* out, int seqlen, const qd::AttnPlan& plan) {
+  qd::AttnParams p;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.out = out;
+  p.part_o = ctx->part_o;
+  p.part_ml = ctx->part_ml;
+  p.counters = ctx->counters;
+  p.row_stride = ctx->cfg.kv_row_stride;
+  p.head_stride = ctx->cfg.kv_head_stride;
+  p.seqlen = seqlen;
+  p.num_heads = ctx->cfg.num_heads;
+  p.splits = plan.splits;
+  p.rows_per_split = plan.rows_per_split;
+  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));  // log2(e)/sqrt(128)
+  return p;
+}
+
+int run_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                  uint16_t* out, int seqlen, const qd::AttnPlan& plan, hipStream_t stream) {
+  const qd::AttnParams p = make_params(ctx, q, k, v, out, seqlen, plan);
+  hipError_t e = qd::launch_decode_attention(p, plan, stream);
+  if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+  return QD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
+  if (!out_ctx) return fail(QD_EINVAL, "out_ctx is NULL");
+  *out_ctx = nullptr;
+  if (!cfg) return fail(QD_EINVAL, "cfg is NULL");
+  if (cfg->head_dim != QD_HEAD_DIM) return fail(QD_EINVAL, "head_dim must be %d", QD_HEAD_DIM);
+  if (cfg->num_heads < 1 || cfg->num_heads > 4096) return fail(QD_EINVAL, "num_heads out of range");
+  if (cfg->max_seqlen < 1) return fail(QD_EINVAL, "max_seqlen must be >= 1");
+  if (cfg->kv_row_stride < 1 || cfg->kv_head_stride < 1 || (cfg->kv_row_stride % 8) ||
+      (cfg->kv_head_stride % 8))
+    return fail(QD_EINVAL, "kv strides must be positive multiples of 8 elements");
+  if (!(cfg->rope_base > 0.0f)) return fail(QD_EINVAL, "rope_base must be > 0");
+
+  qd_ctx* ctx = new (std::nothrow) qd_ctx;
+  if (!ctx) return fail(QD_ENOMEM, "host allocation failed");
+  std::memset(ctx, 0, sizeof(*ctx));
+  ctx->cfg = *cfg;
+  hipError_t e = hipGetDevice(&ctx->device);
+  if (e != hipSuccess) {
+    delete ctx;
+    return hip_fail(e, "hipGetDevice");
+  }
+  const size_t H = (size_t)cfg->num_heads;
+  const size_t S = (size_t)cfg->max_seqlen;
+  auto cleanup = [&](int code) {
+    qd_ctx_destroy(ctx);
+    return code;
+  };
+  if ((e = hipMalloc(&ctx->part_o, H * qd::kMaxSplits * 128 * sizeof(float))) != hipSuccess ||
+      (e = hipMalloc(&ctx->part_ml, H * qd::kMaxSplits * sizeof(float2))) != hipSuccess ||
+      (e = hipMalloc(&ctx->counters, H * sizeof(unsigned))) != hipSuccess ||
+      (e = hipMalloc(&ctx->rope_cs, S * 64 * sizeof(float2))) != hipSuccess) {
+    int code = hip_fail(e, "hipMalloc of context scratch");
+    return cleanup(code == QD_EHIP ? QD_ENOMEM : code);
+  }
+  if ((e = hipMemset(ctx->counters, 0, H * sizeof(unsigned))) != hipSuccess)
+    return cleanup(hip_fail(e, "hipMemset of split counters"));
+
+  // RoPE table: theta = float(pos) * powf(base, (-2*i)/head_dim), then fp32
+  // cosf/sinf (fused_qkv_rope_cache.cuh:36-38), evaluated once per context.
+  std::vector<float2> cs;
+  try {
+    cs.resize(S * 64);
+  } catch (...) {
+    return cleanup(fail(QD_ENOMEM, "host allocation of the RoPE table failed"));
+  }
+  float inv_freq[64];
+  for (int i = 0; i < 64; ++i)
+    inv_freq[i] = powf(cfg->rope_base, (-2.0f * (float)i) / (float)cfg->head_dim);
+  for (size_t pos = 0; pos < S; ++pos) {
+    for (int i = 0; i < 64; ++i) {
+      const float theta = (float)pos * inv_freq[i];
+      cs[pos * 64 + i] = float2{cosf(theta), sinf(theta)};
+    }
+  }
+  if ((e = hipMemcpy(ctx->rope_cs, cs.data(), S * 64 * sizeof(float2), hipMemcpyHostToDevice)) !=
+      hipSuccess)
+    return cleanup(hip_fail(e, "hipMemcpy of the RoPE table"));
+  *out_ctx = ctx;
+  return QD_OK;
+}
+
+int qd_ctx_destroy(qd_ctx* ctx) {
+  if (!ctx) return QD_OK;
+  int dev = -1;
+  const bool switch_dev = hipGetDevice(&dev) == hipSuccess && dev != ctx->device;
+  if (switch_dev) (void)hipSetDevice(ctx->device);
+  if (ctx->part_o) (void)hipFree(ctx->part_o);
+  if (ctx->part_ml) (void)hipFree(ctx->part_ml);
+  if (ctx->counters) (void)hipFree(ctx->counters);
+  if (ctx->rope_cs) (void)hipFree(ctx->rope_cs);
+  if (switch_dev) (void)hipSetDevice(dev);
+  delete ctx;
+  return QD_OK;
+}
+
+int qd_qkv_bias_rope_cache(qd_ctx* ctx, uint16_t* qkv, const uint16_t* bias, uint16_t* k_layer,
+                           uint16_t* v_layer, int pos, int max_seqlen, int num_heads,
+                           int head_dim, hipStream_t stream) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  if (!qkv || !k_layer || !v_layer) return fail(QD_EINVAL, "qkv, k_layer and v_layer must be non-NULL");
+  if (((uintptr_t)qkv | (uintptr_t)k_layer | (uintptr_t)v_layer | (uintptr_t)bias) & 1u)
+    return fail(QD_EINVAL, "fp16 buffers must be 2-byte aligned");
+  if (head_dim != QD_HEAD_DIM) return fail(QD_EINVAL, "head_dim %d unsupported (must be 128)", head_dim);
+  if (num_heads != ctx->cfg.num_heads)
+    return fail(QD_EINVAL, "num_heads %d differs from the context's %d", num_heads, ctx->cfg.num_heads);
+  if (max_seqlen < 1 || max_seqlen > ctx->cfg.max_seqlen)
+    return fail(QD_EINVAL, "max_seqlen %d outside [1, %d]", max_seqlen, ctx->cfg.max_seqlen);
+  if (pos < 0 || pos >= max_seqlen) return fail(QD_EINVAL, "pos %d outside [0, %d)", pos, max_seqlen);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
+    return fail(QD_EINVAL, "current device %d is not the context's device %d", dev, ctx->device);
+  qd::RopeParams p;
+  p.qkv = qkv;
+  p.bias = bias;
+  p.k_layer = k_layer;
+  p.v_layer = v_layer;
+  p.rope_cs = ctx->rope_cs;
+  p.row_stride = ctx->cfg.kv_row_stride;
+  p.head_stride = ctx->cfg.kv_head_stride;
+  p.pos = pos;
+  p.num_heads = num_heads;
+  hipError_t e = qd::launch_qkv_bias_rope_cache(p, stream);
+  if (e != hipSuccess) return hip_fail(e, "qkv_bias_rope_cache launch");
+  return QD_OK;
+}
+
+int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* num_splits) {
+  if (!ctx || !variant || !num_splits) return fail(QD_EINVAL, "NULL argument");
+  if (seqlen < 1 || seqlen > ctx->cfg.max_seqlen)
+    return fail(QD_EINVAL, "seqlen %d outside [1, %d]", seqlen, ctx->cfg.max_seqlen);
+  const qd::AttnPlan plan =
+      seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(seqlen, ctx->cfg.num_heads, 0);
+  *variant = plan.variant;
+  *num_splits = plan.splits;
+  return QD_OK;
+}
+
+int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
+                        const uint16_t* v_layer, uint16_t* out, int seqlen, int num_heads,
+                        int head_dim, hipStream_t stream) {
+  int rc = check_attention_args(ctx, q, k_layer, v_layer, out, seqlen, num_heads, head_dim);
+  if (rc != QD_OK) return rc;
+  const qd::AttnPlan plan =
+      seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(seqlen, num_heads, 0);
+  return run_attention(ctx, q, k_layer, v_layer, out, seqlen, plan, stream);
+}
+
+int qd_decode_attention_fused(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
+                              const uint16_t* v_layer, uint16_t* out, int seqlen, int num_heads,
+                              int head_dim, hipStream_t stream) {
+  int rc = check_attention_args(ctx, q, k_layer, v_layer, out, seqlen, num_heads, head_dim);
+  if (rc != QD_OK) return rc;
+  return run_attention(ctx, q, k_layer, v_layer, out, seqlen, plan_fused(seqlen), stream);
+}
+
+int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
+                              const uint16_t* v_layer, uint16_t* out, int seqlen, int num_heads,
+                              int head_dim, int num_splits, hipStream_t stream) {
+  int rc = check_attention_args(ctx, q, k_layer, v_layer, out, seqlen, num_heads, head_dim);
+  if (rc != QD_OK) return rc;
+  if (num_splits > qd::kMaxSplits)
+    return fail(QD_EINVAL, "num_splits %d above the maximum %d", num_splits, qd::kMaxSplits);
+  return run_attention(ctx, q, k_layer, v_layer, out, seqlen,
+                       plan_split(seqlen, num_heads, num_splits), stream);
+}
+
+int qd_max_splits(void) { return qd::kMaxSplits; }
+
+const char* qd_last_error(void) { return g_err; }
+
+const char* qd_version(void) { return "0.1.0"; }
+
+}  // extern "C"

@@ -1,0 +1,188 @@
+"""Python binding of libqdiy.so, the C ABI declared in include/qdiy/attn.h.
+
+Device memory and streams come from PyTorch (ROCm); every call goes straight to
+the HIP kernels through ctypes.  There is no fallback: if the library is not
+built, or a call fails, an exception is raised.
+
+torch is imported before the library is loaded so that the library binds to
+the HIP runtime torch already has in the process (both carry the SONAME
+libamdhip64.so.7): torch's streams and device pointers are then valid
+arguments.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "lib", "libqdiy.so")
+HEAD_DIM = 128
+
+QD_OK, QD_EINVAL, QD_EHIP, QD_ENOMEM = 0, 1, 2, 3
+FUSED, SPLIT = 0, 1
+
+EXPORTS = (
+    "qd_ctx_create", "qd_ctx_destroy", "qd_qkv_bias_rope_cache", "qd_decode_attention",
+    "qd_decode_attention_fused", "qd_decode_attention_split", "qd_decode_attention_plan",
+    "qd_max_splits", "qd_last_error", "qd_version",
+)
+
+
+class QdError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"qdiy status {code}: {msg}")
+        self.code = code
+
+
+class Cfg(ctypes.Structure):
+    _fields_ = [("num_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+                ("max_seqlen", ctypes.c_int), ("kv_row_stride", ctypes.c_longlong),
+                ("kv_head_stride", ctypes.c_longlong), ("rope_base", ctypes.c_float)]
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads libqdiy.so (raises if it is not built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run python llm-inference-diy_amd/build.py")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, i, ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
+    L.qd_ctx_create.argtypes = [ctypes.POINTER(Cfg), ctypes.POINTER(vp)]
+    L.qd_ctx_destroy.argtypes = [vp]
+    L.qd_qkv_bias_rope_cache.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
+    L.qd_decode_attention.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
+    L.qd_decode_attention_fused.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
+    L.qd_decode_attention_split.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
+    L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
+    L.qd_last_error.restype = ctypes.c_char_p
+    L.qd_version.restype = ctypes.c_char_p
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != QD_OK:
+        raise QdError(rc, load().qd_last_error().decode())
+
+
+def _stream(stream) -> ctypes.c_void_p:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    if isinstance(stream, torch.cuda.Stream):
+        stream = stream.cuda_stream
+    return ctypes.c_void_p(int(stream))
+
+
+def _ptr(t: torch.Tensor, name: str, contiguous: bool = True) -> ctypes.c_void_p:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.dtype != torch.float16:
+        raise TypeError(f"{name} must be float16, got {t.dtype}")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if contiguous and not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class Context:
+    """Owns a qd_ctx (split scratch, merge counters, RoPE table) on the current device."""
+
+    def __init__(self, num_heads: int = 16, max_seqlen: int = 2048, kv_row_stride: int | None = None,
+                 kv_head_stride: int = HEAD_DIM, rope_base: float = 10000.0,
+                 head_dim: int = HEAD_DIM):
+        L = load()
+        self.num_heads = num_heads
+        self.max_seqlen = max_seqlen
+        self.kv_row_stride = num_heads * HEAD_DIM if kv_row_stride is None else kv_row_stride
+        self.kv_head_stride = kv_head_stride
+        cfg = Cfg(num_heads, head_dim, max_seqlen, self.kv_row_stride, kv_head_stride, rope_base)
+        h = ctypes.c_void_p()
+        _check(L.qd_ctx_create(ctypes.byref(cfg), ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().qd_ctx_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # -- host-side extent checks (the C ABI takes raw pointers) ---------------
+    def _check_cache(self, t: torch.Tensor, name: str, rows: int) -> None:
+        last = (rows - 1) * self.kv_row_stride + (self.num_heads - 1) * self.kv_head_stride + HEAD_DIM
+        if t.storage_offset() + last > t.untyped_storage().nbytes() // 2 or t.numel() < last:
+            raise ValueError(f"{name} holds {t.numel()} elements; {rows} rows need {last}")
+
+    def plan(self, seqlen: int):
+        v, s = ctypes.c_int(), ctypes.c_int()
+        _check(load().qd_decode_attention_plan(self._h, seqlen, ctypes.byref(v), ctypes.byref(s)))
+        return ("fused" if v.value == FUSED else "split"), s.value
+
+    def decode_attention(self, q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                         out: torch.Tensor, seqlen: int, variant: str = "auto", num_splits: int = 0,
+                         stream=None) -> torch.Tensor:
+        """out[h] = softmax(q[h] K[:seqlen,h]^T / sqrt(128)) V[:seqlen,h] for all heads."""
+        H = self.num_heads
+        if q.numel() < H * HEAD_DIM or out.numel() < H * HEAD_DIM:
+            raise ValueError("q and out need num_heads*128 elements")
+        if seqlen >= 1:
+            self._check_cache(k_layer, "k_layer", seqlen)
+            self._check_cache(v_layer, "v_layer", seqlen)
+        args = (self._h, _ptr(q, "q"), _ptr(k_layer, "k_layer", False), _ptr(v_layer, "v_layer", False),
+                _ptr(out, "out"), seqlen, H, HEAD_DIM)
+        L = load()
+        if variant == "auto":
+            _check(L.qd_decode_attention(*args, _stream(stream)))
+        elif variant == "fused":
+            _check(L.qd_decode_attention_fused(*args, _stream(stream)))
+        elif variant == "split":
+            _check(L.qd_decode_attention_split(*args, num_splits, _stream(stream)))
+        else:
+            raise ValueError(f"unknown variant {variant!r}")
+        return out
+
+    def qkv_bias_rope_cache(self, qkv: torch.Tensor, bias, k_layer: torch.Tensor,
+                            v_layer: torch.Tensor, pos: int, max_seqlen: int | None = None,
+                            stream=None) -> None:
+        """Bias + RoPE on qkv[3*H*128] in place; rotated K / biased V into cache row pos."""
+        H = self.num_heads
+        if qkv.numel() < 3 * H * HEAD_DIM:
+            raise ValueError("qkv needs 3*num_heads*128 elements")
+        if bias is not None and bias.numel() < 3 * H * HEAD_DIM:
+            raise ValueError("bias needs 3*num_heads*128 elements")
+        if max_seqlen is None:
+            max_seqlen = self.max_seqlen
+        if 0 <= pos < max_seqlen:
+            self._check_cache(k_layer, "k_layer", pos + 1)
+            self._check_cache(v_layer, "v_layer", pos + 1)
+        bptr = None if bias is None else _ptr(bias, "bias")
+        _check(load().qd_qkv_bias_rope_cache(self._h, _ptr(qkv, "qkv"), bptr,
+                                             _ptr(k_layer, "k_layer", False),
+                                             _ptr(v_layer, "v_layer", False), pos, max_seqlen, H,
+                                             HEAD_DIM, _stream(stream)))
+
+
+def version() -> str:
+    return load().qd_version().decode()
+
+
+def max_splits() -> int:
+    return load().qd_max_splits()

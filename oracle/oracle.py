@@ -1,0 +1,133 @@
+"""ctypes wrapper of the CPU oracle (oracle/libqd_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, never by the product package.  fp16 arrays are
+numpy float16 (their uint16 bit patterns cross the C boundary unchanged).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqd_oracle.so")
+
+ENGINE, FUSED, SPLIT = 0, 1, 2
+
+_lib = None
+
+
+def build() -> None:
+    """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
+    subprocess.run(["make", "-s", "-B", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        u16p = ctypes.POINTER(ctypes.c_uint16)
+        f32p = ctypes.POINTER(ctypes.c_float)
+        ll = ctypes.c_longlong
+        L.qd_oracle_h2f_array.argtypes = [u16p, f32p, ll]
+        L.qd_oracle_f2h_array.argtypes = [f32p, u16p, ll]
+        L.qd_oracle_fd_fused_head.argtypes = [u16p, u16p, u16p, u16p, ctypes.c_int, ll,
+                                              ctypes.c_int, ctypes.c_int]
+        L.qd_oracle_fd_split_head.argtypes = [u16p, u16p, u16p, u16p, ctypes.c_int, ll,
+                                              ctypes.c_int, ctypes.c_int, u16p, f32p]
+        L.qd_oracle_decode_attention.argtypes = [u16p, u16p, u16p, u16p, ctypes.c_int,
+                                                 ctypes.c_int, ll, ll, ctypes.c_int,
+                                                 ctypes.c_int]
+        L.qd_oracle_decode_attention.restype = ctypes.c_int
+        L.qd_oracle_qkv_bias_rope_cache.argtypes = [u16p, u16p, u16p, u16p, ctypes.c_int,
+                                                    ctypes.c_int, ctypes.c_int, ll, ll,
+                                                    ctypes.c_float]
+        L.qd_oracle_qkv_bias_rope_cache.restype = ctypes.c_int
+        L.qd_oracle_rope_cos_sin.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             ctypes.c_float, f32p, f32p]
+        _lib = L
+    return _lib
+
+
+def _u16(a: np.ndarray):
+    assert a.dtype == np.float16 and a.flags.c_contiguous
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))
+
+
+def _f32(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def h2f(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.float16)
+    out = np.empty(h.shape, np.float32)
+    lib().qd_oracle_h2f_array(_u16(h), _f32(out), h.size)
+    return out
+
+
+def f2h(f: np.ndarray) -> np.ndarray:
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.float16)
+    lib().qd_oracle_f2h_array(_f32(f), _u16(out), f.size)
+    return out
+
+
+def fd_fused_head(q, k, v, seqlen, row_stride, rows_per_warp=32, num_warps=None):
+    """One head of fd_v5_fused_kernel; k/v are flat fp16 arrays."""
+    if num_warps is None:
+        num_warps = min(32, (seqlen + rows_per_warp - 1) // rows_per_warp)
+    out = np.zeros(128, np.float16)
+    lib().qd_oracle_fd_fused_head(_u16(q), _u16(k), _u16(v), _u16(out), seqlen, row_stride,
+                                  rows_per_warp, num_warps)
+    return out
+
+
+def fd_split_head(q, k, v, seqlen, row_stride, chunk=256, warps=8):
+    """One head of split stage 1 + stage 2; returns (out, partial, lse)."""
+    n = (seqlen + chunk - 1) // chunk
+    out = np.zeros(128, np.float16)
+    part = np.zeros((n, 128), np.float16)
+    lse = np.zeros(n, np.float32)
+    lib().qd_oracle_fd_split_head(_u16(q), _u16(k), _u16(v), _u16(out), seqlen, row_stride,
+                                  chunk, warps, _u16(part), _f32(lse))
+    return out, part, lse
+
+
+def decode_attention(q, k, v, seqlen, num_heads, row_stride, head_stride,
+                     variant=ENGINE, nthreads=1):
+    """All heads: q [H,128] fp16, k/v flat fp16 caches; returns out [H,128]."""
+    q = np.ascontiguousarray(q, dtype=np.float16)
+    out = np.zeros((num_heads, 128), np.float16)
+    rc = lib().qd_oracle_decode_attention(_u16(q), _u16(k), _u16(v), _u16(out), seqlen,
+                                          num_heads, row_stride, head_stride, variant,
+                                          nthreads)
+    if rc != 0:
+        raise ValueError("qd_oracle_decode_attention rejected its arguments")
+    return out
+
+
+def qkv_bias_rope_cache(qkv, bias, k_cache, v_cache, pos, num_heads, head_dim=128,
+                        row_stride=None, head_stride=None, rope_base=10000.0):
+    """In place on qkv / k_cache / v_cache (numpy fp16, flat)."""
+    if row_stride is None:
+        row_stride = num_heads * head_dim
+    if head_stride is None:
+        head_stride = head_dim
+    rc = lib().qd_oracle_qkv_bias_rope_cache(_u16(qkv), None if bias is None else _u16(bias),
+                                             _u16(k_cache), _u16(v_cache), pos, num_heads,
+                                             head_dim, row_stride, head_stride, rope_base)
+    if rc != 0:
+        raise ValueError("qd_oracle_qkv_bias_rope_cache rejected its arguments")
+
+
+def rope_cos_sin(pos, i, head_dim=128, rope_base=10000.0):
+    c = ctypes.c_float()
+    s = ctypes.c_float()
+    lib().qd_oracle_rope_cos_sin(pos, i, head_dim, rope_base, ctypes.byref(c), ctypes.byref(s))
+    return np.float32(c.value), np.float32(s.value)

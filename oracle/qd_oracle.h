@@ -1,0 +1,89 @@
+/*
+ * qd_oracle.h -- CPU restatement of the reference's decode-attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links or calls this
+ * code; it is the checker used by tests/, by __graft_entry__.smoke() and by the
+ * cpu_baseline leg of bench.py.
+ *
+ * Every function restates, in plain C with IEEE fp32 arithmetic and no FP
+ * contraction (built with -ffp-contract=off), the exact operation order of the
+ * reference CUDA kernel it cites.  fp16 values travel as raw IEEE binary16 bit
+ * patterns (uint16_t).
+ *
+ * Reference files (SeaTheDestiny/LLM-inference-DIY):
+ *   kernels/flash_decode_q1_opt.cuh:434-537  fd_v5_fused_kernel
+ *   kernels/flash_decode_q1_opt.cuh:548-656  fd_v5_split_stage1_kernel
+ *   kernels/flash_decode_q1_opt.cuh:666-724  fd_opt_stage2_kernel
+ *   framework_src/qwen_infer.cu:644-678      per-layer fused/split dispatch
+ *   kernels/fused_qkv_rope_cache.cuh:6-55    fused_qkv_rope_cache_kernel
+ *   kernels/bias.cuh:6-11                    add_bias_kernel (QKV bias use)
+ *
+ * Deviations that no run of the reference here can pin (documented, not gaps):
+ *   - the reference builds with --use_fast_math (__expf/__logf/__sinf...); the
+ *     oracle calls glibc expf/logf/powf/cosf/sinf;
+ *   - where the reference source writes `a*b + c` without __fmaf_rn, nvcc may
+ *     contract it; the oracle rounds the product and the sum separately.
+ */
+#ifndef QD_ORACLE_H
+#define QD_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* IEEE binary16 <-> binary32 (round-to-nearest-even), as cuda_fp16's
+ * __half2float / __float2half. */
+float qd_oracle_h2f(uint16_t h);
+uint16_t qd_oracle_f2h(float f);
+void qd_oracle_h2f_array(const uint16_t* in, float* out, long long n);
+void qd_oracle_f2h_array(const float* in, uint16_t* out, long long n);
+
+/* Variants of the decode-attention restatement. */
+enum {
+  QD_ORACLE_ENGINE = 0, /* qwen_infer.cu:646-678: C=ceil(L/256); fused<128,8,32> if C==1 else split */
+  QD_ORACLE_FUSED = 1,  /* fd_v5_fused_kernel<128,32,32>, min(32,ceil(L/32)) warps (bench_fd_opt.cu:303-317); L <= 1024 */
+  QD_ORACLE_SPLIT = 2   /* fd_v5_split_stage1_kernel<128,256,8> + fd_opt_stage2_kernel<128>, any L >= 1 */
+};
+
+/* One head of fd_v5_fused_kernel<128, *, rows_per_warp> launched with
+ * num_warps warps.  q[128]; K/V row r at k + r*row_stride.  Rows beyond
+ * num_warps*rows_per_warp are not visited (as in the reference). */
+void qd_oracle_fd_fused_head(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             uint16_t* out, int seqlen, long long row_stride,
+                             int rows_per_warp, int num_warps);
+
+/* One head of the split path: stage 1 over ceil(L/chunk) chunks of `chunk`
+ * rows with `warps` warps each, then stage 2.  partial (ceil(L/chunk)*128 fp16)
+ * and lse (ceil(L/chunk) floats) receive the stage-1 intermediates when non-NULL. */
+void qd_oracle_fd_split_head(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                             uint16_t* out, int seqlen, long long row_stride,
+                             int chunk, int warps, uint16_t* partial, float* lse);
+
+/* All heads.  q/out are [H][128] contiguous.  Head h's K/V rows live at
+ * k + h*head_stride + r*row_stride (elements).  nthreads >= 1 worker threads
+ * split the (head, chunk) tasks.  Returns 0, or -1 on invalid arguments. */
+int qd_oracle_decode_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               uint16_t* out, int seqlen, int num_heads,
+                               long long row_stride, long long head_stride,
+                               int variant, int nthreads);
+
+/* add_bias_kernel on qkv[3*H*D] (when bias != NULL) followed by
+ * fused_qkv_rope_cache_kernel at position pos: Q rotated in place, rotated K and
+ * raw V written to cache row pos at k_cache/v_cache + pos*row_stride +
+ * h*head_stride + d.  Returns 0, or -1 on invalid arguments. */
+int qd_oracle_qkv_bias_rope_cache(uint16_t* qkv, const uint16_t* bias,
+                                  uint16_t* k_cache, uint16_t* v_cache, int pos,
+                                  int num_heads, int head_dim,
+                                  long long row_stride, long long head_stride,
+                                  float rope_base);
+
+/* cos/sin of fused_qkv_rope_cache.cuh:36-38 for one (pos, i). */
+void qd_oracle_rope_cos_sin(int pos, int i, int head_dim, float rope_base,
+                            float* cos_out, float* sin_out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QD_ORACLE_H */

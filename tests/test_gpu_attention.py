@@ -1,0 +1,198 @@
+"""GPU parity of decode attention (C ABI -> HIP kernels) against the CPU oracle.
+
+Bars: max abs error <= 2e-3 against the oracle's restatement of the
+reference kernels (flash_decode_q1_opt.cuh), and -- stronger -- within half a
+binary16 ulp (+1e-5) of float64 attention, since the kernels keep every
+intermediate in fp32 and round once.  Closed forms (L=1, constant inputs) are
+bit-exact.  Configs 1-3 of the benchmark run at full size.
+"""
+import numpy as np
+import pytest
+import torch
+
+from common import AttnCase, ulp16
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3          # north-star tolerance on fp16 attention outputs
+TAIL = 64            # sentinel elements after `out` that must stay untouched
+
+
+@pytest.fixture(scope="module")
+def qdiy():
+    import qdiy as m
+    torch.cuda.set_device(0)
+    m.load()
+    return m
+
+
+class GpuCase:
+    def __init__(self, qdiy, case: AttnCase):
+        self.case = case
+        self.ctx = qdiy.Context(num_heads=case.H, max_seqlen=case.max_seqlen,
+                                kv_row_stride=case.row_stride, kv_head_stride=case.head_stride)
+        self.q = torch.from_numpy(case.q.reshape(-1)).cuda()
+        self.kc = torch.from_numpy(case.kc).cuda()
+        self.vc = torch.from_numpy(case.vc).cuda()
+
+    def run(self, seqlen=None, variant="auto", num_splits=0):
+        H = self.case.H
+        out = torch.full((H * 128 + TAIL,), 7.0, dtype=torch.float16, device="cuda")
+        self.ctx.decode_attention(self.q, self.kc, self.vc, out, seqlen or self.case.L, variant,
+                                  num_splits)
+        torch.cuda.synchronize()
+        o = out.cpu().numpy()
+        assert np.all(o[H * 128:] == np.float16(7.0)), "write past the end of out"
+        return o[:H * 128].reshape(H, 128)
+
+    def close(self):
+        self.ctx.close()
+
+
+def _oracle(case, variant=oracle.ENGINE, seqlen=None):
+    return oracle.decode_attention(case.q, case.kc, case.vc, seqlen or case.L, case.H,
+                                   case.row_stride, case.head_stride, variant, nthreads=8)
+
+
+def _check(got, case, want_oracle, fp64=None):
+    g = got.astype(np.float64)
+    err = np.max(np.abs(g - want_oracle.astype(np.float64)))
+    assert err <= ATOL, f"max abs err vs oracle {err}"
+    ref = case.fp64() if fp64 is None else fp64
+    bad = np.abs(g - ref) > 0.5 * ulp16(ref) + 1e-5
+    assert not bad.any(), f"{bad.sum()} outputs off float64 by > 0.5 ulp, max {np.max(np.abs(g - ref))}"
+    return err
+
+
+def test_config1_fused_L512(qdiy):
+    case = AttnCase(512, H=16, seed=1)
+    g = GpuCase(qdiy, case)
+    _check(g.run(variant="fused"), case, _oracle(case, oracle.FUSED))
+    _check(g.run(variant="auto"), case, _oracle(case, oracle.FUSED))
+    g.close()
+
+
+def test_config2_split_L8192(qdiy):
+    case = AttnCase(8192, H=16, seed=2, kscale=0.5)
+    g = GpuCase(qdiy, case)
+    want = _oracle(case)
+    _check(g.run(), case, want)
+    for n in (1, 16, 64, 256):
+        _check(g.run(variant="split", num_splits=n), case, want)
+    g.close()
+
+
+@pytest.mark.parametrize("spike", [0, 100])
+def test_config3_long_context_L32768(qdiy, spike):
+    case = AttnCase(32768, H=16, seed=3, spike_every=spike)
+    g = GpuCase(qdiy, case)
+    _check(g.run(), case, _oracle(case))
+    g.close()
+
+
+EDGE_L = [1, 2, 3, 4, 5, 8, 15, 16, 17, 31, 32, 33, 63, 64, 65, 100, 127, 128, 129, 255, 256,
+          257, 511, 513, 1000, 2047, 4097]
+
+
+@pytest.mark.parametrize("L", EDGE_L)
+def test_edge_lengths_all_variants(qdiy, L):
+    case = AttnCase(L, H=4, seed=1000 + L, max_seqlen=L + 37)
+    g = GpuCase(qdiy, case)
+    want = _oracle(case)
+    ref = case.fp64()
+    _check(g.run(variant="auto"), case, want, ref)
+    _check(g.run(variant="fused"), case, want, ref)
+    for n in sorted({1, 2, 3, 7, 64, 256}):
+        if n <= L:
+            _check(g.run(variant="split", num_splits=n), case, want, ref)
+    g.close()
+
+
+@pytest.mark.parametrize("layout", ["engine", "head_major"])
+def test_rows_beyond_seqlen_are_not_read(qdiy, layout):
+    case = AttnCase(3000, H=16, seed=5, layout=layout, max_seqlen=3300)
+    S = case.max_seqlen
+    kc = case.kc.copy()
+    if layout == "engine":
+        kc.reshape(S, 16, 128)[3000:] = np.float16(60.0)     # would dominate any softmax
+    else:
+        kc.reshape(16, S, 128)[:, 3000:] = np.float16(60.0)
+    case.kc = kc
+    g = GpuCase(qdiy, case)
+    _check(g.run(), case, _oracle(case))
+    _check(g.run(variant="fused"), case, _oracle(case))
+    g.close()
+
+
+def test_single_row_is_v0_bit_exact(qdiy):
+    case = AttnCase(1, H=16, seed=6, max_seqlen=16)
+    g = GpuCase(qdiy, case)
+    for variant in ("auto", "fused", "split"):
+        assert np.array_equal(g.run(variant=variant).view(np.uint16), case.Vh[:, 0].view(np.uint16))
+    g.close()
+
+
+@pytest.mark.parametrize("L", [256, 512, 8192, 32768])
+def test_bench_constant_inputs_bit_exact(qdiy, L):
+    fill = np.array([0x3C3C], np.uint16).view(np.float16)[0]   # bench_fd_opt.cu:134-136
+    case = AttnCase(L, H=16, fill=fill)
+    g = GpuCase(qdiy, case)
+    for variant in ("auto", "fused", "split"):
+        assert np.all(g.run(variant=variant).view(np.uint16) == 0x3C3C), variant
+    g.close()
+
+
+def test_repeat_calls_are_deterministic_and_counters_reset(qdiy):
+    case = AttnCase(5000, H=16, seed=7)
+    g = GpuCase(qdiy, case)
+    a = g.run(variant="split", num_splits=40)
+    b = g.run(variant="split", num_splits=13)      # different grid, same context
+    c = g.run(variant="split", num_splits=40)
+    assert np.array_equal(a.view(np.uint16), c.view(np.uint16))
+    assert np.max(np.abs(a.astype(np.float32) - b.astype(np.float32))) <= ATOL
+    for _ in range(3):
+        assert np.array_equal(g.run().view(np.uint16), g.run().view(np.uint16))
+    g.close()
+
+
+def test_inputs_are_not_modified(qdiy):
+    case = AttnCase(777, H=16, seed=8)
+    g = GpuCase(qdiy, case)
+    g.run()
+    g.run(variant="fused")
+    assert np.array_equal(g.kc.cpu().numpy().view(np.uint16), case.kc.view(np.uint16))
+    assert np.array_equal(g.vc.cpu().numpy().view(np.uint16), case.vc.view(np.uint16))
+    assert np.array_equal(g.q.cpu().numpy().view(np.uint16), case.q.reshape(-1).view(np.uint16))
+    g.close()
+
+
+def test_head_independence(qdiy):
+    case = AttnCase(1500, H=16, seed=9)
+    g = GpuCase(qdiy, case)
+    a = g.run()
+    kc = g.kc.view(1500, 16, 128)
+    kc[:, 5] = -kc[:, 5]
+    b = g.run()
+    keep = [h for h in range(16) if h != 5]
+    assert np.array_equal(a[keep].view(np.uint16), b[keep].view(np.uint16))
+    assert not np.array_equal(a[5], b[5])
+    g.close()
+
+
+def test_invalid_arguments_raise(qdiy):
+    case = AttnCase(64, H=16, seed=10)
+    g = GpuCase(qdiy, case)
+    out = torch.empty(16 * 128 + 8, dtype=torch.float16, device="cuda")
+    with pytest.raises(qdiy.QdError) as e:
+        g.ctx.decode_attention(g.q, g.kc, g.vc, out, 0)
+    assert e.value.code == qdiy.QD_EINVAL
+    with pytest.raises(qdiy.QdError):
+        g.ctx.decode_attention(g.q, g.kc, g.vc, out, 65)              # > max_seqlen
+    with pytest.raises(qdiy.QdError):
+        g.ctx.decode_attention(g.q, g.kc, g.vc, out[1:], 10)          # misaligned out
+    with pytest.raises(qdiy.QdError):
+        g.ctx.decode_attention(g.q, g.kc, g.vc, out, 10, "split", qdiy.max_splits() + 1)
+    with pytest.raises(ValueError):
+        g.ctx.decode_attention(g.q, g.kc[:1000], g.vc, out, 64)       # cache too small (host check)
+    g.close()
