@@ -166,6 +166,8 @@ def main() -> int:
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="run one 256 MiB device copy (known FETCH_SIZE/WRITE_SIZE) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -177,11 +179,26 @@ def main() -> int:
     import torch
 
     torch.cuda.set_device(0)
+    if args.pmc_calibration:
+        # Counter calibration: a copy of exactly 256 MiB reads and writes 256 MiB of
+        # HBM.  A third buffer is streamed first so the source is not cache-resident.
+        n = (256 << 20) // 2
+        a = torch.zeros(n, dtype=torch.float16, device="cuda")
+        b = torch.zeros_like(a)
+        c = torch.zeros_like(a)
+        c.add_(1.0)
+        torch.cuda.synchronize()
+        b.copy_(a)
+        torch.cuda.synchronize()
+        log("[bench] pmc calibration: copied 268435456 bytes")
+        return 0
     lib = bench_lib()
     variant = {"auto": 0, "fused": 1, "split": 2}[args.variant]
     kv = sorted(set(args.kv) | {HEADLINE_L})
     res = {L: measure(lib, L, args.steps, args.warmup, variant, args.splits) for L in kv}
     head = res[HEADLINE_L]
+    # config 1 names the fused single-workgroup-per-head path at L=512
+    fused512 = measure(lib, 512, args.steps, args.warmup, 1, 0) if 512 in kv and variant == 0 else None
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -211,6 +228,8 @@ def main() -> int:
             "gbps": {str(L): round(r["gbps"], 1) for L, r in res.items()},
             "pct_of_peak": {str(L): round(100 * r["frac"], 1) for L, r in res.items()},
             "us_per_call_hot": {str(L): round(r["us_hot"], 3) for L, r in res.items()},
+            "plans": {str(L): r["plan"] for L, r in res.items()},
+            "fused_path_us_per_call_512": None if fused512 is None else round(fused512["us_cold"], 3),
         },
         "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": traffic},

@@ -29,10 +29,10 @@
  *     caller's next synchronisation.
  *   - Status codes replace the reference's print-and-continue
  *     (qwen_infer.cu:679-683).  No call ever exits the process.
- *   - A context owns device scratch (split partials, merge counters, RoPE
- *     table).  Calls that share a context must be ordered on one stream, the
- *     way the reference's per-head launches share d_fd_partial on the default
- *     stream (qwen_infer.cu:672-676).
+ *   - A context owns device scratch (split partials, RoPE table).  Calls that
+ *     share a context must be ordered on one stream, the way the reference's
+ *     per-head launches share d_fd_partial on the default stream
+ *     (qwen_infer.cu:672-676).
  */
 #ifndef QDIY_ATTN_H
 #define QDIY_ATTN_H
@@ -93,8 +93,9 @@ int qd_qkv_bias_rope_cache(qd_ctx* ctx, uint16_t* qkv, const uint16_t* bias,
 /* q=1 attention of all heads over cache rows [0, seqlen):
  *   out[h] = half( softmax_j( q[h].K[j,h] / sqrt(128) ) . V[j,h] )
  * in fp32 with fp16 inputs and output.  Picks the single-workgroup-per-head
- * (fused) or the split-KV kernel and its split count from seqlen.  Replaces
- * the 16 per-head launches of qwen_infer.cu:646-678 with one launch.
+ * (fused) or the split-KV path and its split count from seqlen.  Replaces
+ * the 16-32 per-head launches of qwen_infer.cu:646-678 with one launch
+ * (fused) or two (split: stage 1 + merge), covering all heads.
  * Requires 1 <= seqlen <= max_seqlen; q, out, k_layer, v_layer 16-byte
  * aligned; kv strides multiples of 8 elements. */
 int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
@@ -110,9 +111,9 @@ int qd_decode_attention_fused(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
 
 /* Explicit split-KV variant (fd_v5_split_stage1_kernel + fd_opt_stage2_kernel,
  * flash_decode_q1_opt.cuh:548-724): num_splits workgroups per head write fp32
- * partials; the last workgroup of each head to finish merges them with the
- * log-sum-exp rule in the same launch.  num_splits <= 0 picks the count;
- * otherwise 1 <= num_splits <= qd_max_splits(). */
+ * partials (m, l, O[128]); a one-workgroup-per-head merge kernel on the same
+ * stream folds them with the log-sum-exp rule.  num_splits <= 0 picks the
+ * count; otherwise 1 <= num_splits <= qd_max_splits(). */
 int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
                               const uint16_t* v_layer, uint16_t* out, int seqlen,
                               int num_heads, int head_dim, int num_splits,

@@ -3,6 +3,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -27,21 +28,23 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Number of workgroups the split planner aims for: four 256-thread
-// workgroups per CU on MI355X's 256 CUs keeps every CU streaming.
-constexpr int kTargetWorkgroups = 1024;
-// Each split scans at least this many rows so the merge stays a small share.
-constexpr int kMinRowsPerSplit = 64;
+// Split planner, from measured sweeps on MI355X (16 heads, 4-wave workgroups,
+// cold KV): a head's rows are cut into at most kMaxAutoSplits splits of at
+// least kMinRowsPerSplit rows; past kLongRows the split count drops to
+// kLongSplits (one workgroup per CU at 16 heads), where longer per-workgroup
+// scans beat a larger merge.
+constexpr int kMaxAutoSplits = 64;
+constexpr int kMinRowsPerSplit = 32;
+constexpr int kLongRows = 16384;
+constexpr int kLongSplits = 16;
 // Up to this many rows the fused (one workgroup per head) kernel is used.
 constexpr int kFusedMaxRows = 64;
 
-qd::AttnPlan plan_split(int seqlen, int num_heads, int requested) {
+qd::AttnPlan plan_split(int seqlen, int requested) {
   int splits = requested;
   if (splits <= 0) {
-    int target = kTargetWorkgroups / num_heads;
-    if (target < 1) target = 1;
-    int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
-    splits = target < by_rows ? target : by_rows;
+    const int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
+    splits = seqlen > kLongRows ? kLongSplits : (by_rows < kMaxAutoSplits ? by_rows : kMaxAutoSplits);
   }
   if (splits < 1) splits = 1;
   if (splits > qd::kMaxSplits) splits = qd::kMaxSplits;
@@ -51,7 +54,8 @@ qd::AttnPlan plan_split(int seqlen, int num_heads, int requested) {
   plan.variant = 1;
   plan.rows_per_split = rows;
   plan.splits = (seqlen + rows - 1) / rows;    // no empty workgroups
-  plan.rows_per_tile = rows >= 128 ? 8 : (rows >= 64 ? 4 : 2);
+  plan.waves = 4;
+  plan.rows_per_tile = rows >= 64 ? 4 : 2;
   return plan;
 }
 
@@ -61,6 +65,7 @@ qd::AttnPlan plan_fused(int seqlen) {
   plan.splits = 1;
   plan.rows_per_split = seqlen;
   plan.rows_per_tile = 4;
+  plan.waves = 16;
   return plan;
 }
 
@@ -92,7 +97,6 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.out = out;
   p.part_o = ctx->part_o;
   p.part_ml = ctx->part_ml;
-  p.counters = ctx->counters;
   p.row_stride = ctx->cfg.kv_row_stride;
   p.head_stride = ctx->cfg.kv_head_stride;
   p.seqlen = seqlen;
@@ -104,7 +108,8 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
 }
 
 int run_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                  uint16_t* out, int seqlen, const qd::AttnPlan& plan, hipStream_t stream) {
+                  uint16_t* out, int seqlen, const qd::AttnPlan& plan_in, hipStream_t stream) {
+  const qd::AttnPlan& plan = plan_in;
   const qd::AttnParams p = make_params(ctx, q, k, v, out, seqlen, plan);
   hipError_t e = qd::launch_decode_attention(p, plan, stream);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
@@ -144,13 +149,10 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   };
   if ((e = hipMalloc(&ctx->part_o, H * qd::kMaxSplits * 128 * sizeof(float))) != hipSuccess ||
       (e = hipMalloc(&ctx->part_ml, H * qd::kMaxSplits * sizeof(float2))) != hipSuccess ||
-      (e = hipMalloc(&ctx->counters, H * sizeof(unsigned))) != hipSuccess ||
       (e = hipMalloc(&ctx->rope_cs, S * 64 * sizeof(float2))) != hipSuccess) {
     int code = hip_fail(e, "hipMalloc of context scratch");
     return cleanup(code == QD_EHIP ? QD_ENOMEM : code);
   }
-  if ((e = hipMemset(ctx->counters, 0, H * sizeof(unsigned))) != hipSuccess)
-    return cleanup(hip_fail(e, "hipMemset of split counters"));
 
   // RoPE table: theta = float(pos) * powf(base, (-2*i)/head_dim), then fp32
   // cosf/sinf (fused_qkv_rope_cache.cuh:36-38), evaluated once per context.
@@ -183,7 +185,6 @@ int qd_ctx_destroy(qd_ctx* ctx) {
   if (switch_dev) (void)hipSetDevice(ctx->device);
   if (ctx->part_o) (void)hipFree(ctx->part_o);
   if (ctx->part_ml) (void)hipFree(ctx->part_ml);
-  if (ctx->counters) (void)hipFree(ctx->counters);
   if (ctx->rope_cs) (void)hipFree(ctx->rope_cs);
   if (switch_dev) (void)hipSetDevice(dev);
   delete ctx;
@@ -226,7 +227,7 @@ int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* n
   if (seqlen < 1 || seqlen > ctx->cfg.max_seqlen)
     return fail(QD_EINVAL, "seqlen %d outside [1, %d]", seqlen, ctx->cfg.max_seqlen);
   const qd::AttnPlan plan =
-      seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(seqlen, ctx->cfg.num_heads, 0);
+      seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(seqlen, 0);
   *variant = plan.variant;
   *num_splits = plan.splits;
   return QD_OK;
@@ -238,7 +239,7 @@ int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
   int rc = check_attention_args(ctx, q, k_layer, v_layer, out, seqlen, num_heads, head_dim);
   if (rc != QD_OK) return rc;
   const qd::AttnPlan plan =
-      seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(seqlen, num_heads, 0);
+      seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(seqlen, 0);
   return run_attention(ctx, q, k_layer, v_layer, out, seqlen, plan, stream);
 }
 
@@ -258,7 +259,7 @@ int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
   if (num_splits > qd::kMaxSplits)
     return fail(QD_EINVAL, "num_splits %d above the maximum %d", num_splits, qd::kMaxSplits);
   return run_attention(ctx, q, k_layer, v_layer, out, seqlen,
-                       plan_split(seqlen, num_heads, num_splits), stream);
+                       plan_split(seqlen, num_splits), stream);
 }
 
 int qd_max_splits(void) { return qd::kMaxSplits; }

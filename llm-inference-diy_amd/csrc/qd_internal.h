@@ -9,7 +9,7 @@
 
 namespace qd {
 
-// Largest split count per head.  Scratch per context is
+// Largest split count (workgroups per head).  Scratch per context:
 // num_heads * kMaxSplits * (128 + 2) floats (2.1 MB at 16 heads).
 constexpr int kMaxSplits = 256;
 
@@ -22,12 +22,11 @@ struct AttnParams {
   uint16_t* out;          // [H][128]
   float* part_o;          // [H][splits][128] unnormalised fp32 partial outputs
   float2* part_ml;        // [H][splits] (running max in log2 units, running sum)
-  unsigned* counters;     // [H] finished-split counters, zero between launches
   long long row_stride;
   long long head_stride;
   int seqlen;
   int num_heads;
-  int splits;
+  int splits;             // workgroups per head
   int rows_per_split;
   float scale_log2;       // log2(e) / sqrt(128)
 };
@@ -49,7 +48,8 @@ struct AttnPlan {
   int variant;            // 0 fused, 1 split
   int splits;             // workgroups per head
   int rows_per_split;     // rows each workgroup scans
-  int rows_per_tile;      // rows per group per tile (template U) of the split kernel
+  int rows_per_tile;      // rows per group per tile (template U)
+  int waves;              // waves per split workgroup (4, 8 or 16)
 };
 
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream);
@@ -63,5 +63,4 @@ struct qd_ctx {
   float2* rope_cs;        // [max_seqlen][64]
   float* part_o;          // [H][kMaxSplits][128]
   float2* part_ml;        // [H][kMaxSplits]
-  unsigned* counters;     // [H]
 };

@@ -143,7 +143,7 @@ class Context:
         H = self.num_heads
         if q.numel() < H * HEAD_DIM or out.numel() < H * HEAD_DIM:
             raise ValueError("q and out need num_heads*128 elements")
-        if seqlen >= 1:
+        if 1 <= seqlen <= self.max_seqlen:      # out-of-range lengths are the C ABI's to reject
             self._check_cache(k_layer, "k_layer", seqlen)
             self._check_cache(v_layer, "v_layer", seqlen)
         args = (self._h, _ptr(q, "q"), _ptr(k_layer, "k_layer", False), _ptr(v_layer, "v_layer", False),
