@@ -138,6 +138,9 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
       (cfg->kv_head_stride % 8))
     return fail(QD_EINVAL, "kv strides must be positive multiples of 8 elements");
   if (!(cfg->rope_base > 0.0f)) return fail(QD_EINVAL, "rope_base must be > 0");
+  // the kernels address a row as (32-bit byte offset) from a per-head base
+  if ((long long)cfg->max_seqlen * cfg->kv_row_stride * 2 > 0xFFFFFF00LL)
+    return fail(QD_EINVAL, "max_seqlen * kv_row_stride * 2 bytes must stay below 4 GiB");
 
   qd_ctx* ctx = new (std::nothrow) qd_ctx;
   if (!ctx) return fail(QD_ENOMEM, "host allocation failed");

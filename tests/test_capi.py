@@ -51,7 +51,8 @@ def test_ctx_create_rejects_bad_cfg_without_touching_the_gpu(qdiy):
                 qdiy.Cfg(0, 128, 128, 2048, 128, 10000.0),      # no heads
                 qdiy.Cfg(16, 128, 0, 2048, 128, 10000.0),       # no rows
                 qdiy.Cfg(16, 128, 128, 2047, 128, 10000.0),     # stride not a multiple of 8
-                qdiy.Cfg(16, 128, 128, 2048, 128, 0.0)):        # rope base
+                qdiy.Cfg(16, 128, 128, 2048, 128, 0.0),         # rope base
+                qdiy.Cfg(16, 128, 1 << 20, 2048, 128, 1e4)):    # row span beyond 32-bit offsets
         assert lib.qd_ctx_create(ctypes.byref(cfg), ctypes.byref(h)) == qdiy.QD_EINVAL
         assert h.value is None
         assert lib.qd_last_error()
