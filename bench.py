@@ -62,6 +62,7 @@ def bench_lib():
     lib = ctypes.CDLL(path)
     vp, i, ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
     lib.qd_bench_decode_attention.argtypes = [vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
+    lib.qd_bench_attn_front.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
     return lib
 
 
@@ -120,6 +121,63 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     return res
 
 
+def measure_front(lib, steps: int, warmup: int):
+    """Config 4: QKV GEMV [6144 x 2048] + bias + RoPE at pos 2047 + append, then
+    attention over 2048 rows; weights and KV rotate over enough layers (>= 1 GiB)
+    that every call streams from HBM."""
+    import torch
+
+    import qdiy
+
+    L, pos = 2048, 2047
+    w_elems = 3 * HID * HID
+    kv_elems = L * HID
+    n_layers = max(3, math.ceil((1 << 30) / (2 * (w_elems + 2 * kv_elems))))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    x = torch.empty(n_layers * HID, dtype=torch.float16, device="cuda").normal_(generator=gen)
+    w = torch.empty(n_layers * w_elems, dtype=torch.float16, device="cuda").normal_(0.0, 0.02, generator=gen)
+    b = torch.empty(n_layers * 3 * HID, dtype=torch.float16, device="cuda").normal_(0.0, 0.02, generator=gen)
+    kc = torch.empty(n_layers * kv_elems, dtype=torch.float16, device="cuda").normal_(generator=gen)
+    vc = torch.empty_like(kc).normal_(generator=gen)
+    qkv = torch.empty(n_layers * 3 * HID, dtype=torch.float16, device="cuda")
+    out = torch.empty(n_layers * HID, dtype=torch.float16, device="cuda")
+    ctx = qdiy.Context(num_heads=H, max_seqlen=L)
+    stream = torch.cuda.current_stream()
+    sh = ctypes.c_void_p(stream.cuda_stream)
+
+    def run(iters, with_attn):
+        rc = lib.qd_bench_attn_front(ctx._h, x.data_ptr(), w.data_ptr(), b.data_ptr(), qkv.data_ptr(),
+                                     kc.data_ptr(), vc.data_ptr(), out.data_ptr(), w_elems, kv_elems,
+                                     n_layers, pos, L, H, iters, with_attn, sh)
+        if rc != 0:
+            raise RuntimeError(f"front-end bench failed: {qdiy.load().qd_last_error().decode()}")
+
+    def timed(iters, with_attn):
+        run(warmup, with_attn)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        run(iters, with_attn)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / iters
+
+    us_front = timed(steps, 0)
+    us_all = timed(steps, 1)
+    ctx.close()
+    del w, kc, vc
+    torch.cuda.empty_cache()
+    front_bytes = w_elems * 2 + HID * 2 + 3 * HID * 2 + 2 * HID * 2
+    all_bytes = front_bytes + 2 * L * HID * 2 + HID * 2      # BASELINE.md config 4: 41,971,712
+    log(f"[bench] config 4 (L=2048, pos 2047): front end {us_front:.2f} us "
+        f"({front_bytes / us_front / 1e3:.0f} GB/s), front end + attention {us_all:.2f} us "
+        f"({all_bytes / us_all / 1e3:.0f} GB/s), {n_layers} layers rotated")
+    return {"us_front_end": round(us_front, 3), "us_front_end_plus_attention": round(us_all, 3),
+            "bytes": all_bytes, "gbps": round(all_bytes / us_all / 1e3, 1),
+            "front_end_gbps": round(front_bytes / us_front / 1e3, 1)}
+
+
 def cpu_baseline(L: int, seconds: float):
     """Times the C oracle (restatement of the reference kernels) on host cores."""
     import numpy as np
@@ -165,6 +223,7 @@ def main() -> int:
     ap.add_argument("--variant", choices=["auto", "fused", "split"], default="auto")
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-front", action="store_true", help="skip the config-4 front-end timing")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one 256 MiB device copy (known FETCH_SIZE/WRITE_SIZE) and exit")
@@ -199,6 +258,7 @@ def main() -> int:
     head = res[HEADLINE_L]
     # config 1 names the fused single-workgroup-per-head path at L=512
     fused512 = measure(lib, 512, args.steps, args.warmup, 1, 0) if 512 in kv and variant == 0 else None
+    front = None if args.no_front else measure_front(lib, args.steps, args.warmup)
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -230,6 +290,7 @@ def main() -> int:
             "us_per_call_hot": {str(L): round(r["us_hot"], 3) for L, r in res.items()},
             "plans": {str(L): r["plan"] for L, r in res.items()},
             "fused_path_us_per_call_512": None if fused512 is None else round(fused512["us_cold"], 3),
+            "config4_front_end": front,
         },
         "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": traffic},

@@ -90,6 +90,25 @@ int qd_qkv_bias_rope_cache(qd_ctx* ctx, uint16_t* qkv, const uint16_t* bias,
                            int max_seqlen, int num_heads, int head_dim,
                            hipStream_t stream);
 
+/* Attention front end of one decode layer in one launch: RMSNorm of x (when
+ * norm_w != NULL; rmsnorm.cuh:6-57, call qwen_infer.cu:626) -> QKV GEMV
+ * (hgemv_kernel, hgemm_final.cuh:274-295, call :629) -> + qkv_bias (:631) ->
+ * rotate-half RoPE and K/V append at pos (:634-642).  Each intermediate is
+ * rounded to fp16 where the reference stores one (normalised x, GEMV output,
+ * biased QKV).
+ *   x:      [H*128] layer input (d_x), 16-byte aligned
+ *   norm_w: [H*128] RMSNorm weight (ln_1) or NULL to use x as given
+ *   w_qkv:  [3*H*128][H*128] QKV weight in the .bin file's [out][in] layout
+ *           (c_attn.weight, convert_weights.py:133-137), 16-byte aligned
+ *   qkv:    [3*H*128] out: rotated Q, biased K and V (the reference's d_qkv)
+ * H*128 must be a multiple of 512, at most 4096.  The GEMV sums each row in a
+ * fixed order (per-lane sequential, then a fixed 64-lane tree), so results
+ * are deterministic and reproducible on the host. */
+int qd_qkv_proj_rope_cache(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_w, float eps,
+                           const uint16_t* w_qkv, const uint16_t* qkv_bias, uint16_t* qkv,
+                           uint16_t* k_layer, uint16_t* v_layer, int pos, int max_seqlen,
+                           int num_heads, int head_dim, hipStream_t stream);
+
 /* q=1 attention of all heads over cache rows [0, seqlen):
  *   out[h] = half( softmax_j( q[h].K[j,h] / sqrt(128) ) . V[j,h] )
  * in fp32 with fp16 inputs and output.  Picks the single-workgroup-per-head

@@ -16,7 +16,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libqdiy.so")
 BENCH_LIB = os.path.join(LIB_DIR, "libqdiy_bench.so")
 
-SOURCES = ["qd_capi.cpp", "qd_attention.hip", "qd_rope_cache.hip"]
+SOURCES = ["qd_capi.cpp", "qd_attention.hip", "qd_rope_cache.hip", "qd_decode_ops.hip"]
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for all device code: plain float code is

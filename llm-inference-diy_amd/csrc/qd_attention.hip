@@ -27,38 +27,13 @@
 //     whole-L2 writeback per workgroup on gfx950 (buffer_wbl2 sc1, measured
 //     ~1 us each and serialised per XCD), far more than a second launch.
 //   * No MFMA: at q=1 the work is a bandwidth-bound GEMV-like reduction.
+#include "qd_device.h"
 #include "qd_internal.h"
 
 namespace qd {
 namespace {
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
 constexpr int kD = 128;
-
-// DPP row-local permutations (gfx9 encodings).
-constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
-constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]
-constexpr int kDppHalfMirror = 0x141; // row_half_mirror: lane i <-> 7-i within 8
-constexpr int kDppMirror = 0x140;     // row_mirror: lane i <-> 15-i within 16
-
-template <int Ctrl>
-__device__ __forceinline__ float dpp_mov(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), Ctrl, 0xF, 0xF, true));
-}
-
-// Sum over the 16 lanes of a DPP row; all 16 lanes receive the same value
-// (each step adds a partner whose value is the mirror image of its own).
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dpp_mov<kDppQuadSwap1>(x);
-  x += dpp_mov<kDppQuadSwap2>(x);
-  x += dpp_mov<kDppHalfMirror>(x);
-  x += dpp_mov<kDppMirror>(x);
-  return x;
-}
 
 __device__ __forceinline__ float dot8(const f16x8 k, const f16x8 q) {
   float d = __builtin_amdgcn_fdot2(f16x2{k[0], k[1]}, f16x2{q[0], q[1]}, 0.0f, false);

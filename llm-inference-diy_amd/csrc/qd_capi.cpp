@@ -237,6 +237,49 @@ int qd_qkv_bias_rope_cache(qd_ctx* ctx, uint16_t* qkv, const uint16_t* bias, uin
   return QD_OK;
 }
 
+int qd_qkv_proj_rope_cache(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_w, float eps,
+                           const uint16_t* w_qkv, const uint16_t* qkv_bias, uint16_t* qkv,
+                           uint16_t* k_layer, uint16_t* v_layer, int pos, int max_seqlen,
+                           int num_heads, int head_dim, hipStream_t stream) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  if (!x || !w_qkv || !qkv || !k_layer || !v_layer)
+    return fail(QD_EINVAL, "x, w_qkv, qkv, k_layer and v_layer must be non-NULL");
+  if (!aligned16(x) || !aligned16(w_qkv) || (norm_w && !aligned16(norm_w)))
+    return fail(QD_EINVAL, "x, norm_w and w_qkv must be 16-byte aligned");
+  if (((uintptr_t)qkv | (uintptr_t)k_layer | (uintptr_t)v_layer | (uintptr_t)qkv_bias) & 1u)
+    return fail(QD_EINVAL, "fp16 buffers must be 2-byte aligned");
+  if (head_dim != QD_HEAD_DIM) return fail(QD_EINVAL, "head_dim %d unsupported (must be 128)", head_dim);
+  if (num_heads != ctx->cfg.num_heads)
+    return fail(QD_EINVAL, "num_heads %d differs from the context's %d", num_heads, ctx->cfg.num_heads);
+  const int hidden = num_heads * QD_HEAD_DIM;
+  if (hidden % 512 != 0 || hidden > 4096)
+    return fail(QD_EINVAL, "hidden size %d unsupported (multiple of 512, at most 4096)", hidden);
+  if (!(eps >= 0.0f)) return fail(QD_EINVAL, "eps must be >= 0");
+  if (max_seqlen < 1 || max_seqlen > ctx->cfg.max_seqlen)
+    return fail(QD_EINVAL, "max_seqlen %d outside [1, %d]", max_seqlen, ctx->cfg.max_seqlen);
+  if (pos < 0 || pos >= max_seqlen) return fail(QD_EINVAL, "pos %d outside [0, %d)", pos, max_seqlen);
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
+    return fail(QD_EINVAL, "current device %d is not the context's device %d", dev, ctx->device);
+  qd::QkvFrontParams p;
+  p.x = x;
+  p.norm_w = norm_w;
+  p.eps = eps;
+  p.w = w_qkv;
+  p.bias = qkv_bias;
+  p.qkv = qkv;
+  p.k_layer = k_layer;
+  p.v_layer = v_layer;
+  p.rope_cs = ctx->rope_cs;
+  p.row_stride = ctx->cfg.kv_row_stride;
+  p.head_stride = ctx->cfg.kv_head_stride;
+  p.pos = pos;
+  p.num_heads = num_heads;
+  hipError_t e = qd::launch_qkv_front(p, stream);
+  if (e != hipSuccess) return hip_fail(e, "qkv_proj_rope_cache launch");
+  return QD_OK;
+}
+
 int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* num_splits) {
   if (!ctx || !variant || !num_splits) return fail(QD_EINVAL, "NULL argument");
   if (seqlen < 1 || seqlen > ctx->cfg.max_seqlen)

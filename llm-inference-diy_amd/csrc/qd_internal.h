@@ -43,6 +43,24 @@ struct RopeParams {
   int num_heads;
 };
 
+// Attention front end of one decode layer: [RMSNorm] -> QKV GEMV -> bias ->
+// RoPE -> KV append.  hidden = num_heads * 128, a multiple of 512 up to 4096.
+struct QkvFrontParams {
+  const uint16_t* x;      // [hidden] layer input
+  const uint16_t* norm_w; // [hidden] RMSNorm weight, or null for no norm
+  float eps;
+  const uint16_t* w;      // [3*hidden][hidden] QKV weight, [out][in]
+  const uint16_t* bias;   // [3*hidden] or null
+  uint16_t* qkv;          // [3*hidden] out: rotated Q, biased K and V
+  uint16_t* k_layer;
+  uint16_t* v_layer;
+  const float2* rope_cs;  // [max_seqlen][64] (cos, sin)
+  long long row_stride;
+  long long head_stride;
+  int pos;
+  int num_heads;
+};
+
 // Launch plan of one decode-attention call.
 struct AttnPlan {
   int variant;            // 0 fused, 1 split
@@ -54,6 +72,7 @@ struct AttnPlan {
 
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream);
 hipError_t launch_qkv_bias_rope_cache(const RopeParams& p, hipStream_t stream);
+hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream);
 
 }  // namespace qd
 

@@ -24,7 +24,8 @@ QD_OK, QD_EINVAL, QD_EHIP, QD_ENOMEM = 0, 1, 2, 3
 FUSED, SPLIT = 0, 1
 
 EXPORTS = (
-    "qd_ctx_create", "qd_ctx_destroy", "qd_qkv_bias_rope_cache", "qd_decode_attention",
+    "qd_ctx_create", "qd_ctx_destroy", "qd_qkv_bias_rope_cache", "qd_qkv_proj_rope_cache",
+    "qd_decode_attention",
     "qd_decode_attention_fused", "qd_decode_attention_split", "qd_decode_attention_plan",
     "qd_max_splits", "qd_last_error", "qd_version",
 )
@@ -57,6 +58,8 @@ def load() -> ctypes.CDLL:
     L.qd_ctx_create.argtypes = [ctypes.POINTER(Cfg), ctypes.POINTER(vp)]
     L.qd_ctx_destroy.argtypes = [vp]
     L.qd_qkv_bias_rope_cache.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
+    L.qd_qkv_proj_rope_cache.argtypes = [vp, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp, i, i, i,
+                                         i, vp]
     L.qd_decode_attention.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     L.qd_decode_attention_fused.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     L.qd_decode_attention_split.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
@@ -176,6 +179,32 @@ class Context:
         bptr = None if bias is None else _ptr(bias, "bias")
         _check(load().qd_qkv_bias_rope_cache(self._h, _ptr(qkv, "qkv"), bptr,
                                              _ptr(k_layer, "k_layer", False),
+                                             _ptr(v_layer, "v_layer", False), pos, max_seqlen, H,
+                                             HEAD_DIM, _stream(stream)))
+
+
+    def qkv_proj_rope_cache(self, x: torch.Tensor, norm_w, w_qkv: torch.Tensor, bias,
+                            qkv: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                            pos: int, eps: float = 1e-6, max_seqlen: int | None = None,
+                            stream=None) -> None:
+        """[RMSNorm] + QKV GEMV ([out][in] weight) + bias + RoPE + cache append at pos."""
+        H = self.num_heads
+        hid = H * HEAD_DIM
+        if x.numel() < hid or qkv.numel() < 3 * hid or w_qkv.numel() < 3 * hid * hid:
+            raise ValueError("x needs H*128, qkv 3*H*128 and w_qkv 3*H*128*H*128 elements")
+        if norm_w is not None and norm_w.numel() < hid:
+            raise ValueError("norm_w needs H*128 elements")
+        if bias is not None and bias.numel() < 3 * hid:
+            raise ValueError("bias needs 3*H*128 elements")
+        if max_seqlen is None:
+            max_seqlen = self.max_seqlen
+        if 0 <= pos < max_seqlen:
+            self._check_cache(k_layer, "k_layer", pos + 1)
+            self._check_cache(v_layer, "v_layer", pos + 1)
+        opt = lambda t, n: None if t is None else _ptr(t, n)
+        _check(load().qd_qkv_proj_rope_cache(self._h, _ptr(x, "x"), opt(norm_w, "norm_w"), eps,
+                                             _ptr(w_qkv, "w_qkv"), opt(bias, "bias"),
+                                             _ptr(qkv, "qkv"), _ptr(k_layer, "k_layer", False),
                                              _ptr(v_layer, "v_layer", False), pos, max_seqlen, H,
                                              HEAD_DIM, _stream(stream)))
 

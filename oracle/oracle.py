@@ -50,6 +50,15 @@ def lib() -> ctypes.CDLL:
         L.qd_oracle_qkv_bias_rope_cache.restype = ctypes.c_int
         L.qd_oracle_rope_cos_sin.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                              ctypes.c_float, f32p, f32p]
+        L.qd_oracle_wave64_sum.argtypes = [f32p]
+        L.qd_oracle_wave64_sum.restype = ctypes.c_float
+        L.qd_oracle_rmsnorm.argtypes = [u16p, u16p, ctypes.c_int, ctypes.c_float, u16p, ctypes.c_int]
+        L.qd_oracle_gemv.argtypes = [u16p, u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, u16p]
+        L.qd_oracle_qkv_front.argtypes = [u16p, u16p, ctypes.c_float, u16p, u16p, u16p, u16p,
+                                          u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ll, ll,
+                                          ctypes.c_float, ctypes.c_int]
+        L.qd_oracle_qkv_front.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -131,3 +140,45 @@ def rope_cos_sin(pos, i, head_dim=128, rope_base=10000.0):
     s = ctypes.c_float()
     lib().qd_oracle_rope_cos_sin(pos, i, head_dim, rope_base, ctypes.byref(c), ctypes.byref(s))
     return np.float32(c.value), np.float32(s.value)
+
+
+ORDER_REF, ORDER_WAVE64 = 0, 1
+
+
+def wave64_sum(lanes) -> np.float32:
+    a = np.ascontiguousarray(lanes, dtype=np.float32)
+    assert a.size == 64
+    return np.float32(lib().qd_oracle_wave64_sum(_f32(a)))
+
+
+def rmsnorm(x, w, eps=1e-6, order=ORDER_REF):
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    w = np.ascontiguousarray(w, dtype=np.float16)
+    out = np.zeros_like(x)
+    lib().qd_oracle_rmsnorm(_u16(x), _u16(w), x.size, eps, _u16(out), order)
+    return out
+
+
+def gemv(x, W, N, K, layout=0, order=ORDER_REF):
+    """out[n] = half(sum_k x[k] W(n,k)); layout 0: W[n*K+k], 1: W[k*N+n]."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    W = np.ascontiguousarray(W, dtype=np.float16)
+    out = np.zeros(N, np.float16)
+    lib().qd_oracle_gemv(_u16(x), _u16(W), N, K, layout, order, _u16(out))
+    return out
+
+
+def qkv_front(x, norm_w, w_qkv, bias, qkv_out, k_cache, v_cache, pos, num_heads,
+              eps=1e-6, head_dim=128, row_stride=None, head_stride=None, rope_base=10000.0,
+              order=ORDER_WAVE64):
+    """RMSNorm (optional) + QKV GEMV + bias + RoPE + cache append, in place on the outputs."""
+    if row_stride is None:
+        row_stride = num_heads * head_dim
+    if head_stride is None:
+        head_stride = head_dim
+    rc = lib().qd_oracle_qkv_front(_u16(x), None if norm_w is None else _u16(norm_w), eps,
+                                   _u16(w_qkv), None if bias is None else _u16(bias),
+                                   _u16(qkv_out), _u16(k_cache), _u16(v_cache), pos, num_heads,
+                                   head_dim, row_stride, head_stride, rope_base, order)
+    if rc != 0:
+        raise ValueError("qd_oracle_qkv_front rejected its arguments")

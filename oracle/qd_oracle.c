@@ -390,3 +390,120 @@ int qd_oracle_qkv_bias_rope_cache(uint16_t* qkv, const uint16_t* bias,
   }
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Adjacent decode-step ops: RMSNorm, GEMV, QKV front end                    */
+/* ------------------------------------------------------------------------ */
+
+float qd_oracle_wave64_sum(const float* a) {
+  float rows[4];
+  for (int r = 0; r < 4; ++r) {
+    const float* x = a + 16 * r;
+    float q[4];
+    for (int i = 0; i < 4; ++i) q[i] = (x[4 * i] + x[4 * i + 1]) + (x[4 * i + 2] + x[4 * i + 3]);
+    rows[r] = (q[0] + q[1]) + (q[2] + q[3]);
+  }
+  return (rows[0] + rows[1]) + (rows[2] + rows[3]);
+}
+
+/* 32-lane xor butterfly (masks 16..1), the value every lane ends with. */
+static float warp32_sum(float* lane) {
+  float tmp[32];
+  for (int mask = 16; mask >= 1; mask >>= 1) {
+    for (int ln = 0; ln < 32; ++ln) tmp[ln] = lane[ln] + lane[ln ^ mask];
+    memcpy(lane, tmp, sizeof(tmp));
+  }
+  return lane[0];
+}
+
+/* Sequential per-lane sums of f(k) over the wave64 element layout. */
+static void wave64_lane_sums(int n, const float* v, float* lanes) {
+  const int chunks = (n + 511) / 512;
+  for (int l = 0; l < 64; ++l) {
+    float acc = 0.0f;
+    for (int j = 0; j < chunks; ++j)
+      for (int e = 0; e < 8; ++e) {
+        int k = 512 * j + 8 * l + e;
+        acc += (k < n) ? v[k] : 0.0f;
+      }
+    lanes[l] = acc;
+  }
+}
+
+void qd_oracle_rmsnorm(const uint16_t* x, const uint16_t* w, int n, float eps,
+                       uint16_t* out, int order) {
+  float* sq = (float*)malloc(sizeof(float) * (size_t)n);
+  for (int k = 0; k < n; ++k) {
+    float v = qd_oracle_h2f(x[k]);
+    sq[k] = v * v;                                  /* exact: 22-bit product */
+  }
+  float total;
+  if (order == QD_ORDER_WAVE64) {
+    float lanes[64];
+    wave64_lane_sums(n, sq, lanes);
+    total = qd_oracle_wave64_sum(lanes);
+  } else {
+    /* rmsnorm.cuh:9-45 with blockDim 512: thread t sums its n/512 contiguous
+     * items, warps reduce by xor butterfly, warp 0 reduces the 16 warp sums. */
+    const int per = n / 512;
+    float warp_sums[32];
+    for (int wp = 0; wp < 16; ++wp) {
+      float lane[32];
+      for (int ln = 0; ln < 32; ++ln) {
+        int t = wp * 32 + ln;
+        float acc = 0.0f;
+        for (int i = 0; i < per; ++i) acc += sq[t * per + i];
+        lane[ln] = acc;
+      }
+      warp_sums[wp] = warp32_sum(lane);
+    }
+    for (int ln = 16; ln < 32; ++ln) warp_sums[ln] = 0.0f;
+    total = warp32_sum(warp_sums);
+  }
+  const float var = total / (float)n;
+  const float r = 1.0f / sqrtf(var + eps);
+  for (int k = 0; k < n; ++k)
+    out[k] = qd_oracle_f2h(qd_oracle_h2f(x[k]) * r * qd_oracle_h2f(w[k]));
+  free(sq);
+}
+
+static float gemv_row(const uint16_t* x, const uint16_t* W, int N, int K, int layout,
+                      int order, int n, float* scratch) {
+  for (int k = 0; k < K; ++k) {
+    uint16_t wk = layout == 0 ? W[(long long)n * K + k] : W[(long long)k * N + n];
+    scratch[k] = qd_oracle_h2f(x[k]) * qd_oracle_h2f(wk);   /* exact product */
+  }
+  if (order == QD_ORDER_WAVE64) {
+    float lanes[64];
+    wave64_lane_sums(K, scratch, lanes);
+    return qd_oracle_wave64_sum(lanes);
+  }
+  float sum = 0.0f;                                  /* hgemm_final.cuh:278-293 */
+  for (int k = 0; k < K; ++k) sum += scratch[k];
+  return sum;
+}
+
+void qd_oracle_gemv(const uint16_t* x, const uint16_t* W, int N, int K, int layout,
+                    int order, uint16_t* out) {
+  float* scratch = (float*)malloc(sizeof(float) * (size_t)K);
+  for (int n = 0; n < N; ++n) out[n] = qd_oracle_f2h(gemv_row(x, W, N, K, layout, order, n, scratch));
+  free(scratch);
+}
+
+int qd_oracle_qkv_front(const uint16_t* x, const uint16_t* norm_w, float eps,
+                        const uint16_t* w_qkv, const uint16_t* bias, uint16_t* qkv_out,
+                        uint16_t* k_cache, uint16_t* v_cache, int pos, int num_heads,
+                        int head_dim, long long row_stride, long long head_stride,
+                        float rope_base, int order) {
+  if (!x || !w_qkv || !qkv_out || !k_cache || !v_cache || pos < 0 || num_heads < 1 ||
+      head_dim < 2 || (head_dim & 1))
+    return -1;
+  const int hidden = num_heads * head_dim;
+  uint16_t* xn = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)hidden);
+  if (norm_w) qd_oracle_rmsnorm(x, norm_w, hidden, eps, xn, order);
+  else memcpy(xn, x, sizeof(uint16_t) * (size_t)hidden);
+  qd_oracle_gemv(xn, w_qkv, 3 * hidden, hidden, 0, order, qkv_out);   /* qwen_infer.cu:629 */
+  free(xn);
+  return qd_oracle_qkv_bias_rope_cache(qkv_out, bias, k_cache, v_cache, pos, num_heads, head_dim,
+                                       row_stride, head_stride, rope_base);
+}

@@ -83,6 +83,44 @@ int qd_oracle_qkv_bias_rope_cache(uint16_t* qkv, const uint16_t* bias,
 void qd_oracle_rope_cos_sin(int pos, int i, int head_dim, float rope_base,
                             float* cos_out, float* sin_out);
 
+/* Reduction orders of the adjacent decode-step ops.
+ *   QD_ORDER_REF:    the reference kernels' order (rmsnorm.cuh:15-45 per-thread
+ *                    blocks + 32-lane butterflies; hgemm_final.cuh:278-294
+ *                    sequential k per output column);
+ *   QD_ORDER_WAVE64: the fixed order of this build's gfx950 kernels: lane l of
+ *                    a 64-lane wave owns elements k = 512*j + 8*l + e (j outer,
+ *                    e inner, summed sequentially), then the 64 lane sums are
+ *                    added in the tree of qd_oracle_wave64_sum. */
+enum { QD_ORDER_REF = 0, QD_ORDER_WAVE64 = 1 };
+
+/* The gfx950 wave reduction: within each 16-lane row ((a0+a1)+(a2+a3)) +
+ * ((a4+a5)+(a6+a7)) ..., then (row0+row1) + (row2+row3). */
+float qd_oracle_wave64_sum(const float* lanes);
+
+/* RMSNorm (rmsnorm.cuh:6-57): out = half(x * r * w), r = 1/sqrt(mean(x^2)+eps).
+ * ORDER_REF follows the reference's 512-thread reduction (n must be a multiple
+ * of 512); both orders take r = 1.0f / sqrtf(.) where the reference calls
+ * rsqrtf. */
+void qd_oracle_rmsnorm(const uint16_t* x, const uint16_t* w, int n, float eps,
+                       uint16_t* out, int order);
+
+/* out[n] = half(sum_k x[k] * W(n, k)), n < N.  layout 0: W(n,k) = W[n*K + k]
+ * (the .bin file's [out][in]); layout 1: W(n,k) = W[k*N + n] (the reference
+ * engine's transposed [in][out], transpose.cuh:17-30). */
+void qd_oracle_gemv(const uint16_t* x, const uint16_t* W, int N, int K, int layout,
+                    int order, uint16_t* out);
+
+/* Attention front end of one decode layer (qwen_infer.cu:626-642):
+ * [RMSNorm of x with norm_w when norm_w != NULL] -> QKV GEMV with
+ * w_qkv [3*H*D][H*D] ([out][in]) -> half -> + bias -> half -> rotate-half RoPE
+ * at pos -> K/V cache append.  qkv_out receives the rotated Q and the biased
+ * K and V, as the reference's d_qkv after its three launches. */
+int qd_oracle_qkv_front(const uint16_t* x, const uint16_t* norm_w, float eps,
+                        const uint16_t* w_qkv, const uint16_t* bias, uint16_t* qkv_out,
+                        uint16_t* k_cache, uint16_t* v_cache, int pos, int num_heads,
+                        int head_dim, long long row_stride, long long head_stride,
+                        float rope_base, int order);
+
 #ifdef __cplusplus
 }
 #endif
