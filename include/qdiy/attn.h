@@ -142,6 +142,25 @@ int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
  * fused, 1 for split; *num_splits the split count (1 for fused). */
 int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* num_splits);
 
+/* Complete launch plan of one decode-attention call. */
+typedef struct qd_attn_plan {
+  int variant;        /* 0: one workgroup per head (fused), 1: split + merge */
+  int num_splits;     /* workgroups per head (1 when fused) */
+  int rows_per_split; /* KV rows each workgroup scans (seqlen when fused) */
+  int rows_per_tile;  /* rows each 16-lane group loads per tile */
+  int waves;          /* wavefronts per scan workgroup */
+} qd_attn_plan;
+
+/* Plan of the call selected by `entry` (0: qd_decode_attention,
+ * 1: qd_decode_attention_fused, 2: qd_decode_attention_split with num_splits)
+ * at seqlen.  For a given plan and inputs the outputs are bit-for-bit
+ * deterministic; the plan depends on seqlen, num_heads and the device's CU
+ * count.  No counterpart in the reference (its launch shape is fixed at the
+ * call site, qwen_infer.cu:648-678); it lets a host-side checker restate a
+ * call exactly. */
+int qd_decode_attention_plan_detail(const qd_ctx* ctx, int seqlen, int entry, int num_splits,
+                                    qd_attn_plan* plan);
+
 /* Largest split count a context supports. */
 int qd_max_splits(void);
 

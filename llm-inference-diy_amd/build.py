@@ -20,8 +20,10 @@ SOURCES = ["qd_capi.cpp", "qd_attention.hip", "qd_rope_cache.hip", "qd_decode_op
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for all device code: plain float code is
-# compiled to scalar v_fma/v_mul/v_add only.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# compiled to scalar v_fma/v_mul/v_add only.  No floating-point contraction:
+# every a*b+c in the sources rounds twice unless written as fmaf, which keeps
+# the kernels' arithmetic restatable bit for bit on the host.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-ffp-contract=off"]
 
 
 def hipcc() -> str:

@@ -8,24 +8,35 @@
 //
 // Mapping (wave64):
 //   * A 128-dim fp16 row is 256 B = 16 lanes x 16 B, so a wavefront holds four
-//     16-lane "groups", each owning one KV row per load instruction.  A group's
-//     row-dot is 4 v_dot2 (fp16 x fp16 -> fp32) per lane plus a 4-step DPP
-//     butterfly inside the 16-lane DPP row; every lane of the group ends with
-//     the same score.
+//     16-lane "groups", each owning one KV row per load instruction.  A lane's
+//     share of a row-dot is a pairwise tree of its 8 exact fp16 x fp16
+//     products; a 4-step DPP butterfly inside the 16-lane DPP row adds the
+//     lanes, and every lane of the group ends with the same score.
 //   * Each group keeps its own online-softmax state (m, l, 8 dims of O) in
-//     fp32.  It consumes rows in tiles of U: all 2U 16-byte loads of a tile are
-//     issued first, then one max/rescale per tile, then U exp2 + 8U fp16*fp32
-//     FMAs (v_fma_mix_f32, no conversions).
-//   * Scores live in log2 units (scale_log2 = log2(e)/sqrt(128)) so the
-//     exponentials are single v_exp_f32 instructions.
-//   * The four groups of a wave are merged with lane shuffles, the waves of a
-//     workgroup in LDS.  A split workgroup writes one fp32 partial
-//     (m, l, O[128]); the reference keeps fp16 partials.
-//   * Partials are folded with the log-sum-exp rule by a second,
-//     one-workgroup-per-head kernel.  Cross-workgroup hand-off goes through the
-//     kernel boundary: an agent-scope release inside the kernel lowers to a
-//     whole-L2 writeback per workgroup on gfx950 (buffer_wbl2 sc1, measured
-//     ~1 us each and serialised per XCD), far more than a second launch.
+//     fp32.  It consumes rows in tiles of U: one max/rescale per tile, then U
+//     exp2 + 8U fp16*fp32 FMAs (v_fma_mix_f32, no conversions).
+//   * A launch has about one wave per SIMD, so no other wave hides a tile's
+//     compute latency: the arithmetic is kept short (Estrin exp2, pairwise
+//     dot trees, max-first merges whose exponentials are independent).
+//   * Scores live in log2 units (scale_log2 = log2(e)/sqrt(128)); the
+//     exponentials are exp2_rep (qd_device.h), a polynomial whose every step a
+//     host implementation can repeat.
+//   * Every floating-point operation is explicit (the library is built with
+//     -ffp-contract=off; fused operations are written as fmaf) and every
+//     reduction has a fixed order, so for a given launch plan the outputs are
+//     a deterministic function of the inputs that the host oracle restates
+//     bit for bit.
+//   * Merges are max-first: the common maximum is found before any
+//     exponential, so the rescaling exponentials are independent of each
+//     other and the sums that follow are plain fmaf / add chains.  The four
+//     groups of a wave merge with lane shuffles, the waves of a workgroup in
+//     LDS.  A split workgroup writes one fp32 partial (m, l, O[128]); the
+//     reference keeps fp16 partials.
+//   * Partials are folded by a second, one-workgroup-per-head kernel.
+//     Cross-workgroup hand-off goes through the kernel boundary: an
+//     agent-scope release inside the kernel lowers to a whole-L2 writeback per
+//     workgroup on gfx950 (buffer_wbl2 sc1, measured ~1 us each and
+//     serialised per XCD), far more than a second launch.
 //   * No MFMA: at q=1 the work is a bandwidth-bound GEMV-like reduction.
 #include "qd_device.h"
 #include "qd_internal.h"
@@ -35,15 +46,14 @@ namespace {
 
 constexpr int kD = 128;
 
+// One lane's share of a row-dot: the 8 fp16 x fp16 products are exact in
+// fp32; they are added as ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)).
 __device__ __forceinline__ float dot8(const f16x8 k, const f16x8 q) {
-  float d = __builtin_amdgcn_fdot2(f16x2{k[0], k[1]}, f16x2{q[0], q[1]}, 0.0f, false);
-  d = __builtin_amdgcn_fdot2(f16x2{k[2], k[3]}, f16x2{q[2], q[3]}, d, false);
-  d = __builtin_amdgcn_fdot2(f16x2{k[4], k[5]}, f16x2{q[4], q[5]}, d, false);
-  d = __builtin_amdgcn_fdot2(f16x2{k[6], k[7]}, f16x2{q[6], q[7]}, d, false);
-  return d;
+  float pr[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) pr[e] = (float)k[e] * (float)q[e];
+  return ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
 }
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Base of a running max that may still be -inf (no rows seen): exp2(x - base)
 // then maps -inf inputs to 0 without producing NaN.
@@ -63,79 +73,118 @@ __device__ __forceinline__ void init_state(GroupState& st) {
   for (int j = 0; j < 8; ++j) st.o[j] = 0.0f;
 }
 
-// Scan rows [0, nrows) of one head.  kbase/vbase are workgroup-uniform (the
-// head's first row of this workgroup); lane t of group g reads the 16 bytes at
-// byte offset row*row_bytes + 16t, a 32-bit offset added to a scalar base
-// (global_load ... saddr form).  Wave `wave` of NW takes blocks of 4U
-// consecutive rows round-robin; row blk + 4u + g goes to group g.  All 2U
-// loads of a block are issued before any of them is consumed.  KV rows are
-// read once, so the loads carry the non-temporal hint: streamed lines do not
-// displace L2 contents (measured ~15% faster per call at L=32768).
+template <int U>
+struct KvTile {
+  f16x8 k[U];
+  f16x8 v[U];
+};
+
+// Issue the loads of the tile starting at row blk: lane t of group g reads the
+// 16 bytes at byte offset r*row_bytes + 16t for rows r = blk + 4u + g, clamped
+// to nrows - 1 (a clamped row is loaded but masked out of the softmax).
+// kbase/vbase are workgroup-uniform, so the loads take the saddr form (scalar
+// base + 32-bit lane offset).  KV rows are read once, so the loads carry the
+// non-temporal hint: streamed lines do not displace L2 contents (measured ~15%
+// faster per call at L=32768).
+template <int U>
+__device__ __forceinline__ void load_tile(KvTile<U>& tl, const char* __restrict__ kbase,
+                                          const char* __restrict__ vbase, unsigned row_bytes,
+                                          int blk, int nrows, int g, int t) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const unsigned r = (unsigned)min(blk + 4 * u + g, nrows - 1);
+    tl.k[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kbase + (r * row_bytes + t * 16u)));
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const unsigned r = (unsigned)min(blk + 4 * u + g, nrows - 1);
+    tl.v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vbase + (r * row_bytes + t * 16u)));
+  }
+}
+
+// Online-softmax update of a group with one tile: scores s_u (rows >= nrows
+// get -inf), tile max mt = max_u s_u (u ascending), mn = max(m, mt),
+// alpha = exp2(m - mn), l = l*alpha, o = o*alpha, then for u ascending
+// p = exp2(s_u - mn), l = l + p, o = fmaf(v_u, p, o).  Every exponent here
+// and in the merges is <= 0, hence exp2_rep_nonpos.
+template <int U>
+__device__ __forceinline__ void consume_tile(GroupState& st, const KvTile<U>& tl, int blk,
+                                             int nrows, int g, const f16x8 qv, float scale_log2) {
+  float s[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const float d = row16_sum(dot8(tl.k[u], qv));
+    s[u] = (blk + 4 * u + g < nrows) ? d * scale_log2 : -__builtin_inff();
+  }
+  float mt = s[0];
+#pragma unroll
+  for (int u = 1; u < U; ++u) mt = fmaxf(mt, s[u]);
+  const float mn = fmaxf(st.m, mt);
+  const float base = safe_base(mn);
+  float p[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) p[u] = exp2_rep_nonpos(s[u] - base);
+  // The rescale is skipped when no group of the wave raised its maximum: alpha
+  // would then be exp2(0) = 1 (or 0 on a state that is still empty and all
+  // zero), so skipping it changes no bit.  The test is wave-uniform.
+  if (__builtin_amdgcn_ballot_w64(mn != st.m)) {
+    const float alpha = exp2_rep_nonpos(st.m - base);
+    st.l *= alpha;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) st.o[j] *= alpha;
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    st.l += p[u];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) st.o[j] = __builtin_fmaf((float)tl.v[u][j], p[u], st.o[j]);
+  }
+  st.m = mn;
+}
+
+// Scan rows [0, nrows) of one head.  Wave `wave` of NW takes the tiles of 4U
+// consecutive rows starting at wave*4U, (wave+NW)*4U, ...; row blk + 4u + g of
+// a tile goes to group g.  All 2U loads of a tile are issued before any of
+// them is consumed.  (Double-buffering the tiles was measured: it was slower
+// at L = 8192-32768, where the launch already streams at the box's read
+// ceiling, by 4-8%.)
 template <int NW, int U>
 __device__ __forceinline__ void scan_rows(GroupState& st, const char* __restrict__ kbase,
                                           const char* __restrict__ vbase, unsigned row_bytes,
                                           int nrows, int wave, int g, int t, const f16x8 qv,
                                           float scale_log2) {
   for (int blk = wave * 4 * U; blk < nrows; blk += NW * 4 * U) {
-    f16x8 kt[U], vt[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const unsigned r = (unsigned)min(blk + 4 * u + g, nrows - 1);
-      kt[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kbase + (r * row_bytes + t * 16u)));
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const unsigned r = (unsigned)min(blk + 4 * u + g, nrows - 1);
-      vt[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vbase + (r * row_bytes + t * 16u)));
-    }
+    KvTile<U> tl;
+    load_tile<U>(tl, kbase, vbase, row_bytes, blk, nrows, g, t);
     // keep the scheduler from sinking loads next to their uses
     __builtin_amdgcn_sched_barrier(0);
-    float s[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float d = row16_sum(dot8(kt[u], qv));
-      s[u] = (blk + 4 * u + g < nrows) ? d * scale_log2 : -__builtin_inff();
-    }
-    float mt = s[0];
-#pragma unroll
-    for (int u = 1; u < U; ++u) mt = fmaxf(mt, s[u]);
-    const float mn = fmaxf(st.m, mt);
-    const float base = safe_base(mn);
-    const float alpha = fast_exp2(st.m - base);
-    st.l *= alpha;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) st.o[j] *= alpha;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float p = fast_exp2(s[u] - base);
-      st.l += p;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) st.o[j] = __builtin_fmaf((float)vt[u][j], p, st.o[j]);
-    }
-    st.m = mn;
+    consume_tile<U>(st, tl, blk, nrows, g, qv, scale_log2);
   }
 }
 
 // Fold the four groups of a wave (lanes t, t+16, t+32, t+48 hold the same
-// dims) with a two-step xor butterfly over lane ^ 16 and lane ^ 32.  Afterwards
-// lanes 0..15 hold the wave's merged state.
+// dims), max-first: M = max of the four m (xor 16, then xor 32), each group
+// scales its l and o by exp2(m - M), and the scaled values are summed as
+// (g0 + g1) + (g2 + g3) with xor-16 then xor-32 shuffles.  Afterwards every
+// lane holds the wave's state for its dims.
 __device__ __forceinline__ void wave_merge(GroupState& st) {
+  float M = fmaxf(st.m, __shfl_xor(st.m, 16));
+  M = fmaxf(M, __shfl_xor(M, 32));
+  const float sc = exp2_rep_nonpos(st.m - safe_base(M));
+  float l = st.l * sc;
+  float o[8];
 #pragma unroll
-  for (int mask = 16; mask <= 32; mask <<= 1) {
-    const float om = __shfl_xor(st.m, mask);
-    const float ol = __shfl_xor(st.l, mask);
-    float oo[8];
+  for (int j = 0; j < 8; ++j) o[j] = st.o[j] * sc;
+  l += __shfl_xor(l, 16);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) oo[j] = __shfl_xor(st.o[j], mask);
-    const float mn = fmaxf(st.m, om);
-    const float base = safe_base(mn);
-    const float a = fast_exp2(st.m - base);
-    const float b = fast_exp2(om - base);
-    st.l = st.l * a + ol * b;
+  for (int j = 0; j < 8; ++j) o[j] += __shfl_xor(o[j], 16);
+  l += __shfl_xor(l, 32);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) st.o[j] = st.o[j] * a + oo[j] * b;
-    st.m = mn;
-  }
+  for (int j = 0; j < 8; ++j) o[j] += __shfl_xor(o[j], 32);
+  st.m = M;
+  st.l = l;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) st.o[j] = o[j];
 }
 
 // Scan kernel.  Workgroup (split c, head h) with blockIdx.x = c * num_heads + h
@@ -153,7 +202,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
   __shared__ float sl[NW];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
   const int g = lane >> 4;
   const int t = lane & 15;
   const int h = blockIdx.x % p.num_heads;
@@ -186,7 +235,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
     float L = 0.0f, O = 0.0f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float wt = fast_exp2(sm[w] - base);
+      const float wt = exp2_rep_nonpos(sm[w] - base);
       L = __builtin_fmaf(wt, sl[w], L);
       O = __builtin_fmaf(wt, so[w][tid], O);
     }
@@ -195,16 +244,19 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
       p.part_o[slot * kD + tid] = O;
       if (tid == 0) p.part_ml[slot] = float2{M, L};
     } else {
-      reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = (_Float16)(O / L);
+      reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = (_Float16)__fdiv_rn(O, L);
     }
   }
 }
 
 // Stage 2: one workgroup per head folds the head's p.splits partials with the
 // log-sum-exp rule (fd_opt_stage2_kernel's role) and writes the fp16 output.
-// Thread (dq = tid % 32 -> dims 4dq..4dq+3, slice = tid / 32) folds splits
-// slice, slice + P, ... with its own running max, issuing eight splits' loads
-// at a time; the P slices are then folded in LDS.  The kernel boundary after
+// Max-first: thread (dq = tid % 32 -> dims 4dq..4dq+3, slice = tid / 32)
+// takes splits slice, slice + P, ...; the slices' maxima meet in LDS, so all
+// threads share the head's maximum M before any exponential.  Each thread
+// then sums w_c * l_c and w_c * O_c (w_c = exp2(m_c - M)) over its splits in
+// ascending order with fmaf, issuing B splits' loads at a time, and the P
+// slice sums are added in LDS (slice order).  The kernel boundary after
 // stage 1 makes every partial visible on every XCD.
 template <int NT>
 __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p) {
@@ -219,52 +271,59 @@ __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p
   const int slice = tid >> 5;
   const float* po = p.part_o + (long long)h * p.splits * kD + dq * 4;
   const float2* pml = p.part_ml + (long long)h * p.splits;
-  float mm = -__builtin_inff(), ll = 0.0f;
+  // First batch of this thread's splits (slice, slice + P, ..., B of them),
+  // loaded before the maximum is known so one memory round trip serves both.
+  float2 ml[B];
+  f32x4 ov[B];
+#pragma unroll
+  for (int j = 0; j < B; ++j) {
+    const int cc = min(slice + j * P, p.splits - 1);
+    ml[j] = pml[cc];
+    ov[j] = *reinterpret_cast<const f32x4*>(po + (long long)cc * kD);
+  }
+  float mm = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < B; ++j)
+    if (slice + j * P < p.splits) mm = fmaxf(mm, ml[j].x);
+  for (int c = slice + B * P; c < p.splits; c += P) mm = fmaxf(mm, pml[c].x);
+  if (dq == 0) sm[slice] = mm;
+  __syncthreads();
+  float M = sm[0];
+#pragma unroll
+  for (int s = 1; s < P; ++s) M = fmaxf(M, sm[s]);
+  const float base = safe_base(M);
+  float ll = 0.0f;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c0 = slice; c0 < p.splits; c0 += B * P) {
-    float2 ml[B];
-    f32x4 ov[B];
+  for (int c0 = slice;;) {
 #pragma unroll
     for (int j = 0; j < B; ++j) {
-      const int cc = c0 + j * P;
-      if (cc < p.splits) {
-        ml[j] = pml[cc];
-        ov[j] = *reinterpret_cast<const f32x4*>(po + (long long)cc * kD);
-      } else {
-        ml[j] = float2{-__builtin_inff(), 0.0f};
-        ov[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (c0 + j * P < p.splits) {
+        const float w = exp2_rep_nonpos(ml[j].x - base);
+        ll = __builtin_fmaf(w, ml[j].y, ll);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(w, ov[j][e], acc[e]);
       }
     }
+    c0 += B * P;
+    if (c0 >= p.splits) break;
 #pragma unroll
     for (int j = 0; j < B; ++j) {
-      const float mn = fmaxf(mm, ml[j].x);
-      const float base = safe_base(mn);
-      const float a = fast_exp2(mm - base);
-      const float b = fast_exp2(ml[j].x - base);
-      ll = ll * a + ml[j].y * b;
-      acc = acc * a + ov[j] * b;
-      mm = mn;
+      const int cc = min(c0 + j * P, p.splits - 1);
+      ml[j] = pml[cc];
+      ov[j] = *reinterpret_cast<const f32x4*>(po + (long long)cc * kD);
     }
   }
   *reinterpret_cast<f32x4*>(&so[slice][dq * 4]) = acc;
-  if (dq == 0) {
-    sm[slice] = mm;
-    sl[slice] = ll;
-  }
+  if (dq == 0) sl[slice] = ll;
   __syncthreads();
   if (tid < kD) {
-    float M = -__builtin_inff();
+    float L = sl[0], O = so[0][tid];
 #pragma unroll
-    for (int s = 0; s < P; ++s) M = fmaxf(M, sm[s]);
-    const float base = safe_base(M);
-    float L = 0.0f, O = 0.0f;
-#pragma unroll
-    for (int s = 0; s < P; ++s) {
-      const float w = fast_exp2(sm[s] - base);
-      L = __builtin_fmaf(w, sl[s], L);
-      O = __builtin_fmaf(w, so[s][tid], O);
+    for (int s = 1; s < P; ++s) {
+      L += sl[s];
+      O += so[s][tid];
     }
-    reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = (_Float16)(O / L);
+    reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = (_Float16)__fdiv_rn(O, L);
   }
 }
 
@@ -273,9 +332,6 @@ __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p
 template <int NW, bool kSplit>
 static void launch_scan(const AttnParams& p, int rows_per_tile, dim3 grid, hipStream_t stream) {
   switch (rows_per_tile) {
-    case 8:
-      hipLaunchKernelGGL((decode_attention_scan_kernel<NW, 8, kSplit>), grid, dim3(NW * 64), 0, stream, p);
-      break;
     case 4:
       hipLaunchKernelGGL((decode_attention_scan_kernel<NW, 4, kSplit>), grid, dim3(NW * 64), 0, stream, p);
       break;

@@ -291,6 +291,25 @@ int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* n
   return QD_OK;
 }
 
+int qd_decode_attention_plan_detail(const qd_ctx* ctx, int seqlen, int entry, int num_splits,
+                                    qd_attn_plan* plan) {
+  if (!ctx || !plan) return fail(QD_EINVAL, "NULL argument");
+  if (seqlen < 1 || seqlen > ctx->cfg.max_seqlen)
+    return fail(QD_EINVAL, "seqlen %d outside [1, %d]", seqlen, ctx->cfg.max_seqlen);
+  if (entry < 0 || entry > 2) return fail(QD_EINVAL, "entry %d is not 0, 1 or 2", entry);
+  if (entry == 2 && num_splits > qd::kMaxSplits)
+    return fail(QD_EINVAL, "num_splits %d above the maximum %d", num_splits, qd::kMaxSplits);
+  const qd::AttnPlan p = entry == 0   ? plan_auto(ctx, seqlen)
+                         : entry == 1 ? plan_fused(seqlen)
+                                      : plan_split(ctx, seqlen, num_splits);
+  plan->variant = p.variant;
+  plan->num_splits = p.splits;
+  plan->rows_per_split = p.rows_per_split;
+  plan->rows_per_tile = p.rows_per_tile;
+  plan->waves = p.waves;
+  return QD_OK;
+}
+
 int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
                         const uint16_t* v_layer, uint16_t* out, int seqlen, int num_heads,
                         int head_dim, hipStream_t stream) {

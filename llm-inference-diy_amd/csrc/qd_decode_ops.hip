@@ -45,7 +45,7 @@ __device__ __forceinline__ void load_input(const QkvFrontParams& p, int lane, f1
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float v = (float)xv[j][e];
-      acc += v * v;
+      acc = __builtin_fmaf(v, v, acc);   // exact square: rounds only the sum
     }
   const float var = wave64_sum(acc) / (float)hidden;
   const float r = __fdiv_rn(1.0f, __fsqrt_rn(var + p.eps));
@@ -69,7 +69,8 @@ __device__ __forceinline__ float row_dot(const uint16_t* __restrict__ w_row, int
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (float)wv[j][e] * (float)xv[j][e];   // exact products
+    for (int e = 0; e < 8; ++e)   // exact product: the fmaf rounds only the sum
+      acc = __builtin_fmaf((float)wv[j][e], (float)xv[j][e], acc);
   return wave64_sum(acc);
 }
 

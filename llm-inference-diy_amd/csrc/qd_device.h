@@ -42,4 +42,52 @@ __device__ __forceinline__ float wave64_sum(float x) {
   return x;
 }
 
+// 2^x, reproducible bit for bit by a host implementation of the same steps
+// (all library code is built with -ffp-contract=off, so each operation below
+// rounds exactly once):
+//   n = rint(x) (ties to even), f = x - n (exact, |f| <= 1/2),
+//   2^f ~= 1 + f*q(f), q(f) = c1 + c2 f + ... + c6 f^5 evaluated in Estrin
+//   form: (c1 + c2 f) + f^2 ((c3 + c4 f) + f^2 (c5 + c6 f)), each bracket an
+//   fmaf, then one fmaf for 1 + f*q;
+//   result = ldexp(2^f, n).
+// Dependency depth is 4 fmaf after f (Horner would be 6); the kernels that
+// call it run one wave per SIMD, so latency is what matters.  The
+// coefficients were fitted to 2^f on [-1/2, 1/2] by iteratively reweighted
+// least squares on 4000 Chebyshev nodes and rounded to fp32; this evaluation
+// is within 1.25 ulp of 2^f there (1.17 the largest error seen in 2e7
+// samples).  exp2_rep(0) == 1 exactly.  Inputs <= -125
+// and NaN give 0 (so no result is subnormal); inputs >= 128 give +inf.
+//
+// Branch-free: the polynomial runs on x clamped to [-126, 128] (v_med3_f32;
+// a NaN clamps to -126) and the out-of-range results are selected at the end,
+// so a wave never splits on it.  In range the clamp leaves x unchanged.
+__device__ __forceinline__ float exp2_rep(float x) {
+  const float xc = __builtin_amdgcn_fmed3f(x, -126.0f, 128.0f);
+  const float n = __builtin_rintf(xc);
+  const float f = xc - n;
+  const float f2 = f * f;
+  const float a = __builtin_fmaf(0x1.ebfbdcp-3f, f, 0x1.62e430p-1f);
+  const float b = __builtin_fmaf(0x1.3b2d4ep-7f, f, 0x1.c6aee8p-5f);
+  const float c = __builtin_fmaf(0x1.41fbb0p-13f, f, 0x1.5f3e54p-10f);
+  const float q = __builtin_fmaf(__builtin_fmaf(c, f2, b), f2, a);
+  const float r = __builtin_ldexpf(__builtin_fmaf(q, f, 1.0f), (int)n);
+  return x >= 128.0f ? __builtin_inff() : (x > -125.0f ? r : 0.0f);
+}
+
+// exp2_rep for arguments known to be <= 0 (or -inf / NaN), as every softmax
+// exponent is: the same operations on the same clamped value, so the result is
+// bit-identical to exp2_rep(x), without the overflow select.
+__device__ __forceinline__ float exp2_rep_nonpos(float x) {
+  const float xc = fmaxf(x, -126.0f);
+  const float n = __builtin_rintf(xc);
+  const float f = xc - n;
+  const float f2 = f * f;
+  const float a = __builtin_fmaf(0x1.ebfbdcp-3f, f, 0x1.62e430p-1f);
+  const float b = __builtin_fmaf(0x1.3b2d4ep-7f, f, 0x1.c6aee8p-5f);
+  const float c = __builtin_fmaf(0x1.41fbb0p-13f, f, 0x1.5f3e54p-10f);
+  const float q = __builtin_fmaf(__builtin_fmaf(c, f2, b), f2, a);
+  const float r = __builtin_ldexpf(__builtin_fmaf(q, f, 1.0f), (int)n);
+  return x > -125.0f ? r : 0.0f;
+}
+
 }  // namespace qd

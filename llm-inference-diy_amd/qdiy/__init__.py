@@ -27,6 +27,7 @@ EXPORTS = (
     "qd_ctx_create", "qd_ctx_destroy", "qd_qkv_bias_rope_cache", "qd_qkv_proj_rope_cache",
     "qd_decode_attention",
     "qd_decode_attention_fused", "qd_decode_attention_split", "qd_decode_attention_plan",
+    "qd_decode_attention_plan_detail",
     "qd_max_splits", "qd_last_error", "qd_version",
 )
 
@@ -41,6 +42,16 @@ class Cfg(ctypes.Structure):
     _fields_ = [("num_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
                 ("max_seqlen", ctypes.c_int), ("kv_row_stride", ctypes.c_longlong),
                 ("kv_head_stride", ctypes.c_longlong), ("rope_base", ctypes.c_float)]
+
+
+class AttnPlan(ctypes.Structure):
+    """qd_attn_plan: the complete launch plan of one decode-attention call."""
+    _fields_ = [("variant", ctypes.c_int), ("num_splits", ctypes.c_int),
+                ("rows_per_split", ctypes.c_int), ("rows_per_tile", ctypes.c_int),
+                ("waves", ctypes.c_int)]
+
+    def as_tuple(self):
+        return (self.variant, self.num_splits, self.rows_per_split, self.rows_per_tile, self.waves)
 
 
 _lib = None
@@ -64,6 +75,7 @@ def load() -> ctypes.CDLL:
     L.qd_decode_attention_fused.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     L.qd_decode_attention_split.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
     L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
+    L.qd_decode_attention_plan_detail.argtypes = [vp, i, i, i, ctypes.POINTER(AttnPlan)]
     L.qd_last_error.restype = ctypes.c_char_p
     L.qd_version.restype = ctypes.c_char_p
     _lib = L
@@ -138,6 +150,14 @@ class Context:
         v, s = ctypes.c_int(), ctypes.c_int()
         _check(load().qd_decode_attention_plan(self._h, seqlen, ctypes.byref(v), ctypes.byref(s)))
         return ("fused" if v.value == FUSED else "split"), s.value
+
+    def plan_detail(self, seqlen: int, variant: str = "auto", num_splits: int = 0) -> AttnPlan:
+        """The complete launch plan decode_attention(variant=...) uses at seqlen."""
+        entry = {"auto": 0, "fused": 1, "split": 2}[variant]
+        plan = AttnPlan()
+        _check(load().qd_decode_attention_plan_detail(self._h, seqlen, entry, num_splits,
+                                                      ctypes.byref(plan)))
+        return plan
 
     def decode_attention(self, q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
                          out: torch.Tensor, seqlen: int, variant: str = "auto", num_splits: int = 0,

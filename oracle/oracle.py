@@ -20,6 +20,17 @@ ENGINE, FUSED, SPLIT = 0, 1, 2
 _lib = None
 
 
+class Plan(ctypes.Structure):
+    """qd_oracle_plan: the launch plan of one decode-attention call."""
+    _fields_ = [("variant", ctypes.c_int), ("num_splits", ctypes.c_int),
+                ("rows_per_split", ctypes.c_int), ("rows_per_tile", ctypes.c_int),
+                ("waves", ctypes.c_int)]
+
+    def __repr__(self):
+        return (f"Plan(variant={self.variant}, num_splits={self.num_splits}, rows_per_split="
+                f"{self.rows_per_split}, rows_per_tile={self.rows_per_tile}, waves={self.waves})")
+
+
 def build() -> None:
     """Compile the oracle with its Makefile (gcc, -ffp-contract=off)."""
     subprocess.run(["make", "-s", "-B", "-C", HERE], check=True)
@@ -59,6 +70,11 @@ def lib() -> ctypes.CDLL:
                                           u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ll, ll,
                                           ctypes.c_float, ctypes.c_int]
         L.qd_oracle_qkv_front.restype = ctypes.c_int
+        L.qd_oracle_exp2_array.argtypes = [f32p, f32p, ll]
+        L.qd_oracle_attention_planned.argtypes = [u16p, u16p, u16p, u16p, ctypes.c_int,
+                                                  ctypes.c_int, ll, ll,
+                                                  ctypes.POINTER(Plan), ctypes.c_int]
+        L.qd_oracle_attention_planned.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -182,3 +198,37 @@ def qkv_front(x, norm_w, w_qkv, bias, qkv_out, k_cache, v_cache, pos, num_heads,
                                    head_dim, row_stride, head_stride, rope_base, order)
     if rc != 0:
         raise ValueError("qd_oracle_qkv_front rejected its arguments")
+
+
+def exp2(x) -> np.ndarray:
+    """exp2_rep of the gfx950 kernels, elementwise on float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().qd_oracle_exp2_array(_f32(x), _f32(out), x.size)
+    return out
+
+
+def fused_plan(seqlen, rows_per_tile=4, waves=16) -> Plan:
+    return Plan(0, 1, seqlen, rows_per_tile, waves)
+
+
+def split_plan(seqlen, num_splits, rows_per_tile=None, waves=4) -> Plan:
+    """A split plan laid out as the library's planner lays one out for an
+    explicit split count: rows per split rounded up to a multiple of 4."""
+    rows = -(-seqlen // num_splits)
+    rows = (rows + 3) & ~3
+    if rows_per_tile is None:
+        rows_per_tile = 4 if rows >= 64 else 2
+    return Plan(1, -(-seqlen // rows), rows, rows_per_tile, waves)
+
+
+def attention_planned(q, k, v, seqlen, num_heads, row_stride, head_stride, plan, nthreads=1):
+    """The gfx950 kernels' arithmetic for all heads under `plan`; out [H,128]."""
+    q = np.ascontiguousarray(q, dtype=np.float16)
+    out = np.zeros((num_heads, 128), np.float16)
+    rc = lib().qd_oracle_attention_planned(_u16(q), _u16(k), _u16(v), _u16(out), seqlen,
+                                           num_heads, row_stride, head_stride,
+                                           ctypes.byref(plan), nthreads)
+    if rc != 0:
+        raise ValueError(f"qd_oracle_attention_planned rejected its arguments ({plan})")
+    return out

@@ -424,7 +424,7 @@ static void wave64_lane_sums(int n, const float* v, float* lanes) {
     for (int j = 0; j < chunks; ++j)
       for (int e = 0; e < 8; ++e) {
         int k = 512 * j + 8 * l + e;
-        acc += (k < n) ? v[k] : 0.0f;
+        if (k < n) acc += v[k];
       }
     lanes[l] = acc;
   }
@@ -506,4 +506,245 @@ int qd_oracle_qkv_front(const uint16_t* x, const uint16_t* norm_w, float eps,
   free(xn);
   return qd_oracle_qkv_bias_rope_cache(qkv_out, bias, k_cache, v_cache, pos, num_heads, head_dim,
                                        row_stride, head_stride, rope_base);
+}
+
+/* ------------------------------------------------------------------------ */
+/* The gfx950 kernels' own arithmetic: exp2 and decode attention             */
+/* ------------------------------------------------------------------------ */
+
+/* exp2_rep of llm-inference-diy_amd/csrc/qd_device.h, step for step. */
+float qd_oracle_exp2(float x) {
+  if (!(x > -125.0f)) return 0.0f;
+  if (x >= 128.0f) return INFINITY;
+  const float n = rintf(x);
+  const float f = x - n;
+  const float f2 = f * f;
+  const float a = fmaf(0x1.ebfbdcp-3f, f, 0x1.62e430p-1f);
+  const float b = fmaf(0x1.3b2d4ep-7f, f, 0x1.c6aee8p-5f);
+  const float c = fmaf(0x1.41fbb0p-13f, f, 0x1.5f3e54p-10f);
+  const float q = fmaf(fmaf(c, f2, b), f2, a);
+  return ldexpf(fmaf(q, f, 1.0f), (int)n);
+}
+
+void qd_oracle_exp2_array(const float* x, float* out, long long n) {
+  for (long long i = 0; i < n; ++i) out[i] = qd_oracle_exp2(x[i]);
+}
+
+static float safe_base(float m) { return m == -INFINITY ? 0.0f : m; }
+
+/* Online-softmax state of one 16-lane group; lane t owns dims 8t..8t+7. */
+typedef struct {
+  float m, l;
+  float o[QD_D];
+} gstate;
+
+static void gstate_init(gstate* st) {
+  st->m = -INFINITY;
+  st->l = 0.0f;
+  for (int d = 0; d < QD_D; ++d) st->o[d] = 0.0f;
+}
+
+/* wave_merge, max-first: M = max of the four groups' m, each group scaled by
+ * exp2(m - M), summed as (g0 + g1) + (g2 + g3).  Result in g[0]. */
+static void wave_merge4(gstate* g) {
+  float M = fmaxf(fmaxf(g[0].m, g[1].m), fmaxf(g[2].m, g[3].m));
+  const float base = safe_base(M);
+  float sc[4];
+  for (int i = 0; i < 4; ++i) sc[i] = qd_oracle_exp2(g[i].m - base);
+  float l[4];
+  for (int i = 0; i < 4; ++i) l[i] = g[i].l * sc[i];
+  g[0].l = (l[0] + l[1]) + (l[2] + l[3]);
+  for (int d = 0; d < QD_D; ++d) {
+    float o[4];
+    for (int i = 0; i < 4; ++i) o[i] = g[i].o[d] * sc[i];
+    g[0].o[d] = (o[0] + o[1]) + (o[2] + o[3]);
+  }
+  g[0].m = M;
+}
+
+/* The score of one row for one 16-lane group: lane t adds its 8 exact
+ * products as ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)), then the 16-lane tree of
+ * row16_sum. */
+static float group_score(const float* qf, const uint16_t* krow) {
+  float lanes[16];
+  for (int t = 0; t < 16; ++t) {
+    float pr[8];
+    for (int e = 0; e < 8; ++e) pr[e] = qd_oracle_h2f(krow[8 * t + e]) * qf[8 * t + e];   /* exact */
+    lanes[t] = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+  }
+  float q4[4];
+  for (int i = 0; i < 4; ++i) q4[i] = (lanes[4 * i] + lanes[4 * i + 1]) + (lanes[4 * i + 2] + lanes[4 * i + 3]);
+  return (q4[0] + q4[1]) + (q4[2] + q4[3]);
+}
+
+static float gfx_scale_log2(void) { return (float)(1.4426950408889634 / sqrt(128.0)); }
+
+/* One workgroup of decode_attention_scan_kernel<NW, U, *>: rows [0, nrows) at
+ * k/v + r*row_stride.  Returns the LDS fold (M, L, O[128]). */
+static void scan_workgroup(const float* qf, const uint16_t* k, const uint16_t* v,
+                           long long row_stride, int nrows, int nw, int u_rows,
+                           float* M_out, float* L_out, float* O_out) {
+  const float scale = gfx_scale_log2();
+  gstate* st = (gstate*)malloc(sizeof(gstate) * (size_t)nw * 4);
+  float* s = (float*)malloc(sizeof(float) * (size_t)u_rows);
+  int* rr = (int*)malloc(sizeof(int) * (size_t)u_rows);
+  for (int i = 0; i < nw * 4; ++i) gstate_init(&st[i]);
+  for (int w = 0; w < nw; ++w) {
+    for (int blk = w * 4 * u_rows; blk < nrows; blk += nw * 4 * u_rows) {
+      for (int g = 0; g < 4; ++g) {
+        gstate* x = &st[w * 4 + g];
+        for (int u = 0; u < u_rows; ++u) {
+          const int row = blk + 4 * u + g;
+          rr[u] = row < nrows - 1 ? row : nrows - 1;       /* clamped load row */
+          const float d = group_score(qf, k + (long long)rr[u] * row_stride);
+          s[u] = row < nrows ? d * scale : -INFINITY;
+        }
+        float mt = s[0];
+        for (int u = 1; u < u_rows; ++u) mt = fmaxf(mt, s[u]);
+        const float mn = fmaxf(x->m, mt);
+        const float base = safe_base(mn);
+        const float alpha = qd_oracle_exp2(x->m - base);   /* consume_tile */
+        x->l *= alpha;
+        for (int d = 0; d < QD_D; ++d) x->o[d] *= alpha;
+        for (int u = 0; u < u_rows; ++u) {
+          const float p = qd_oracle_exp2(s[u] - base);
+          x->l += p;
+          const uint16_t* vrow = v + (long long)rr[u] * row_stride;
+          for (int d = 0; d < QD_D; ++d) x->o[d] = fmaf(qd_oracle_h2f(vrow[d]), p, x->o[d]);
+        }
+        x->m = mn;
+      }
+    }
+  }
+  for (int w = 0; w < nw; ++w) wave_merge4(&st[w * 4]);
+  /* LDS fold by threads 0..127, one dim each */
+  float M = -INFINITY;
+  for (int w = 0; w < nw; ++w) M = fmaxf(M, st[w * 4].m);
+  const float base = safe_base(M);
+  float L = 0.0f;
+  for (int d = 0; d < QD_D; ++d) O_out[d] = 0.0f;
+  for (int w = 0; w < nw; ++w) {
+    const float wt = qd_oracle_exp2(st[w * 4].m - base);
+    L = fmaf(wt, st[w * 4].l, L);
+    for (int d = 0; d < QD_D; ++d) O_out[d] = fmaf(wt, st[w * 4].o[d], O_out[d]);
+  }
+  *M_out = M;
+  *L_out = L;
+  free(rr);
+  free(s);
+  free(st);
+}
+
+/* decode_attention_merge_kernel<256> for one head, max-first: M = max of all
+ * splits' m; slice s (of 8) sums w_c*l_c and w_c*O_c, w_c = exp2(m_c - M),
+ * over splits c = s, s+8, ... in ascending order with fmaf; the slice sums
+ * are added in slice order; out = half(O / L). */
+static void merge_head(const float* part_o, const float* part_m, const float* part_l,
+                       int splits, uint16_t* out) {
+  enum { P = 8 };
+  float M = -INFINITY;
+  for (int s = 0; s < P; ++s) {
+    float mm = -INFINITY;
+    for (int c = s; c < splits; c += P) mm = fmaxf(mm, part_m[c]);
+    M = s == 0 ? mm : fmaxf(M, mm);
+  }
+  const float base = safe_base(M);
+  float sl[P];
+  static __thread float so[P][QD_D];
+  for (int s = 0; s < P; ++s) {
+    float ll = 0.0f;
+    for (int d = 0; d < QD_D; ++d) so[s][d] = 0.0f;
+    for (int c = s; c < splits; c += P) {
+      const float w = qd_oracle_exp2(part_m[c] - base);
+      ll = fmaf(w, part_l[c], ll);
+      for (int d = 0; d < QD_D; ++d) so[s][d] = fmaf(w, part_o[(long long)c * QD_D + d], so[s][d]);
+    }
+    sl[s] = ll;
+  }
+  for (int d = 0; d < QD_D; ++d) {
+    float L = sl[0], O = so[0][d];
+    for (int s = 1; s < P; ++s) {
+      L += sl[s];
+      O += so[s][d];
+    }
+    out[d] = qd_oracle_f2h(O / L);
+  }
+}
+
+typedef struct {
+  const uint16_t *q, *k, *v;
+  uint16_t* out;
+  int seqlen, num_heads;
+  long long row_stride, head_stride;
+  qd_oracle_plan plan;
+  int next;
+} gfx_job;
+
+static void gfx_head(gfx_job* j, int h) {
+  float qf[QD_D];
+  for (int d = 0; d < QD_D; ++d) qf[d] = qd_oracle_h2f(j->q[(long long)h * QD_D + d]);
+  const uint16_t* kh = j->k + (long long)h * j->head_stride;
+  const uint16_t* vh = j->v + (long long)h * j->head_stride;
+  uint16_t* oh = j->out + (long long)h * QD_D;
+  const qd_oracle_plan* pl = &j->plan;
+  if (pl->variant == 0) {
+    float M, L, O[QD_D];
+    scan_workgroup(qf, kh, vh, j->row_stride, j->seqlen, pl->waves, pl->rows_per_tile, &M, &L, O);
+    for (int d = 0; d < QD_D; ++d) oh[d] = qd_oracle_f2h(O[d] / L);
+    return;
+  }
+  const int S = pl->num_splits;
+  float* po = (float*)malloc(sizeof(float) * (size_t)S * QD_D);
+  float* pm = (float*)malloc(sizeof(float) * (size_t)S);
+  float* plv = (float*)malloc(sizeof(float) * (size_t)S);
+  for (int c = 0; c < S; ++c) {
+    const int r0 = c * pl->rows_per_split;
+    int nrows = j->seqlen - r0;
+    if (nrows > pl->rows_per_split) nrows = pl->rows_per_split;
+    scan_workgroup(qf, kh + (long long)r0 * j->row_stride, vh + (long long)r0 * j->row_stride,
+                   j->row_stride, nrows, pl->waves, pl->rows_per_tile, &pm[c], &plv[c],
+                   po + (long long)c * QD_D);
+  }
+  merge_head(po, pm, plv, S, oh);
+  free(plv);
+  free(pm);
+  free(po);
+}
+
+static void* gfx_worker(void* arg) {
+  gfx_job* j = (gfx_job*)arg;
+  for (;;) {
+    int h = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
+    if (h >= j->num_heads) break;
+    gfx_head(j, h);
+  }
+  return NULL;
+}
+
+int qd_oracle_attention_planned(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                uint16_t* out, int seqlen, int num_heads, long long row_stride,
+                                long long head_stride, const qd_oracle_plan* plan, int nthreads) {
+  if (!q || !k || !v || !out || !plan || seqlen < 1 || num_heads < 1) return -1;
+  if (plan->rows_per_tile < 1 || plan->waves < 1) return -1;
+  if (plan->variant != 0) {
+    if (plan->num_splits < 1 || plan->rows_per_split < 1) return -1;
+    /* every split workgroup has rows, and together they cover [0, seqlen) */
+    if ((long long)(plan->num_splits - 1) * plan->rows_per_split >= seqlen) return -1;
+    if ((long long)plan->num_splits * plan->rows_per_split < seqlen) return -1;
+  }
+  gfx_job j = {q, k, v, out, seqlen, num_heads, row_stride, head_stride, *plan, 0};
+  if (nthreads > num_heads) nthreads = num_heads;
+  if (nthreads <= 1) {
+    gfx_worker(&j);
+    return 0;
+  }
+  pthread_t th[256];
+  if (nthreads > 256) nthreads = 256;
+  int started = 0;
+  for (int i = 0; i < nthreads; ++i)
+    if (pthread_create(&th[i], NULL, gfx_worker, &j) == 0) started++;
+    else break;
+  if (started == 0) gfx_worker(&j);
+  for (int i = 0; i < started; ++i) pthread_join(th[i], NULL);
+  return 0;
 }

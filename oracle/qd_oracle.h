@@ -121,6 +121,38 @@ int qd_oracle_qkv_front(const uint16_t* x, const uint16_t* norm_w, float eps,
                         int head_dim, long long row_stride, long long head_stride,
                         float rope_base, int order);
 
+/* ---- the gfx950 kernels' own arithmetic (llm-inference-diy_amd/csrc) ----
+ * These restate this build's kernels step for step, so the GPU results can be
+ * compared bit for bit.  They are pinned independently (float64, the
+ * reference-order functions above, closed forms) by tests/test_oracle_gfx.py. */
+
+/* exp2_rep (qd_device.h): n = rint(x), f = x - n, 2^f = 1 + f*q(f) with q
+ * in Estrin form (c1 + c2 f) + f^2((c3 + c4 f) + f^2 (c5 + c6 f)), every
+ * bracket and the final 1 + f*q one fmaf, ldexp by n; 0 for x <= -125 or
+ * NaN, +inf for x >= 128. */
+float qd_oracle_exp2(float x);
+void qd_oracle_exp2_array(const float* x, float* out, long long n);
+
+/* A decode-attention launch plan (qd_attn_plan of include/qdiy/attn.h). */
+typedef struct {
+  int variant;        /* 0: one workgroup per head (fused), 1: split + merge */
+  int num_splits;     /* split workgroups per head */
+  int rows_per_split; /* KV rows per split workgroup */
+  int rows_per_tile;  /* rows each 16-lane group takes per tile (template U) */
+  int waves;          /* wavefronts per scan workgroup */
+} qd_oracle_plan;
+
+/* decode_attention_scan_kernel (+ decode_attention_merge_kernel for split
+ * plans) of qd_attention.hip for all heads under `plan`: scores by 8-term
+ * fmaf chains per lane and the 16-lane tree, exp2 by qd_oracle_exp2, the
+ * tile-wise online softmax, the lane-shuffle and LDS folds, and the 8-slice
+ * merge.  Same argument meaning as qd_oracle_decode_attention.  Returns 0, or
+ * -1 on invalid arguments (including a split plan that does not cover
+ * [0, seqlen) with non-empty workgroups). */
+int qd_oracle_attention_planned(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                uint16_t* out, int seqlen, int num_heads, long long row_stride,
+                                long long head_stride, const qd_oracle_plan* plan, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,10 +1,15 @@
 """GPU parity of decode attention (C ABI -> HIP kernels) against the CPU oracle.
 
-Bars: max abs error <= 2e-3 against the oracle's restatement of the
-reference kernels (flash_decode_q1_opt.cuh), and -- stronger -- within half a
-binary16 ulp (+1e-5) of float64 attention, since the kernels keep every
-intermediate in fp32 and round once.  Closed forms (L=1, constant inputs) are
-bit-exact.  Configs 1-3 of the benchmark run at full size.
+Bars, on every call:
+  * bit-exact against the oracle's restatement of this build's kernels
+    (oracle.attention_planned) under the plan the library reports for the call
+    (qd_decode_attention_plan_detail);
+  * max abs error <= 2e-3 against the oracle's restatement of the reference
+    kernels (flash_decode_q1_opt.cuh);
+  * within half a binary16 ulp (+1e-5) of float64 attention, since the
+    kernels keep every intermediate in fp32 and round once.
+Closed forms (L=1, constant inputs) are bit-exact.  Configs 1-3 of the
+benchmark run at full size.
 """
 import numpy as np
 import pytest
@@ -44,7 +49,16 @@ class GpuCase:
         torch.cuda.synchronize()
         o = out.cpu().numpy()
         assert np.all(o[H * 128:] == np.float16(7.0)), "write past the end of out"
-        return o[:H * 128].reshape(H, 128)
+        o = o[:H * 128].reshape(H, 128)
+        L = seqlen or self.case.L
+        plan = self.ctx.plan_detail(L, variant, num_splits)
+        want = oracle.attention_planned(self.case.q, self.case.kc, self.case.vc, L, H,
+                                        self.case.row_stride, self.case.head_stride,
+                                        oracle.Plan(*plan.as_tuple()), nthreads=8)
+        same = o.view(np.uint16) == want.view(np.uint16)
+        assert same.all(), (f"{np.count_nonzero(~same)} outputs differ from the kernel-order "
+                            f"oracle under {plan.as_tuple()}")
+        return o
 
     def close(self):
         self.ctx.close()
@@ -173,6 +187,7 @@ def test_head_independence(qdiy):
     a = g.run()
     kc = g.kc.view(1500, 16, 128)
     kc[:, 5] = -kc[:, 5]
+    case.kc = g.kc.cpu().numpy()          # the oracle check in run() sees the same cache
     b = g.run()
     keep = [h for h in range(16) if h != 5]
     assert np.array_equal(a[keep].view(np.uint16), b[keep].view(np.uint16))
