@@ -17,7 +17,12 @@ The CPU baseline is the repository's C restatement of the reference kernels
 (oracle/) on the host cores of the same box, on a bounded sample of the same
 workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Also measured and reported under `config`: config 4 (the fused QKV front end
+followed by attention at L=2048) and config 5 (greedy decode of a random-init
+Qwen-1.8B-shaped model through the engine: tokens/s and an estimate of the
+attention share of a decode step).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
 """
 from __future__ import annotations
 
@@ -178,6 +183,61 @@ def measure_front(lib, steps: int, warmup: int):
             "front_end_gbps": round(front_bytes / us_front / 1e3, 1)}
 
 
+def measure_e2e(lib, seed: int = 5, n_prompt: int = 128, n_new: int = 256):
+    """Config 5: random-init Qwen-1.8B (24 layers, hidden 2048, 16 heads, FFN
+    5504, vocab 151936; weights ~N(0, 0.02) by the library's generator, norm
+    weights 1) in the .bin format, a prompt of n_prompt uniform-random ids, then
+    n_new greedy tokens through qdiy.Engine (one synchronising step per token,
+    as the reference engine).  Decode tokens/s is timed over the n_new steps;
+    the prompt runs through the decode path first and is timed separately."""
+    import numpy as np
+
+    import qdiy
+
+    cfg = qdiy.model_cfg()
+    t0 = time.perf_counter()
+    img = qdiy.random_model_image(cfg, seed, 0.02, nthreads=16)
+    t_fill = time.perf_counter() - t0
+    eng = qdiy.Engine(image=img)
+    del img
+    rng = np.random.default_rng(seed)
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, n_prompt)]
+    eng.generate(prompt[:8], 8, stop_at_eos=False)            # warm-up
+    eng.reset()
+    t0 = time.perf_counter()
+    pos = eng.prefill(prompt[:-1])
+    t_prompt = time.perf_counter() - t0
+    last, toks = prompt[-1], []
+    t0 = time.perf_counter()
+    for _ in range(n_new):
+        last = eng.step(last, pos)
+        pos += 1
+        toks.append(last)
+    t_dec = time.perf_counter() - t0
+    eng.close()
+    ms_tok = t_dec * 1e3 / n_new
+    # Attention per token: 24 qd_decode_attention calls at the mean KV length of
+    # the generated tokens, timed cold in isolation.
+    mean_L = n_prompt + n_new // 2
+    att = measure(lib, mean_L, 400, 40, 0, 0)
+    share = cfg.num_layers * att["us_cold"] / 1e3 / ms_tok
+    H_, I_, V_, NL = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_layers
+    w_bytes = 2 * (NL * (3 * H_ * H_ + 3 * H_ + H_ * H_ + 2 * H_ + 3 * I_ * H_) + H_ + V_ * H_ + H_)
+    tok_bytes = w_bytes + NL * 2 * mean_L * H_ * 2
+    log(f"[bench] config 5: {n_new / t_dec:.1f} tokens/s ({ms_tok:.3f} ms/token, "
+        f"{tok_bytes / (ms_tok * 1e-3) / 1e9:.0f} GB/s over {tok_bytes / 1e9:.3f} GB/token), "
+        f"prompt {n_prompt - 1} tokens in {t_prompt * 1e3:.1f} ms, attention share ~{100 * share:.1f}% "
+        f"(24 x {att['us_cold']:.2f} us at L={mean_L}), image fill {t_fill:.1f} s")
+    return {"model": "Qwen-1.8B shape, random init (library generator, std 0.02, norm weights 1)",
+            "prompt_tokens": n_prompt, "generated_tokens": n_new,
+            "tokens_per_s": round(n_new / t_dec, 2), "ms_per_token": round(ms_tok, 4),
+            "prompt_ms": round(t_prompt * 1e3, 2), "bytes_per_token": tok_bytes,
+            "gbps": round(tok_bytes / (ms_tok * 1e-3) / 1e9, 1),
+            "attention_share_est": round(share, 4),
+            "attention_us_per_call_at_mean_L": round(att["us_cold"], 3), "mean_L": mean_L,
+            "first_tokens": toks[:8]}
+
+
 def cpu_baseline(L: int, seconds: float):
     """Times the C oracle (restatement of the reference kernels) on host cores."""
     import numpy as np
@@ -224,6 +284,7 @@ def main() -> int:
     ap.add_argument("--splits", type=int, default=0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-front", action="store_true", help="skip the config-4 front-end timing")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-5 end-to-end timing")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one 256 MiB device copy (known FETCH_SIZE/WRITE_SIZE) and exit")
@@ -259,6 +320,7 @@ def main() -> int:
     # config 1 names the fused single-workgroup-per-head path at L=512
     fused512 = measure(lib, 512, args.steps, args.warmup, 1, 0) if 512 in kv and variant == 0 else None
     front = None if args.no_front else measure_front(lib, args.steps, args.warmup)
+    e2e = None if args.no_e2e else measure_e2e(lib)
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -291,6 +353,7 @@ def main() -> int:
             "plans": {str(L): r["plan"] for L, r in res.items()},
             "fused_path_us_per_call_512": None if fused512 is None else round(fused512["us_cold"], 3),
             "config4_front_end": front,
+            "config5_e2e": e2e,
         },
         "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": traffic},

@@ -1,0 +1,84 @@
+/*
+ * qdiy/decode.h -- C ABI of the rest of one decode step on MI355X (gfx950):
+ * the launches of the reference engine's QwenEngine::step around attention
+ * (SeaTheDestiny/LLM-inference-DIY, framework_src/qwen_infer.cu:700-731).
+ *
+ *   gemm(d_attn_proj, d_qkv_out, attn_proj_w, 1, H, H)        (:701)
+ *   add_bias_kernel(d_x, d_attn_proj, H)                      (:704)
+ *       -> qd_proj_residual(d_qkv_out, attn_proj_w, d_x, d_x, H, H)
+ *   rmsnorm_kernel(d_norm_x, d_x, ln_2, H, eps)               (:708)
+ *   gemm(d_ffn_w1, ...) ; gemm(d_ffn_w2, ...)                 (:711-712)
+ *   swiglu_kernel(d_ffn_act, d_ffn_w1, d_ffn_w2, IM)          (:715)
+ *       -> qd_ffn_up_swiglu(d_x, ln_2, eps, ffn_w1, ffn_w2, d_ffn_act, H, IM)
+ *   gemm(d_ffn_proj, d_ffn_act, ffn_proj_w, 1, H, IM)         (:718)
+ *   add_bias_kernel(d_x, d_ffn_proj, H)                       (:721)
+ *       -> qd_proj_residual(d_ffn_act, ffn_proj_w, d_x, d_x, H, IM)
+ *   rmsnorm_kernel(d_norm_x, d_x, ln_f, H, eps)               (:725)
+ *   gemm(d_logits, d_norm_x, lm_head, 1, V, H)                (:728)
+ *   argmax_kernel(d_next_token, d_logits, V)                  (:731)
+ *       -> qd_lm_head_argmax(d_x, ln_f, eps, lm_head, d_logits, V, H, ws, ...)
+ *
+ * Conventions are those of qdiy/attn.h: fp16 as uint16_t bit patterns in
+ * device memory, asynchronous on `stream`, status codes, no host sync.
+ * Weight matrices stay in the .bin file's [out][in] layout
+ * (model_weights/convert_weights.py:135-172); the reference engine transposes
+ * them at load (qwen_infer.cu:230-241) for its hgemv_kernel, this library
+ * reads them as stored.
+ *
+ * Numerics: every GEMV output is the fp32 sum of exact fp16 x fp16 products in
+ * one fixed order -- lane l of a 64-lane wave owns elements
+ * k = 512*j + 8*l + e and adds them sequentially (j, then e ascending), then
+ * the 64 lane sums are added in a fixed tree -- rounded once to fp16 where the
+ * reference stores a half.  RMSNorm uses the same order for its sum of
+ * squares.  Results are therefore bit-for-bit reproducible on the host.
+ */
+#ifndef QDIY_DECODE_H
+#define QDIY_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "qdiy/attn.h"
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* out[n] = half(residual[n] + half(sum_k W[n][k] * x[k])) for n < n_out.
+ * W is [n_out][k_in] fp16; k_in a multiple of 8; x, w 16-byte aligned.
+ * residual and out may be the same buffer (the reference adds in place into
+ * d_x).  Replaces hgemv_kernel + add_bias_kernel (hgemm_final.cuh:274-295,
+ * bias.cuh:6-11; qwen_infer.cu:701-704 and :718-721). */
+int qd_proj_residual(const uint16_t* x, const uint16_t* w, const uint16_t* residual,
+                     uint16_t* out, int n_out, int k_in, hipStream_t stream);
+
+/* act[i] = half(g_i * (u_i / (1 + exp(-u_i)))), g_i = half(W1[i] . xn),
+ * u_i = half(W2[i] . xn), xn = half(x * (1/sqrt(mean(x^2) + eps)) * norm_w),
+ * for i < inter.  W1 (gate, ffn_w1) and W2 (up, ffn_w2) are [inter][hidden];
+ * hidden a multiple of 512, at most 4096.  exp(-u) is computed as
+ * 2^(-u * log2 e) by a polynomial the host can repeat exactly.  Replaces
+ * rmsnorm_kernel + 2 x hgemv_kernel + swiglu_kernel (rmsnorm.cuh:6-57,
+ * swiglu.cuh:6-15; qwen_infer.cu:708-715). */
+int qd_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* w1,
+                     const uint16_t* w2, uint16_t* act, int hidden, int inter,
+                     hipStream_t stream);
+
+/* Device workspace (bytes) qd_lm_head_argmax needs for a vocabulary size. */
+size_t qd_lm_head_workspace_bytes(int vocab);
+
+/* logits[v] = half(W[v] . xn) for v < vocab with xn the RMSNorm of x by
+ * norm_w (as above), then *token (device int) = the index of the largest
+ * logit.  Ties go to the lowest index; -0 equals +0; NaN never wins.  (The
+ * reference's argmax_kernel breaks ties by its thread and lane order,
+ * argmax.cuh:19-66.)  W is [vocab][hidden].  workspace: device memory of
+ * qd_lm_head_workspace_bytes(vocab) bytes, 8-byte aligned.  Replaces
+ * rmsnorm_kernel + hgemv_kernel + argmax_kernel (qwen_infer.cu:725-731). */
+int qd_lm_head_argmax(const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* w,
+                      uint16_t* logits, int vocab, int hidden, void* workspace,
+                      size_t workspace_bytes, int* token, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QDIY_DECODE_H */

@@ -15,8 +15,9 @@ INCLUDE = os.path.join(ROOT, "include")
 LIB_DIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIB_DIR, "libqdiy.so")
 BENCH_LIB = os.path.join(LIB_DIR, "libqdiy_bench.so")
+ENGINE_EXE = os.path.join(LIB_DIR, "qdiy_engine")
 
-SOURCES = ["qd_capi.cpp", "qd_attention.hip", "qd_rope_cache.hip", "qd_decode_ops.hip"]
+SOURCES = ["qd_capi.cpp", "qd_engine.cpp", "qd_attention.hip", "qd_rope_cache.hip", "qd_decode_ops.hip"]
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for all device code: plain float code is
@@ -47,7 +48,8 @@ def _run(cmd, verbose):
 
 
 def build(verbose: bool = False) -> str:
-    """Builds libqdiy.so (kernels + C ABI) and libqdiy_bench.so (bench loop)."""
+    """Builds libqdiy.so (kernels + C ABI), libqdiy_bench.so (bench loop) and the
+    qdiy_engine executable (stdin/stdout protocol)."""
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB + ".tmp"
     _run([hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -59,6 +61,11 @@ def build(verbose: bool = False) -> str:
           "-o", tmp, os.path.join(CSRC, "qd_bench.cpp"), "-L", LIB_DIR, "-lqdiy",
           "-Wl,-rpath,$ORIGIN"], verbose)
     os.replace(tmp, BENCH_LIB)
+    tmp = ENGINE_EXE + ".tmp"
+    _run([hipcc(), "-O2", "-std=c++17", "-Wall", "-I", INCLUDE, "-o", tmp,
+          os.path.join(CSRC, "qd_engine_main.cpp"), "-L", LIB_DIR, "-lqdiy", "-Wl,-rpath,$ORIGIN"],
+         verbose)
+    os.replace(tmp, ENGINE_EXE)
     return LIB
 
 

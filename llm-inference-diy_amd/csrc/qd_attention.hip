@@ -244,7 +244,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
       p.part_o[slot * kD + tid] = O;
       if (tid == 0) p.part_ml[slot] = float2{M, L};
     } else {
-      reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = (_Float16)__fdiv_rn(O, L);
+      reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = to_f16(O / L);
     }
   }
 }
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p
       L += sl[s];
       O += so[s][tid];
     }
-    reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = (_Float16)__fdiv_rn(O, L);
+    reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = to_f16(O / L);
   }
 }
 

@@ -11,8 +11,10 @@
 #include "qd_internal.h"
 
 namespace {
-
 thread_local char g_err[512] = "";
+}  // namespace
+
+namespace qd {
 
 int fail(int code, const char* fmt, ...) {
   va_list ap;
@@ -26,7 +28,13 @@ int hip_fail(hipError_t e, const char* what) {
   return fail(QD_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+}  // namespace qd
+
+namespace {
+
+using qd::aligned16;
+using qd::fail;
+using qd::hip_fail;
 
 // Launch planner, from measured sweeps on MI355X (16 heads, cold KV, 4-wave
 // workgroups, non-temporal KV loads):

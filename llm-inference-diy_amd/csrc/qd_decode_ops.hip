@@ -1,5 +1,7 @@
 // Decode-step kernels around attention for gfx950: the fused attention front
-// end (RMSNorm -> QKV GEMV -> bias -> RoPE -> KV-cache append).
+// end (RMSNorm -> QKV GEMV -> bias -> RoPE -> KV-cache append), the output
+// projections with their residual adds, the SwiGLU FFN input side, and the
+// lm_head GEMV with greedy argmax.
 //
 // Replaces, for one decode token of one layer, the reference's
 //   rmsnorm_kernel<<<1,512>>>            (kernels/rmsnorm.cuh:6-57, qwen_infer.cu:626)
@@ -27,18 +29,27 @@
 namespace qd {
 namespace {
 
+constexpr float kLog2e = 1.44269504088896340736f;
+
 // x (optionally RMS-normalised) for this lane's elements k = 512*j + 8*l + e.
+// The normalisation (rmsnorm.cuh:6-57) is x * (1 / sqrt(sum(x^2) / n + eps))
+// * w with the sum of squares in the wave64 order, correctly rounded sqrt and
+// divide, each product rounded to fp32 and the result to fp16.  (HIP's
+// __fsqrt_rn is the native v_sqrt_f32, not correctly rounded; sqrtf and '/'
+// are, by hipcc's default -fhip-fp32-correctly-rounded-divide-sqrt.)
 template <int NJ>
-__device__ __forceinline__ void load_input(const QkvFrontParams& p, int lane, f16x8 (&xv)[NJ]) {
+__device__ __forceinline__ void load_input(const uint16_t* __restrict__ x,
+                                           const uint16_t* __restrict__ norm_w, float eps,
+                                           int lane, f16x8 (&xv)[NJ]) {
   const int hidden = NJ * 512;
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
-    xv[j] = *reinterpret_cast<const f16x8*>(p.x + 512 * j + 8 * lane);
-  if (p.norm_w == nullptr) return;
+    xv[j] = *reinterpret_cast<const f16x8*>(x + 512 * j + 8 * lane);
+  if (norm_w == nullptr) return;
   f16x8 wv[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
-    wv[j] = *reinterpret_cast<const f16x8*>(p.norm_w + 512 * j + 8 * lane);
+    wv[j] = *reinterpret_cast<const f16x8*>(norm_w + 512 * j + 8 * lane);
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
@@ -48,13 +59,13 @@ __device__ __forceinline__ void load_input(const QkvFrontParams& p, int lane, f1
       acc = __builtin_fmaf(v, v, acc);   // exact square: rounds only the sum
     }
   const float var = wave64_sum(acc) / (float)hidden;
-  const float r = __fdiv_rn(1.0f, __fsqrt_rn(var + p.eps));
+  const float r = 1.0f / __builtin_sqrtf(var + eps);
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
 #pragma clang fp contract(off)
-      xv[j][e] = (_Float16)(((float)xv[j][e] * r) * (float)wv[j][e]);
+      xv[j][e] = to_f16(((float)xv[j][e] * r) * (float)wv[j][e]);
     }
 }
 
@@ -93,8 +104,8 @@ __device__ __forceinline__ void qkv_front_epilogue(const QkvFrontParams& p, int 
   const float k1c = k1 * cs.x, k2s = k2 * cs.y, k2c = k2 * cs.x, k1s = k1 * cs.y;
   _Float16* qkv = reinterpret_cast<_Float16*>(p.qkv);
   const int idx1 = h * 128 + i;
-  qkv[idx1] = (_Float16)(q1c - q2s);
-  qkv[idx1 + 64] = (_Float16)(q2c + q1s);
+  qkv[idx1] = to_f16(q1c - q2s);
+  qkv[idx1 + 64] = to_f16(q2c + q1s);
   qkv[hidden + idx1] = v6[2];
   qkv[hidden + idx1 + 64] = v6[3];
   qkv[2 * hidden + idx1] = v6[4];
@@ -102,8 +113,8 @@ __device__ __forceinline__ void qkv_front_epilogue(const QkvFrontParams& p, int 
   const long long base = (long long)p.pos * p.row_stride + (long long)h * p.head_stride;
   _Float16* kc = reinterpret_cast<_Float16*>(p.k_layer) + base;
   _Float16* vc = reinterpret_cast<_Float16*>(p.v_layer) + base;
-  kc[i] = (_Float16)(k1c - k2s);
-  kc[64 + i] = (_Float16)(k2c + k1s);
+  kc[i] = to_f16(k1c - k2s);
+  kc[64 + i] = to_f16(k2c + k1s);
   vc[i] = v6[4];
   vc[64 + i] = v6[5];
 }
@@ -119,11 +130,192 @@ __global__ __launch_bounds__(384) void qkv_front_kernel(QkvFrontParams p) {
   const int row = (wave >> 1) * hidden + h * 128 + i + (wave & 1) * 64;
 
   f16x8 xv[NJ];
-  load_input<NJ>(p, lane, xv);
+  load_input<NJ>(p.x, p.norm_w, p.eps, lane, xv);
   const float acc = row_dot<NJ>(p.w + (long long)row * hidden, lane, xv);
-  if (lane == 0) y[wave] = (_Float16)acc;     // hgemv's half output
+  if (lane == 0) y[wave] = to_f16(acc);       // hgemv's half output
   __syncthreads();
   if (threadIdx.x == 0) qkv_front_epilogue(p, h, i, hidden, y);
+}
+
+// This lane's sequential sum of x[k] * w_row[k] over k = 512*j + 8*lane + e
+// (j ascending, e ascending, k < K; K a multiple of 8); the caller adds the
+// lanes with wave64_sum.  Four 512-element chunks are loaded at a time.
+__device__ __forceinline__ float lane_dot(const uint16_t* __restrict__ w_row,
+                                          const uint16_t* __restrict__ x, int lane, int K) {
+  float acc = 0.0f;
+  const int nfull = K >> 9;
+  int j = 0;
+  for (; j + 4 <= nfull; j += 4) {
+    f16x8 wv[4], xv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      wv[q] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(w_row + 512 * (j + q) + 8 * lane));
+      xv[q] = *reinterpret_cast<const f16x8*>(x + 512 * (j + q) + 8 * lane);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)wv[q][e], (float)xv[q][e], acc);
+  }
+  for (; j < nfull; ++j) {
+    const f16x8 wv = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(w_row + 512 * j + 8 * lane));
+    const f16x8 xv = *reinterpret_cast<const f16x8*>(x + 512 * j + 8 * lane);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)wv[e], (float)xv[e], acc);
+  }
+  if (8 * lane < K - (nfull << 9)) {
+    const f16x8 wv = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(w_row + 512 * nfull + 8 * lane));
+    const f16x8 xv = *reinterpret_cast<const f16x8*>(x + 512 * nfull + 8 * lane);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)wv[e], (float)xv[e], acc);
+  }
+  return acc;
+}
+
+// Output projection + residual add (qwen_infer.cu:701-704 and :717-720:
+// hgemv into a half buffer, then add_bias_kernel onto d_x).  One wave per
+// output row, four waves per workgroup.
+__global__ __launch_bounds__(256) void proj_residual_kernel(ProjResidualParams p) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= p.n_out) return;                    // whole wave
+  const float s = wave64_sum(lane_dot(p.w + (long long)n * p.k_in, p.x, lane, p.k_in));
+  if (lane == 0) {
+    const _Float16 y = to_f16(s);              // hgemv's half output
+    reinterpret_cast<_Float16*>(p.out)[n] =
+        (_Float16)((float)reinterpret_cast<const _Float16*>(p.res)[n] + (float)y);
+  }
+}
+
+// SwiGLU input side (qwen_infer.cu:708-715): RMSNorm(x) with ln_2, the W1
+// (gate) and W2 (up) GEMVs, and act = half(g * (u / (1 + exp(-u)))) as in
+// swiglu.cuh:6-15, with exp(-u) = exp2_rep(-u * log2(e)).  One wave per
+// intermediate index: both rows' loads are issued before either sum.
+template <int NJ>
+__global__ __launch_bounds__(256) void ffn_up_kernel(FfnUpParams p) {
+  const int lane = threadIdx.x & 63;
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (i >= p.inter) return;                    // whole wave
+  constexpr int hidden = NJ * 512;
+  f16x8 xv[NJ];
+  load_input<NJ>(p.x, p.norm_w, p.eps, lane, xv);
+  const uint16_t* r1 = p.w1 + (long long)i * hidden;
+  const uint16_t* r2 = p.w2 + (long long)i * hidden;
+  f16x8 a[NJ], b[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    a[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(r1 + 512 * j + 8 * lane));
+    b[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(r2 + 512 * j + 8 * lane));
+  }
+  float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      ga = __builtin_fmaf((float)a[j][e], (float)xv[j][e], ga);
+      ua = __builtin_fmaf((float)b[j][e], (float)xv[j][e], ua);
+    }
+  const float g = wave64_sum(ga);
+  const float u = wave64_sum(ua);
+  if (lane == 0) {
+    const float gh = (float)to_f16(g);
+    const float uh = (float)to_f16(u);
+    const float e = exp2_rep(-uh * kLog2e);
+    const float silu = uh / (1.0f + e);
+    reinterpret_cast<_Float16*>(p.act)[i] = to_f16(gh * silu);
+  }
+}
+
+// Packed argmax key of an fp16 logit at index `row`: the upper half orders the
+// values (-0 counts as +0, NaN below everything), the lower half is
+// 0xFFFFFFFF - row, so the largest key is the largest value at its lowest
+// index.
+__device__ __forceinline__ unsigned long long argmax_key(_Float16 h, int row) {
+  unsigned int b = __builtin_bit_cast(unsigned short, h);
+  if (b == 0x8000u) b = 0u;
+  unsigned int k;
+  if ((b & 0x7FFFu) > 0x7C00u) k = 0u;
+  else k = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
+  return ((unsigned long long)k << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned int)row);
+}
+
+// Final RMSNorm with ln_f, lm_head GEMV and the first half of the greedy
+// argmax (qwen_infer.cu:725-731).  Each wave normalises x once and takes
+// kLmRowsPerWave consecutive rows, two at a time; every logit is written (the
+// reference's d_logits) and each workgroup stores its best key.
+template <int NJ>
+__global__ __launch_bounds__(kLmWaves * 64) void lm_head_kernel(LmHeadParams p) {
+  __shared__ unsigned long long best[kLmWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  constexpr int hidden = NJ * 512;
+  const int row0 = (blockIdx.x * kLmWaves + wave) * kLmRowsPerWave;
+  unsigned long long key = 0ull;
+  if (row0 < p.vocab) {
+    f16x8 xv[NJ];
+    load_input<NJ>(p.x, p.norm_w, p.eps, lane, xv);
+#pragma unroll
+    for (int r = 0; r < kLmRowsPerWave; r += 2) {
+      const int ra = min(row0 + r, p.vocab - 1);
+      const int rb = min(row0 + r + 1, p.vocab - 1);
+      f16x8 a[NJ], b[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        a[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p.w + (long long)ra * hidden + 512 * j + 8 * lane));
+        b[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p.w + (long long)rb * hidden + 512 * j + 8 * lane));
+      }
+      float sa = 0.0f, sb = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          sa = __builtin_fmaf((float)a[j][e], (float)xv[j][e], sa);
+          sb = __builtin_fmaf((float)b[j][e], (float)xv[j][e], sb);
+        }
+      const _Float16 ha = to_f16(wave64_sum(sa));
+      const _Float16 hb = to_f16(wave64_sum(sb));
+      if (row0 + r < p.vocab) {
+        if (lane == 0) reinterpret_cast<_Float16*>(p.logits)[row0 + r] = ha;
+        const unsigned long long k = argmax_key(ha, row0 + r);
+        key = k > key ? k : key;
+      }
+      if (row0 + r + 1 < p.vocab) {
+        if (lane == 0) reinterpret_cast<_Float16*>(p.logits)[row0 + r + 1] = hb;
+        const unsigned long long k = argmax_key(hb, row0 + r + 1);
+        key = k > key ? k : key;
+      }
+    }
+  }
+  if (lane == 0) best[wave] = key;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long k = best[0];
+#pragma unroll
+    for (int w = 1; w < kLmWaves; ++w) k = best[w] > k ? best[w] : k;
+    p.part[blockIdx.x] = k;
+  }
+}
+
+// Second half of the argmax: one workgroup folds the per-workgroup keys and
+// writes the winning row as the next token id.
+__global__ __launch_bounds__(1024) void argmax_reduce_kernel(const unsigned long long* part,
+                                                             int nparts, int* token) {
+  __shared__ unsigned long long best[16];
+  unsigned long long k = 0ull;
+  for (int i = threadIdx.x; i < nparts; i += 1024) k = part[i] > k ? part[i] : k;
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) {
+    const unsigned long long o = __shfl_xor(k, m);
+    k = o > k ? o : k;
+  }
+  if ((threadIdx.x & 63) == 0) best[threadIdx.x >> 6] = k;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned long long b = best[0];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) b = best[w] > b ? best[w] : b;
+    *token = (int)(0xFFFFFFFFu - (unsigned int)(b & 0xFFFFFFFFull));
+  }
 }
 
 }  // namespace
@@ -141,6 +333,52 @@ hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream) {
     case 8: hipLaunchKernelGGL(qkv_front_kernel<8>, grid, block, 0, stream, p); break;
     default: return hipErrorInvalidValue;
   }
+  return hipGetLastError();
+}
+
+}  // namespace qd
+
+namespace qd {
+
+hipError_t launch_proj_residual(const ProjResidualParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL(proj_residual_kernel, dim3((p.n_out + 3) / 4), dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_ffn_up(const FfnUpParams& p, hipStream_t stream) {
+  const dim3 grid((p.inter + 3) / 4), block(256);
+  switch (p.hidden / 512) {
+    case 1: hipLaunchKernelGGL(ffn_up_kernel<1>, grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(ffn_up_kernel<2>, grid, block, 0, stream, p); break;
+    case 3: hipLaunchKernelGGL(ffn_up_kernel<3>, grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(ffn_up_kernel<4>, grid, block, 0, stream, p); break;
+    case 5: hipLaunchKernelGGL(ffn_up_kernel<5>, grid, block, 0, stream, p); break;
+    case 6: hipLaunchKernelGGL(ffn_up_kernel<6>, grid, block, 0, stream, p); break;
+    case 7: hipLaunchKernelGGL(ffn_up_kernel<7>, grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL(ffn_up_kernel<8>, grid, block, 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_head_argmax(const LmHeadParams& p, int* token, hipStream_t stream) {
+  const int parts = lm_head_parts(p.vocab);
+  const dim3 grid(parts), block(kLmWaves * 64);
+  switch (p.hidden / 512) {
+    case 1: hipLaunchKernelGGL(lm_head_kernel<1>, grid, block, 0, stream, p); break;
+    case 2: hipLaunchKernelGGL(lm_head_kernel<2>, grid, block, 0, stream, p); break;
+    case 3: hipLaunchKernelGGL(lm_head_kernel<3>, grid, block, 0, stream, p); break;
+    case 4: hipLaunchKernelGGL(lm_head_kernel<4>, grid, block, 0, stream, p); break;
+    case 5: hipLaunchKernelGGL(lm_head_kernel<5>, grid, block, 0, stream, p); break;
+    case 6: hipLaunchKernelGGL(lm_head_kernel<6>, grid, block, 0, stream, p); break;
+    case 7: hipLaunchKernelGGL(lm_head_kernel<7>, grid, block, 0, stream, p); break;
+    case 8: hipLaunchKernelGGL(lm_head_kernel<8>, grid, block, 0, stream, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(argmax_reduce_kernel, dim3(1), dim3(1024), 0, stream,
+                     (const unsigned long long*)p.part, parts, token);
   return hipGetLastError();
 }
 

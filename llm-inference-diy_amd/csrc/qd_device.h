@@ -10,6 +10,16 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// fp32 -> fp16, round to nearest even, of a value already rounded to fp32.
+// The empty asm pins x as an fp32 register value, so the compiler cannot fold
+// the multiply or add that produced it into the conversion (v_fma_mixlo_f16
+// and v_mad_mixlo_f16 round once, straight to fp16, which differs from
+// rounding to fp32 first wherever the fp32 value sits on an fp16 tie).
+__device__ __forceinline__ _Float16 to_f16(float x) {
+  asm volatile("" : "+v"(x));
+  return (_Float16)x;
+}
+
 // DPP row-local permutations (gfx9 encodings).
 constexpr int kDppQuadSwap1 = 0xB1;   // quad_perm [1,0,3,2]
 constexpr int kDppQuadSwap2 = 0x4E;   // quad_perm [2,3,0,1]

@@ -61,6 +61,52 @@ struct QkvFrontParams {
   int num_heads;
 };
 
+// out[n] = half(res[n] + half(W[n] . x)) for n < n_out; W is [n_out][k_in]
+// ([out][in]), k_in a multiple of 8.  res and out may alias.
+struct ProjResidualParams {
+  const uint16_t* x;
+  const uint16_t* w;
+  const uint16_t* res;
+  uint16_t* out;
+  int n_out;
+  int k_in;
+};
+
+// act[i] = half(g * (u / (1 + exp(-u)))) with g = half(W1[i] . xn),
+// u = half(W2[i] . xn), xn = RMSNorm(x) * norm_w; W1/W2 are [inter][hidden].
+struct FfnUpParams {
+  const uint16_t* x;
+  const uint16_t* norm_w;
+  float eps;
+  const uint16_t* w1;
+  const uint16_t* w2;
+  uint16_t* act;
+  int hidden;
+  int inter;
+};
+
+// logits[v] = half(W[v] . xn) for v < vocab, xn = RMSNorm(x) * norm_w; each
+// workgroup also writes its best (logit, lowest index) as a packed key.
+struct LmHeadParams {
+  const uint16_t* x;
+  const uint16_t* norm_w;
+  float eps;
+  const uint16_t* w;
+  uint16_t* logits;
+  unsigned long long* part;
+  int vocab;
+  int hidden;
+};
+
+// Rows per wave and waves per workgroup of the lm_head kernel; the number of
+// per-workgroup keys for a vocabulary follows from them.
+constexpr int kLmRowsPerWave = 8;
+constexpr int kLmWaves = 4;
+inline int lm_head_parts(int vocab) {
+  const int rows = kLmRowsPerWave * kLmWaves;
+  return (vocab + rows - 1) / rows;
+}
+
 // Launch plan of one decode-attention call.
 struct AttnPlan {
   int variant;            // 0 fused, 1 split
@@ -70,9 +116,19 @@ struct AttnPlan {
   int waves;              // waves per split workgroup (4, 8 or 16)
 };
 
+// Error reporting of the C ABI: records a printf-style message for
+// qd_last_error() on this host thread and returns `code`.
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char* what);
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream);
 hipError_t launch_qkv_bias_rope_cache(const RopeParams& p, hipStream_t stream);
 hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream);
+hipError_t launch_proj_residual(const ProjResidualParams& p, hipStream_t stream);
+hipError_t launch_ffn_up(const FfnUpParams& p, hipStream_t stream);
+// lm_head kernel, then the one-workgroup reduction of its keys into *token.
+hipError_t launch_lm_head_argmax(const LmHeadParams& p, int* token, hipStream_t stream);
 
 }  // namespace qd
 

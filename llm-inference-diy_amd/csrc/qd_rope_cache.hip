@@ -12,6 +12,7 @@
 // is evaluated as written -- mul, mul, add/sub, each rounded (FP contraction
 // is disabled in this kernel) -- so results equal a host fp32 evaluation of
 // the reference formula bit for bit.
+#include "qd_device.h"
 #include "qd_internal.h"
 
 namespace qd {
@@ -49,14 +50,14 @@ __global__ __launch_bounds__(256) void qkv_bias_rope_cache_kernel(RopeParams p) 
   const float q1 = (float)hq1, q2 = (float)hq2, k1 = (float)hk1, k2 = (float)hk2;
   const float q1c = q1 * cs.x, q2s = q2 * cs.y, q2c = q2 * cs.x, q1s = q1 * cs.y;
   const float k1c = k1 * cs.x, k2s = k2 * cs.y, k2c = k2 * cs.x, k1s = k1 * cs.y;
-  qkv[idx1] = (_Float16)(q1c - q2s);
-  qkv[idx2] = (_Float16)(q2c + q1s);
+  qkv[idx1] = to_f16(q1c - q2s);
+  qkv[idx2] = to_f16(q2c + q1s);
 
   const long long base = (long long)p.pos * p.row_stride + (long long)h * p.head_stride;
   _Float16* kc = reinterpret_cast<_Float16*>(p.k_layer) + base;
   _Float16* vc = reinterpret_cast<_Float16*>(p.v_layer) + base;
-  kc[i] = (_Float16)(k1c - k2s);
-  kc[64 + i] = (_Float16)(k2c + k1s);
+  kc[i] = to_f16(k1c - k2s);
+  kc[64 + i] = to_f16(k2c + k1s);
   vc[i] = hv1;
   vc[64 + i] = hv2;
 }

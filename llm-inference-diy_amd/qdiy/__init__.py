@@ -14,10 +14,12 @@ from __future__ import annotations
 import ctypes
 import os
 
+import numpy as np
 import torch
 
 PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.path.join(PKG_DIR, "lib", "libqdiy.so")
+ENGINE_EXE = os.path.join(PKG_DIR, "lib", "qdiy_engine")
 HEAD_DIM = 128
 
 QD_OK, QD_EINVAL, QD_EHIP, QD_ENOMEM = 0, 1, 2, 3
@@ -29,6 +31,12 @@ EXPORTS = (
     "qd_decode_attention_fused", "qd_decode_attention_split", "qd_decode_attention_plan",
     "qd_decode_attention_plan_detail",
     "qd_max_splits", "qd_last_error", "qd_version",
+    # qdiy/decode.h
+    "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
+    # qdiy/engine.h
+    "qd_model_image_bytes", "qd_model_fill_random", "qd_model_write_random", "qd_engine_create",
+    "qd_engine_create_from_image", "qd_engine_destroy", "qd_engine_config", "qd_engine_reset",
+    "qd_engine_prefill", "qd_engine_step", "qd_engine_logits", "qd_engine_generate",
 )
 
 
@@ -42,6 +50,20 @@ class Cfg(ctypes.Structure):
     _fields_ = [("num_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
                 ("max_seqlen", ctypes.c_int), ("kv_row_stride", ctypes.c_longlong),
                 ("kv_head_stride", ctypes.c_longlong), ("rope_base", ctypes.c_float)]
+
+
+class ModelCfg(ctypes.Structure):
+    """qd_model_cfg: the .bin header's model configuration."""
+    _fields_ = [("vocab_size", ctypes.c_uint32), ("hidden_size", ctypes.c_uint32),
+                ("num_layers", ctypes.c_uint32), ("num_heads", ctypes.c_uint32),
+                ("intermediate_size", ctypes.c_uint32), ("max_seqlen", ctypes.c_uint32)]
+
+    def as_dict(self):
+        return {f: int(getattr(self, f)) for f, _ in self._fields_}
+
+
+QWEN_1_8B = dict(vocab_size=151936, hidden_size=2048, num_layers=24, num_heads=16,
+                 intermediate_size=5504, max_seqlen=32768)
 
 
 class AttnPlan(ctypes.Structure):
@@ -76,6 +98,28 @@ def load() -> ctypes.CDLL:
     L.qd_decode_attention_split.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
     L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
     L.qd_decode_attention_plan_detail.argtypes = [vp, i, i, i, ctypes.POINTER(AttnPlan)]
+    u16p = ctypes.POINTER(ctypes.c_uint16)
+    ip = ctypes.POINTER(ctypes.c_int)
+    L.qd_proj_residual.argtypes = [vp, vp, vp, vp, i, i, vp]
+    L.qd_ffn_up_swiglu.argtypes = [vp, vp, ctypes.c_float, vp, vp, vp, i, i, vp]
+    L.qd_lm_head_workspace_bytes.argtypes = [i]
+    L.qd_lm_head_workspace_bytes.restype = ctypes.c_size_t
+    L.qd_lm_head_argmax.argtypes = [vp, vp, ctypes.c_float, vp, vp, i, i, vp, ctypes.c_size_t, vp, vp]
+    L.qd_model_image_bytes.argtypes = [ctypes.POINTER(ModelCfg)]
+    L.qd_model_image_bytes.restype = ll
+    L.qd_model_fill_random.argtypes = [vp, ll, ctypes.POINTER(ModelCfg), ctypes.c_uint64,
+                                       ctypes.c_float, i]
+    L.qd_model_write_random.argtypes = [ctypes.c_char_p, ctypes.POINTER(ModelCfg), ctypes.c_uint64,
+                                        ctypes.c_float]
+    L.qd_engine_create.argtypes = [ctypes.c_char_p, ctypes.POINTER(vp)]
+    L.qd_engine_create_from_image.argtypes = [vp, ll, ctypes.POINTER(vp)]
+    L.qd_engine_destroy.argtypes = [vp]
+    L.qd_engine_config.argtypes = [vp, ctypes.POINTER(ModelCfg)]
+    L.qd_engine_reset.argtypes = [vp]
+    L.qd_engine_prefill.argtypes = [vp, ip, i, ip]
+    L.qd_engine_step.argtypes = [vp, i, i, ip]
+    L.qd_engine_logits.argtypes = [vp, u16p]
+    L.qd_engine_generate.argtypes = [vp, ip, i, i, i, ip, ip]
     L.qd_last_error.restype = ctypes.c_char_p
     L.qd_version.restype = ctypes.c_char_p
     _lib = L
@@ -227,6 +271,141 @@ class Context:
                                              _ptr(qkv, "qkv"), _ptr(k_layer, "k_layer", False),
                                              _ptr(v_layer, "v_layer", False), pos, max_seqlen, H,
                                              HEAD_DIM, _stream(stream)))
+
+
+# ---------------------------------------------------------------- decode.h
+
+def proj_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, out: torch.Tensor,
+                  n_out: int, k_in: int, stream=None) -> torch.Tensor:
+    """out[n] = half(residual[n] + half(W[n] . x)); W is [n_out][k_in]."""
+    if x.numel() < k_in or w.numel() < n_out * k_in or residual.numel() < n_out or out.numel() < n_out:
+        raise ValueError("x needs k_in, w n_out*k_in, residual and out n_out elements")
+    _check(load().qd_proj_residual(_ptr(x, "x"), _ptr(w, "w"), _ptr(residual, "residual"),
+                                   _ptr(out, "out"), n_out, k_in, _stream(stream)))
+    return out
+
+
+def ffn_up_swiglu(x: torch.Tensor, norm_w: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+                  act: torch.Tensor, hidden: int, inter: int, eps: float = 1e-6,
+                  stream=None) -> torch.Tensor:
+    """act[i] = half(g * silu(u)) with g, u the W1 / W2 rows times RMSNorm(x) * norm_w."""
+    if (x.numel() < hidden or norm_w.numel() < hidden or w1.numel() < inter * hidden
+            or w2.numel() < inter * hidden or act.numel() < inter):
+        raise ValueError("buffer smaller than hidden / inter imply")
+    _check(load().qd_ffn_up_swiglu(_ptr(x, "x"), _ptr(norm_w, "norm_w"), eps, _ptr(w1, "w1"),
+                                   _ptr(w2, "w2"), _ptr(act, "act"), hidden, inter,
+                                   _stream(stream)))
+    return act
+
+
+def lm_head_workspace_bytes(vocab: int) -> int:
+    return int(load().qd_lm_head_workspace_bytes(vocab))
+
+
+def lm_head_argmax(x: torch.Tensor, norm_w: torch.Tensor, w: torch.Tensor, logits: torch.Tensor,
+                   vocab: int, hidden: int, workspace: torch.Tensor, token: torch.Tensor,
+                   eps: float = 1e-6, stream=None) -> None:
+    """logits = half(W . RMSNorm(x) * norm_w); token[0] = argmax (lowest index on ties)."""
+    if x.numel() < hidden or norm_w.numel() < hidden or w.numel() < vocab * hidden or logits.numel() < vocab:
+        raise ValueError("buffer smaller than vocab / hidden imply")
+    if token.dtype != torch.int32 or not token.is_cuda or workspace.device.type != "cuda":
+        raise TypeError("token must be a GPU int32 tensor and workspace a GPU tensor")
+    ws = workspace.numel() * workspace.element_size()
+    _check(load().qd_lm_head_argmax(_ptr(x, "x"), _ptr(norm_w, "norm_w"), eps, _ptr(w, "w"),
+                                    _ptr(logits, "logits"), vocab, hidden,
+                                    ctypes.c_void_p(workspace.data_ptr()), ws,
+                                    ctypes.c_void_p(token.data_ptr()), _stream(stream)))
+
+
+# ---------------------------------------------------------------- engine.h
+
+def model_cfg(**kw) -> ModelCfg:
+    d = dict(QWEN_1_8B)
+    d.update(kw)
+    return ModelCfg(*(d[f] for f, _ in ModelCfg._fields_))
+
+
+def model_image_bytes(cfg: ModelCfg) -> int:
+    n = load().qd_model_image_bytes(ctypes.byref(cfg))
+    if n < 0:
+        raise ValueError(f"invalid model configuration {cfg.as_dict()}")
+    return int(n)
+
+
+def random_model_image(cfg: ModelCfg, seed: int, std: float = 0.02, nthreads: int = 8) -> np.ndarray:
+    """A complete .bin image (uint8 array) with qd_model_fill_random's weights."""
+    img = np.empty(model_image_bytes(cfg), np.uint8)
+    _check(load().qd_model_fill_random(img.ctypes.data_as(ctypes.c_void_p), img.size,
+                                       ctypes.byref(cfg), seed, std, nthreads))
+    return img
+
+
+def write_random_model(path: str, cfg: ModelCfg, seed: int, std: float = 0.02) -> None:
+    _check(load().qd_model_write_random(path.encode(), ctypes.byref(cfg), seed, std))
+
+
+class Engine:
+    """The greedy decode engine (qd_engine) on the current device."""
+
+    def __init__(self, path: str | None = None, image: np.ndarray | None = None):
+        L = load()
+        h = ctypes.c_void_p()
+        if (path is None) == (image is None):
+            raise ValueError("give exactly one of path and image")
+        if path is not None:
+            _check(L.qd_engine_create(path.encode(), ctypes.byref(h)))
+        else:
+            img = np.ascontiguousarray(image).view(np.uint8)
+            _check(L.qd_engine_create_from_image(img.ctypes.data_as(ctypes.c_void_p), img.size,
+                                                 ctypes.byref(h)))
+        self._h = h
+        c = ModelCfg()
+        _check(L.qd_engine_config(h, ctypes.byref(c)))
+        self.cfg = c
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            load().qd_engine_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def reset(self) -> None:
+        _check(load().qd_engine_reset(self._h))
+
+    def prefill(self, tokens, pos: int = 0) -> int:
+        t = (ctypes.c_int * len(tokens))(*tokens)
+        p = ctypes.c_int(pos)
+        _check(load().qd_engine_prefill(self._h, t, len(tokens), ctypes.byref(p)))
+        return p.value
+
+    def step(self, token: int, pos: int) -> int:
+        n = ctypes.c_int()
+        _check(load().qd_engine_step(self._h, token, pos, ctypes.byref(n)))
+        return n.value
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.cfg.vocab_size, np.float16)
+        _check(load().qd_engine_logits(self._h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))))
+        return out
+
+    def generate(self, prompt, max_new: int, stop_at_eos: bool = True) -> list:
+        p = (ctypes.c_int * len(prompt))(*prompt)
+        out = (ctypes.c_int * max(1, max_new))()
+        n = ctypes.c_int()
+        _check(load().qd_engine_generate(self._h, p, len(prompt), max_new, int(stop_at_eos), out,
+                                         ctypes.byref(n)))
+        return list(out[:n.value])
 
 
 def version() -> str:

@@ -71,6 +71,21 @@ def lib() -> ctypes.CDLL:
                                           ctypes.c_float, ctypes.c_int]
         L.qd_oracle_qkv_front.restype = ctypes.c_int
         L.qd_oracle_exp2_array.argtypes = [f32p, f32p, ll]
+        vp, i = ctypes.c_void_p, ctypes.c_int
+        L.qd_oracle_proj_residual.argtypes = [u16p, u16p, u16p, u16p, i, i, i]
+        L.qd_oracle_swiglu.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
+        L.qd_oracle_swiglu.restype = ctypes.c_uint16
+        L.qd_oracle_ffn_up_swiglu.argtypes = [u16p, u16p, ctypes.c_float, u16p, u16p, u16p, i, i, i]
+        L.qd_oracle_lm_head_argmax.argtypes = [u16p, u16p, ctypes.c_float, u16p, u16p, i, i, i]
+        L.qd_oracle_lm_head_argmax.restype = i
+        L.qd_oracle_generate.argtypes = [vp, ll, ctypes.POINTER(i), i, i, i, ctypes.POINTER(Plan), i,
+                                         ctypes.POINTER(i), ctypes.POINTER(i), u16p, i]
+        L.qd_oracle_generate.restype = i
+        L.qd_oracle_model_new.argtypes = [vp, ll, i, i]
+        L.qd_oracle_model_new.restype = vp
+        L.qd_oracle_model_free.argtypes = [vp]
+        L.qd_oracle_model_forward.argtypes = [vp, i, i, ctypes.POINTER(Plan), i, u16p]
+        L.qd_oracle_model_forward.restype = i
         L.qd_oracle_attention_planned.argtypes = [u16p, u16p, u16p, u16p, ctypes.c_int,
                                                   ctypes.c_int, ll, ll,
                                                   ctypes.POINTER(Plan), ctypes.c_int]
@@ -232,3 +247,88 @@ def attention_planned(q, k, v, seqlen, num_heads, row_stride, head_stride, plan,
     if rc != 0:
         raise ValueError(f"qd_oracle_attention_planned rejected its arguments ({plan})")
     return out
+
+
+# ------------------------------------------------------- decode step, model
+
+def proj_residual(x, W, residual, n_out, k_in, nthreads=4):
+    """out[n] = half(residual[n] + half(W[n] . x)); W flat [n_out*k_in]."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    W = np.ascontiguousarray(W, dtype=np.float16)
+    out = np.ascontiguousarray(residual, dtype=np.float16).copy()
+    lib().qd_oracle_proj_residual(_u16(x), _u16(W), _u16(out), _u16(out), n_out, k_in, nthreads)
+    return out
+
+
+def swiglu(g, u) -> np.float16:
+    r = lib().qd_oracle_swiglu(int(np.float16(g).view(np.uint16)), int(np.float16(u).view(np.uint16)))
+    return np.uint16(r).view(np.float16)
+
+
+def ffn_up_swiglu(x, norm_w, W1, W2, hidden, inter, eps=1e-6, nthreads=4):
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    norm_w = np.ascontiguousarray(norm_w, dtype=np.float16)
+    W1 = np.ascontiguousarray(W1, dtype=np.float16)
+    W2 = np.ascontiguousarray(W2, dtype=np.float16)
+    act = np.zeros(inter, np.float16)
+    lib().qd_oracle_ffn_up_swiglu(_u16(x), _u16(norm_w), eps, _u16(W1), _u16(W2), _u16(act),
+                                  hidden, inter, nthreads)
+    return act
+
+
+def lm_head_argmax(x, norm_w, W, vocab, hidden, eps=1e-6, nthreads=4):
+    """(token, logits[vocab] fp16)."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    norm_w = np.ascontiguousarray(norm_w, dtype=np.float16)
+    W = np.ascontiguousarray(W, dtype=np.float16)
+    logits = np.zeros(vocab, np.float16)
+    t = lib().qd_oracle_lm_head_argmax(_u16(x), _u16(norm_w), eps, _u16(W), _u16(logits), vocab,
+                                       hidden, nthreads)
+    return t, logits
+
+
+def generate(image, prompt, n_new, plans, stop_at_eos=False, nthreads=8):
+    """Greedy tokens of the model in the .bin image (uint8 array); plans[L-1] is
+    the attention plan at length L.  Returns (tokens, last_logits)."""
+    img = np.ascontiguousarray(image).view(np.uint8)
+    vocab = int(np.frombuffer(img[:28].tobytes(), np.uint32)[1])
+    pr = (ctypes.c_int * len(prompt))(*prompt)
+    pl = (Plan * len(plans))(*plans)
+    out = (ctypes.c_int * max(1, n_new))()
+    n = ctypes.c_int()
+    logits = np.zeros(vocab, np.float16)
+    rc = lib().qd_oracle_generate(img.ctypes.data_as(ctypes.c_void_p), img.size, pr, len(prompt),
+                                  n_new, int(stop_at_eos), pl, len(plans), out, ctypes.byref(n),
+                                  _u16(logits), nthreads)
+    if rc != 0:
+        raise ValueError("qd_oracle_generate rejected its arguments")
+    return list(out[:n.value]), logits
+
+
+class Model:
+    """Stateful oracle model over a .bin image: forward(token, pos, plan)."""
+
+    def __init__(self, image, max_pos, nthreads=8):
+        self._img = np.ascontiguousarray(image).view(np.uint8)       # kept alive
+        self.vocab = int(np.frombuffer(self._img[:28].tobytes(), np.uint32)[1])
+        self._h = lib().qd_oracle_model_new(self._img.ctypes.data_as(ctypes.c_void_p), self._img.size,
+                                            max_pos, nthreads)
+        if not self._h:
+            raise ValueError("qd_oracle_model_new rejected its arguments")
+
+    def forward(self, token, pos, plan, want_logits=True):
+        """Next token and logits (want_logits) or None."""
+        logits = np.zeros(self.vocab, np.float16) if want_logits else None
+        r = lib().qd_oracle_model_forward(self._h, int(token), pos, ctypes.byref(plan), int(want_logits),
+                                          _u16(logits) if want_logits else None)
+        if r < 0:
+            raise ValueError("qd_oracle_model_forward rejected its arguments")
+        return (r, logits) if want_logits else None
+
+    def close(self):
+        if self._h:
+            lib().qd_oracle_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()

@@ -153,6 +153,60 @@ int qd_oracle_attention_planned(const uint16_t* q, const uint16_t* k, const uint
                                 uint16_t* out, int seqlen, int num_heads, long long row_stride,
                                 long long head_stride, const qd_oracle_plan* plan, int nthreads);
 
+/* ---- the rest of the decode step and the model (qd_oracle_model.c) ----
+ * GEMVs in the wave64 order (QD_ORDER_WAVE64), fp16 roundings where the
+ * reference stores halves; nthreads >= 1 host threads split GEMV rows (results
+ * do not depend on it). */
+
+/* out[n] = half(residual[n] + half(W[n] . x)), W [n_out][k_in] (out may alias
+ * residual): qwen_infer.cu:701-704, :718-721. */
+void qd_oracle_proj_residual(const uint16_t* x, const uint16_t* W, const uint16_t* residual,
+                             uint16_t* out, int n_out, int k_in, int nthreads);
+
+/* half(g * (u / (1 + exp2(-u * log2 e)))) of two fp16 values (swiglu.cuh:6-15
+ * with exp(-u) as qd_oracle_exp2). */
+uint16_t qd_oracle_swiglu(uint16_t g, uint16_t u);
+
+/* act[i] = swiglu(half(W1[i] . xn), half(W2[i] . xn)), xn = RMSNorm(x) * norm_w:
+ * qwen_infer.cu:708-715. */
+void qd_oracle_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps,
+                             const uint16_t* w1, const uint16_t* w2, uint16_t* act, int hidden,
+                             int inter, int nthreads);
+
+/* logits[v] = half(W[v] . xn) (logits may be NULL); returns the argmax, ties
+ * to the lowest index, -0 == +0, NaN never wins: qwen_infer.cu:725-731. */
+int qd_oracle_lm_head_argmax(const uint16_t* x, const uint16_t* norm_w, float eps,
+                             const uint16_t* W, uint16_t* logits, int vocab, int hidden,
+                             int nthreads);
+
+/* A model over a .bin image (include/qdiy/engine.h's format; the image is
+ * referenced, not copied, and must outlive the model) with a KV cache of
+ * max_pos positions.  NULL on invalid arguments. */
+typedef struct qd_oracle_model qd_oracle_model;
+qd_oracle_model* qd_oracle_model_new(const void* image, long long bytes, int max_pos, int nthreads);
+void qd_oracle_model_free(qd_oracle_model* m);
+
+/* One token through all layers at `pos` (KV rows written), attention under
+ * `plan` (the plan at length pos + 1).  With want_logits, also the final norm,
+ * lm_head and argmax: returns the next token and copies the vocab fp16
+ * logits to logits_out (may be NULL); otherwise returns 0.  -1 on invalid
+ * arguments. */
+int qd_oracle_model_forward(qd_oracle_model* m, int token, int pos, const qd_oracle_plan* plan,
+                            int want_logits, uint16_t* logits_out);
+
+/* Greedy generation from a .bin image (include/qdiy/engine.h's format): the
+ * prompt's first n_prompt - 1 tokens fill the KV cache, then n_new steps from
+ * the last prompt token, each token produced by the full layer stack and
+ * lm_head argmax (qwen_infer.cu:780-817, prompts through the decode step).
+ * plans[L - 1] is the attention launch plan at length L for L = 1 ..
+ * n_prompt + n_new.  out_tokens receives *n_out tokens (fewer than n_new only
+ * when stop_at_eos hits 151645 or 151643); last_logits (vocab fp16, may be
+ * NULL) the logits of the last step.  Returns 0, or -1 on invalid
+ * arguments. */
+int qd_oracle_generate(const void* image, long long bytes, const int* prompt, int n_prompt,
+                       int n_new, int stop_at_eos, const qd_oracle_plan* plans, int n_plans,
+                       int* out_tokens, int* n_out, uint16_t* last_logits, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

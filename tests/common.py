@@ -79,3 +79,85 @@ class AttnCase:
 
     def fp64(self) -> np.ndarray:
         return np.stack([attn_fp64(self.q[h], self.Kh[h], self.Vh[h]) for h in range(self.H)])
+
+
+# ----------------------------------------------------------------- .bin images
+
+MODEL_MAGIC = 0x46445751
+
+
+def model_tensors(image: np.ndarray) -> dict:
+    """Views of every tensor of a .bin image (convert_weights.py:105-185):
+    header (7 x uint32), wte, per-layer [ln_1, qkv_w, qkv_b, attn_proj_w,
+    ln_2, ffn_w1, ffn_w2, ffn_proj_w], ln_f, lm_head."""
+    hdr = np.frombuffer(image[:28].tobytes(), np.uint32)
+    assert hdr[0] == MODEL_MAGIC
+    V, H, NL, NH, I, S = (int(v) for v in hdr[1:])
+    t = image[28:].view(np.float16)
+    o = 0
+
+    def take(*shape):
+        nonlocal o
+        n = int(np.prod(shape))
+        a = t[o:o + n].reshape(shape)
+        o += n
+        return a
+
+    m = {"cfg": dict(vocab=V, hidden=H, layers=NL, heads=NH, inter=I, max_seqlen=S)}
+    m["wte"] = take(V, H)
+    m["layers"] = []
+    for _ in range(NL):
+        m["layers"].append({"ln_1": take(H), "qkv_w": take(3 * H, H), "qkv_b": take(3 * H),
+                            "proj_w": take(H, H), "ln_2": take(H), "w1": take(I, H),
+                            "w2": take(I, H), "w_down": take(H, I)})
+    m["ln_f"] = take(H)
+    m["lm_head"] = take(V, H)
+    assert o == t.size
+    return m
+
+
+def model_logits_fp64(m: dict, tokens, rope_base: float = 10000.0, mutate: str = "") -> np.ndarray:
+    """Textbook float64 forward of the Qwen decoder over `tokens` (positions
+    0..n-1, one at a time with a KV cache); returns the last token's logits.
+    RMSNorm, fused QKV + bias, rotate-half RoPE on pairs (i, i+64), softmax
+    attention per head, SwiGLU w1 * silu(w2), residual adds, final norm and
+    lm_head.  `mutate` plants one mistake (for tests of the comparison)."""
+    c = m["cfg"]
+    H, NH, D = c["hidden"], c["heads"], 128
+    f = lambda a: a.astype(np.float64)
+
+    def rms(x, w):
+        return x / np.sqrt(np.mean(x * x) + 1e-6) * f(w)
+
+    inv = rope_base ** (-np.arange(64) * 2.0 / D)
+    Ks = [[] for _ in range(c["layers"])]
+    Vs = [[] for _ in range(c["layers"])]
+    for pos, tok in enumerate(tokens):
+        x = f(m["wte"][tok])
+        th = pos * inv
+        cs, sn = np.cos(th), np.sin(th)
+        if mutate == "rope_sign":
+            sn = -sn
+        for l, L in enumerate(m["layers"]):
+            qkv = f(L["qkv_w"]) @ rms(x, L["ln_1"]) + f(L["qkv_b"])
+            q, k, v = (qkv[i * H:(i + 1) * H].reshape(NH, D) for i in range(3))
+
+            def rot(a):
+                a1, a2 = a[:, :64], a[:, 64:]
+                return np.concatenate([a1 * cs - a2 * sn, a2 * cs + a1 * sn], axis=1)
+
+            q, k = rot(q), rot(k)
+            Ks[l].append(k)
+            Vs[l].append(v)
+            K, V = np.stack(Ks[l], 1), np.stack(Vs[l], 1)          # [NH, n, D]
+            s = np.einsum("hd,hnd->hn", q, K) / np.sqrt(D)
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            p /= p.sum(axis=1, keepdims=True)
+            a = np.einsum("hn,hnd->hd", p, V).reshape(-1)
+            x = x + f(L["proj_w"]) @ a
+            xn = rms(x, L["ln_2"])
+            g, u = f(L["w1"]) @ xn, f(L["w2"]) @ xn
+            if mutate == "swap_gate_up":
+                g, u = u, g
+            x = x + f(L["w_down"]) @ (g * u / (1.0 + np.exp(-u)))
+    return f(m["lm_head"]) @ rms(x, m["ln_f"])

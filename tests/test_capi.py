@@ -1,4 +1,4 @@
-"""The C-ABI library loads and exports every entry point include/qdiy/attn.h
+"""The C-ABI library loads and exports every entry point include/qdiy/*.h
 declares; argument validation answers with status codes before any GPU work
 (these calls make no device allocation and launch nothing)."""
 import ctypes
@@ -8,12 +8,12 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "qdiy", "attn.h")
+HEADERS = [os.path.join(ROOT, "include", "qdiy", h) for h in ("attn.h", "decode.h", "engine.h")]
 
 
 def _declared():
-    text = open(HEADER).read()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(qd_\w+)\s*\(", text, re.M)))
+    text = "".join(open(h).read() for h in HEADERS)
+    return sorted(set(re.findall(r"^(?:int|const char\*|size_t|long long)\s+(qd_\w+)\s*\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")

@@ -1,0 +1,238 @@
+"""GPU parity of the rest of the decode step (include/qdiy/decode.h) and of the
+engine (include/qdiy/engine.h) against the oracle's restatement in the
+kernels' order (oracle/qd_oracle_model.c).
+
+Bars: every op bit-exact (fp16 outputs, argmax token); engine logits
+bit-exact and greedy token streams identical to the oracle's, up to the full
+config-5 shape (24 layers, hidden 2048, FFN 5504, vocab 151936, 128-token
+prompt, 256 generated tokens); the stdin/stdout protocol answers as the
+reference's main() does (qwen_infer.cu:743-822).
+"""
+import os
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from common import normal_f16
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def qdiy():
+    import qdiy as m
+    torch.cuda.set_device(0)
+    m.load()
+    return m
+
+
+def _g(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _same(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint16), np.asarray(b).view(np.uint16))
+
+
+@pytest.mark.parametrize("N,K", [(2048, 2048), (2048, 5504), (37, 72), (1000, 1536)])
+def test_proj_residual_bit_exact(qdiy, N, K):
+    rng = np.random.default_rng(N + K)
+    x, W, res = normal_f16(rng, K), normal_f16(rng, (N, K), 0.02), normal_f16(rng, N)
+    want = oracle.proj_residual(x, W, res, N, K)
+    out = torch.full((N + 8,), 3.0, dtype=torch.float16, device="cuda")
+    qdiy.proj_residual(_g(x), _g(W), _g(res), out, N, K)
+    got = out.cpu().numpy()
+    assert _same(got[:N], want) and np.all(got[N:] == 3.0)
+    r = _g(res)                                    # in place, as the engine adds into d_x
+    qdiy.proj_residual(_g(x), _g(W), r, r, N, K)
+    assert _same(r.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("H,I", [(2048, 5504), (512, 37), (1024, 1368)])
+def test_ffn_up_swiglu_bit_exact(qdiy, H, I):
+    rng = np.random.default_rng(H + I)
+    x, nw = normal_f16(rng, H), (1 + normal_f16(rng, H, 0.1).astype(np.float32)).astype(np.float16)
+    W1, W2 = normal_f16(rng, (I, H), 0.03), normal_f16(rng, (I, H), 0.03)
+    want = oracle.ffn_up_swiglu(x, nw, W1, W2, H, I)
+    act = torch.zeros(I, dtype=torch.float16, device="cuda")
+    qdiy.ffn_up_swiglu(_g(x), _g(nw), _g(W1), _g(W2), act, H, I)
+    assert _same(act.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("V,H", [(151936, 2048), (3001, 512), (33, 1024)])
+def test_lm_head_argmax_bit_exact(qdiy, V, H):
+    rng = np.random.default_rng(V)
+    x, nw = normal_f16(rng, H), np.ones(H, np.float16)
+    W = normal_f16(rng, (V, H), 0.02)
+    tok, want = oracle.lm_head_argmax(x, nw, W, V, H, nthreads=8)
+    logits = torch.zeros(V, dtype=torch.float16, device="cuda")
+    ws = torch.zeros(qdiy.lm_head_workspace_bytes(V) // 8, dtype=torch.int64, device="cuda")
+    token = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    qdiy.lm_head_argmax(_g(x), _g(nw), _g(W), logits, V, H, ws, token)
+    assert _same(logits.cpu().numpy(), want)
+    assert int(token.item()) == tok
+
+
+def test_lm_head_argmax_ties_zero_nan(qdiy):
+    H, V = 512, 300
+    x, nw = np.ones(H, np.float16), np.ones(H, np.float16)
+    ws = torch.zeros(qdiy.lm_head_workspace_bytes(V) // 8, dtype=torch.int64, device="cuda")
+    token = torch.zeros(1, dtype=torch.int32, device="cuda")
+    logits = torch.zeros(V, dtype=torch.float16, device="cuda")
+    cases = []
+    W = np.zeros((V, H), np.float16)
+    W[[70, 230, 41], 0] = 1.0                      # ties in different workgroups
+    cases.append((W, 41))
+    W = np.zeros((V, H), np.float16)
+    W[:, 0] = -1.0
+    W[[150, 12, 299], 0] = [0.0, -0.0, 0.0]        # -0 ties +0
+    cases.append((W, 12))
+    W = np.zeros((V, H), np.float16)
+    W[:, 0] = -2.0
+    W[5, 0], W[5, 1] = np.inf, -np.inf              # NaN logit
+    W[290, 0] = 1.0
+    cases.append((W, 290))
+    for W, want in cases:
+        qdiy.lm_head_argmax(_g(x), _g(nw), _g(W), logits, V, H, ws, token)
+        assert int(token.item()) == want
+        assert oracle.lm_head_argmax(x, nw, W, V, H)[0] == want
+
+
+def test_decode_ops_reject_bad_arguments(qdiy):
+    x = torch.zeros(2048, dtype=torch.float16, device="cuda")
+    W = torch.zeros(2048 * 2048, dtype=torch.float16, device="cuda")
+    with pytest.raises(qdiy.QdError):
+        qdiy.proj_residual(x, W, x, x, 2048, 2044)          # k_in not a multiple of 8
+    with pytest.raises(qdiy.QdError):
+        qdiy.ffn_up_swiglu(x, x, W, W, x, 2000, 4)           # hidden not a multiple of 512
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    small = torch.zeros(1, dtype=torch.int64, device="cuda")
+    with pytest.raises(qdiy.QdError):                         # workspace too small
+        qdiy.lm_head_argmax(x, x, W, x, 2048, 2048, small, tok)
+
+
+# -------------------------------------------------------------------- engine
+
+TINY = dict(vocab_size=1000, hidden_size=512, num_layers=2, num_heads=4, intermediate_size=1368,
+            max_seqlen=600)
+
+
+def _plans(qdiy, cfg, n):
+    """The engine's attention plans at lengths 1..n: its context has the same
+    heads, cache layout and device, hence the same planner decisions."""
+    with qdiy.Context(num_heads=cfg.num_heads, max_seqlen=cfg.max_seqlen,
+                      kv_row_stride=cfg.hidden_size, kv_head_stride=128) as ctx:
+        return [oracle.Plan(*ctx.plan_detail(L).as_tuple()) for L in range(1, n + 1)]
+
+
+def test_engine_tiny_matches_oracle(qdiy):
+    cfg = qdiy.model_cfg(**TINY)
+    img = qdiy.random_model_image(cfg, 21, 0.05)
+    prompt = [3, 999, 0, 500, 77, 12]
+    with qdiy.Engine(image=img) as eng:
+        got = eng.generate(prompt, 40, stop_at_eos=False)
+        got_logits = eng.logits()
+        pos = eng.prefill(prompt[:-1])                        # the same again, by hand
+        assert pos == len(prompt) - 1
+        t = eng.step(prompt[-1], pos)
+        assert t == got[0]
+        eng.reset()
+        assert eng.generate(prompt, 40, stop_at_eos=False) == got
+    want, want_logits = oracle.generate(img, prompt, 40, _plans(qdiy, cfg, len(prompt) + 40))
+    assert got == want
+    assert _same(got_logits, want_logits)
+
+
+def test_engine_long_context_split_plans(qdiy):
+    """Positions past the fused/split boundary (256 rows) and a single-token prompt."""
+    cfg = qdiy.model_cfg(**TINY)
+    img = qdiy.random_model_image(cfg, 22, 0.05)
+    prompt = [int(t) for t in np.random.default_rng(1).integers(0, 1000, 300)]
+    with qdiy.Engine(image=img) as eng:
+        got = eng.generate(prompt, 8, stop_at_eos=False)
+        lg = eng.logits()
+        one = eng.generate([17], 5, stop_at_eos=False)
+    want, wl = oracle.generate(img, prompt, 8, _plans(qdiy, cfg, 308))
+    assert got == want and _same(lg, wl)
+    assert one == oracle.generate(img, [17], 5, _plans(qdiy, cfg, 6))[0]
+
+
+def test_engine_rejects_bad_input(qdiy, tmp_path):
+    cfg = qdiy.model_cfg(**TINY)
+    img = qdiy.random_model_image(cfg, 23)
+    with pytest.raises(qdiy.QdError):
+        qdiy.Engine(image=img[:-2])                           # truncated
+    bad = img.copy()
+    bad[0] ^= 1                                               # magic
+    with pytest.raises(qdiy.QdError):
+        qdiy.Engine(image=bad)
+    with pytest.raises(qdiy.QdError):
+        qdiy.Engine(path=str(tmp_path / "missing.bin"))
+    with qdiy.Engine(image=img) as eng:
+        with pytest.raises(qdiy.QdError):
+            eng.step(1000, 0)                                 # token outside the vocabulary
+        with pytest.raises(qdiy.QdError):
+            eng.step(1, 600)                                  # pos == max_seqlen
+
+
+def test_engine_cli_protocol(qdiy, tmp_path):
+    """qdiy_engine speaks web_chat/app.py's protocol: [ENGINE_READY], reset ->
+    [RESET_DONE], a prompt line -> [GENERATION_START], token lines,
+    [GENERATION_END]; at most 512 tokens; exit ends the process."""
+    cfg = qdiy.model_cfg(**TINY)
+    path = str(tmp_path / "tiny.bin")
+    qdiy.write_random_model(path, cfg, 24, 0.05)
+    with qdiy.Engine(path=path) as eng:
+        want_a = eng.generate([5, 6, 7], 512)
+        want_b = eng.generate([9], 512)
+    env = dict(os.environ)
+    proc = subprocess.run([qdiy.ENGINE_EXE, path], input="reset\n5 6 7\n9\nexit\n",
+                          capture_output=True, text=True, timeout=240, env=env)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    lines = [ln.strip() for ln in proc.stdout.splitlines() if ln.strip()]
+    i = next(k for k, ln in enumerate(lines) if "[ENGINE_READY]" in ln)
+    rest = lines[i + 1:]
+    assert rest[0] == "[RESET_DONE]"
+    blocks, cur = [], None
+    for ln in rest[1:]:
+        if ln == "[GENERATION_START]":
+            cur = []
+        elif ln == "[GENERATION_END]":
+            blocks.append(cur)
+            cur = None
+        else:
+            cur.append(int(ln))
+    assert blocks == [want_a, want_b]
+    assert len(want_a) == 512
+
+
+@pytest.mark.timeout(900)
+def test_config5_greedy_tokens_identical(qdiy):
+    """Config 5: random-init Qwen-1.8B shape, 128 uniform-random prompt ids, 256
+    greedy tokens; the GPU stream and last logits equal the oracle's."""
+    cfg = qdiy.model_cfg(max_seqlen=512)
+    img = qdiy.random_model_image(cfg, 5, 0.02, nthreads=16)
+    prompt = [int(t) for t in np.random.default_rng(5).integers(0, cfg.vocab_size, 128)]
+    with qdiy.Engine(image=img) as eng:
+        got = eng.generate(prompt, 256, stop_at_eos=False)
+        lg = eng.logits()
+    print(f"\n[config5] GPU generated {len(got)} tokens; first 8 {got[:8]}", flush=True)
+    plans = _plans(qdiy, cfg, 384)
+    m = oracle.Model(img, 384, nthreads=min(16, os.cpu_count() or 1))
+    for pos, tok in enumerate(prompt[:-1]):
+        m.forward(tok, pos, plans[pos], want_logits=False)
+        if pos % 32 == 31:
+            print(f"[config5] oracle prompt position {pos + 1}/127", flush=True)
+    last, pos = prompt[-1], len(prompt) - 1
+    for i in range(256):
+        nxt, wl = m.forward(last, pos, plans[pos])
+        assert nxt == got[i], f"token {i}: oracle {nxt}, GPU {got[i]}"
+        last, pos = nxt, pos + 1
+        if i % 32 == 31:
+            print(f"[config5] oracle token {i + 1}/256 matches", flush=True)
+    m.close()
+    assert _same(lg, wl)
