@@ -46,7 +46,8 @@ extern "C" {
 #endif
 
 /* out[n] = half(residual[n] + half(sum_k W[n][k] * x[k])) for n < n_out.
- * W is [n_out][k_in] fp16; k_in a multiple of 8; x, w 16-byte aligned.
+ * W is [n_out][k_in] fp16; k_in a multiple of 8, at most 8192; x, w 16-byte
+ * aligned.
  * residual and out may be the same buffer (the reference adds in place into
  * d_x).  Replaces hgemv_kernel + add_bias_kernel (hgemm_final.cuh:274-295,
  * bias.cuh:6-11; qwen_infer.cu:701-704 and :718-721). */

@@ -45,7 +45,7 @@ typedef struct qd_model_cfg {
   uint32_t hidden_size;        /* num_heads * 128, a multiple of 512, <= 4096 */
   uint32_t num_layers;
   uint32_t num_heads;
-  uint32_t intermediate_size;  /* a multiple of 8 */
+  uint32_t intermediate_size;  /* a multiple of 8, at most 8192 */
   uint32_t max_seqlen;
 } qd_model_cfg;
 

@@ -31,25 +31,29 @@ namespace {
 
 constexpr float kLog2e = 1.44269504088896340736f;
 
-// x (optionally RMS-normalised) for this lane's elements k = 512*j + 8*l + e.
-// The normalisation (rmsnorm.cuh:6-57) is x * (1 / sqrt(sum(x^2) / n + eps))
-// * w with the sum of squares in the wave64 order, correctly rounded sqrt and
+// This lane's x elements k = 512*j + 8*l + e, and the RMSNorm weights when
+// norm_w is non-null.  Issued before a kernel's weight loads: x and norm_w are
+// small and L2-resident, so the normalisation below waits only for them while
+// the weight rows are still in flight (loads complete in issue order).
+template <int NJ>
+__device__ __forceinline__ void issue_input(const uint16_t* __restrict__ x,
+                                            const uint16_t* __restrict__ norm_w, int lane,
+                                            f16x8 (&xv)[NJ], f16x8 (&nv)[NJ]) {
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) xv[j] = *reinterpret_cast<const f16x8*>(x + 512 * j + 8 * lane);
+  if (norm_w == nullptr) return;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) nv[j] = *reinterpret_cast<const f16x8*>(norm_w + 512 * j + 8 * lane);
+}
+
+// RMSNorm in place (rmsnorm.cuh:6-57): x * (1 / sqrt(sum(x^2) / n + eps)) * w
+// with the sum of squares in the wave64 order, correctly rounded sqrt and
 // divide, each product rounded to fp32 and the result to fp16.  (HIP's
 // __fsqrt_rn is the native v_sqrt_f32, not correctly rounded; sqrtf and '/'
 // are, by hipcc's default -fhip-fp32-correctly-rounded-divide-sqrt.)
 template <int NJ>
-__device__ __forceinline__ void load_input(const uint16_t* __restrict__ x,
-                                           const uint16_t* __restrict__ norm_w, float eps,
-                                           int lane, f16x8 (&xv)[NJ]) {
-  const int hidden = NJ * 512;
-#pragma unroll
-  for (int j = 0; j < NJ; ++j)
-    xv[j] = *reinterpret_cast<const f16x8*>(x + 512 * j + 8 * lane);
-  if (norm_w == nullptr) return;
-  f16x8 wv[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j)
-    wv[j] = *reinterpret_cast<const f16x8*>(norm_w + 512 * j + 8 * lane);
+__device__ __forceinline__ void normalise(f16x8 (&xv)[NJ], const f16x8 (&nv)[NJ], float eps) {
+  constexpr int hidden = NJ * 512;
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
@@ -63,42 +67,39 @@ __device__ __forceinline__ void load_input(const uint16_t* __restrict__ x,
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-#pragma clang fp contract(off)
-      xv[j][e] = to_f16(((float)xv[j][e] * r) * (float)wv[j][e]);
-    }
+    for (int e = 0; e < 8; ++e) xv[j][e] = to_f16(((float)xv[j][e] * r) * (float)nv[j][e]);
 }
 
+// Non-temporal loads of this lane's chunks of a weight row (read once).
 template <int NJ>
-__device__ __forceinline__ float row_dot(const uint16_t* __restrict__ w_row, int lane,
-                                         const f16x8 (&xv)[NJ]) {
-  f16x8 wv[NJ];
+__device__ __forceinline__ void issue_row(const uint16_t* __restrict__ w_row, int lane,
+                                          f16x8 (&wv)[NJ]) {
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
     wv[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(w_row + 512 * j + 8 * lane));
+}
+
+// This lane's sequential sum over (j, e) of exact fp16 products.
+template <int NJ>
+__device__ __forceinline__ float lane_sum(const f16x8 (&wv)[NJ], const f16x8 (&xv)[NJ]) {
   float acc = 0.0f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e)   // exact product: the fmaf rounds only the sum
       acc = __builtin_fmaf((float)wv[j][e], (float)xv[j][e], acc);
-  return wave64_sum(acc);
+  return acc;
 }
 
 // Bias, rotate-half RoPE and cache append for pair (h, i), evaluated as
 // written (each product and sum rounded; no contraction), on the six GEMV
 // outputs y = {q1, q2, k1, k2, v1, v2}.
 __device__ __forceinline__ void qkv_front_epilogue(const QkvFrontParams& p, int h, int i,
-                                                   int hidden, const _Float16* y) {
-#pragma clang fp contract(off)
+                                                   int hidden, const _Float16* y,
+                                                   const _Float16 (&bias6)[6], float2 cs) {
   _Float16 v6[6];
 #pragma unroll
-  for (int r = 0; r < 6; ++r) {
-    const int n = (r >> 1) * hidden + h * 128 + i + (r & 1) * 64;
-    v6[r] = p.bias ? (_Float16)((float)y[r] + (float)reinterpret_cast<const _Float16*>(p.bias)[n])
-                   : y[r];
-  }
-  const float2 cs = p.rope_cs[p.pos * 64 + i];
+  for (int r = 0; r < 6; ++r) v6[r] = p.bias ? (_Float16)((float)y[r] + (float)bias6[r]) : y[r];
   const float q1 = (float)v6[0], q2 = (float)v6[1], k1 = (float)v6[2], k2 = (float)v6[3];
   const float q1c = q1 * cs.x, q2s = q2 * cs.y, q2c = q2 * cs.x, q1s = q1 * cs.y;
   const float k1c = k1 * cs.x, k2s = k2 * cs.y, k2c = k2 * cs.x, k1s = k1 * cs.y;
@@ -129,57 +130,56 @@ __global__ __launch_bounds__(384) void qkv_front_kernel(QkvFrontParams p) {
   const int hidden = NJ * 512;
   const int row = (wave >> 1) * hidden + h * 128 + i + (wave & 1) * 64;
 
-  f16x8 xv[NJ];
-  load_input<NJ>(p.x, p.norm_w, p.eps, lane, xv);
-  const float acc = row_dot<NJ>(p.w + (long long)row * hidden, lane, xv);
+  // the epilogue's operands, fetched at the start so their latency overlaps the GEMV
+  _Float16 bias6[6] = {};
+  float2 cs = {0.0f, 0.0f};
+  if (threadIdx.x == 0) {
+    cs = p.rope_cs[p.pos * 64 + i];
+    if (p.bias) {
+#pragma unroll
+      for (int r = 0; r < 6; ++r)
+        bias6[r] = reinterpret_cast<const _Float16*>(p.bias)[(r >> 1) * hidden + h * 128 + i + (r & 1) * 64];
+    }
+  }
+  f16x8 xv[NJ], nv[NJ], wv[NJ];
+  issue_input<NJ>(p.x, p.norm_w, lane, xv, nv);
+  issue_row<NJ>(p.w + (long long)row * hidden, lane, wv);
+  __builtin_amdgcn_sched_barrier(0);
+  if (p.norm_w) normalise<NJ>(xv, nv, p.eps);
+  const float acc = wave64_sum(lane_sum<NJ>(wv, xv));
   if (lane == 0) y[wave] = to_f16(acc);       // hgemv's half output
   __syncthreads();
-  if (threadIdx.x == 0) qkv_front_epilogue(p, h, i, hidden, y);
+  if (threadIdx.x == 0) qkv_front_epilogue(p, h, i, hidden, y, bias6, cs);
 }
 
-// This lane's sequential sum of x[k] * w_row[k] over k = 512*j + 8*lane + e
-// (j ascending, e ascending, k < K; K a multiple of 8); the caller adds the
-// lanes with wave64_sum.  Four 512-element chunks are loaded at a time.
-__device__ __forceinline__ float lane_dot(const uint16_t* __restrict__ w_row,
-                                          const uint16_t* __restrict__ x, int lane, int K) {
-  float acc = 0.0f;
-  const int nfull = K >> 9;
-  int j = 0;
-  for (; j + 4 <= nfull; j += 4) {
-    f16x8 wv[4], xv[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      wv[q] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(w_row + 512 * (j + q) + 8 * lane));
-      xv[q] = *reinterpret_cast<const f16x8*>(x + 512 * (j + q) + 8 * lane);
-    }
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)wv[q][e], (float)xv[q][e], acc);
-  }
-  for (; j < nfull; ++j) {
-    const f16x8 wv = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(w_row + 512 * j + 8 * lane));
-    const f16x8 xv = *reinterpret_cast<const f16x8*>(x + 512 * j + 8 * lane);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)wv[e], (float)xv[e], acc);
-  }
-  if (8 * lane < K - (nfull << 9)) {
-    const f16x8 wv = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(w_row + 512 * nfull + 8 * lane));
-    const f16x8 xv = *reinterpret_cast<const f16x8*>(x + 512 * nfull + 8 * lane);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)wv[e], (float)xv[e], acc);
-  }
-  return acc;
-}
-
-// Output projection + residual add (qwen_infer.cu:701-704 and :717-720:
+// Output projection + residual add (qwen_infer.cu:701-704 and :718-721:
 // hgemv into a half buffer, then add_bias_kernel onto d_x).  One wave per
-// output row, four waves per workgroup.
+// output row, four waves per workgroup.  NJ = ceil(k_in / 512) chunks per lane
+// are all in flight at once; in the last chunk only lanes with 8*lane <
+// k_in - 512*(NJ-1) hold elements (the others skip it, they do not add zeros).
+template <int NJ>
 __global__ __launch_bounds__(256) void proj_residual_kernel(ProjResidualParams p) {
   const int lane = threadIdx.x & 63;
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (n >= p.n_out) return;                    // whole wave
-  const float s = wave64_sum(lane_dot(p.w + (long long)n * p.k_in, p.x, lane, p.k_in));
+  const int K = p.k_in;
+  const bool tail = 8 * lane < K - 512 * (NJ - 1);
+  const uint16_t* w_row = p.w + (long long)n * K;
+  f16x8 xv[NJ], wv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (j < NJ - 1 || tail) {
+      xv[j] = *reinterpret_cast<const f16x8*>(p.x + 512 * j + 8 * lane);
+      wv[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(w_row + 512 * j + 8 * lane));
+    }
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    if (j < NJ - 1 || tail)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)wv[j][e], (float)xv[j][e], acc);
+  const float s = wave64_sum(acc);
   if (lane == 0) {
     const _Float16 y = to_f16(s);              // hgemv's half output
     reinterpret_cast<_Float16*>(p.out)[n] =
@@ -197,16 +197,12 @@ __global__ __launch_bounds__(256) void ffn_up_kernel(FfnUpParams p) {
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (i >= p.inter) return;                    // whole wave
   constexpr int hidden = NJ * 512;
-  f16x8 xv[NJ];
-  load_input<NJ>(p.x, p.norm_w, p.eps, lane, xv);
-  const uint16_t* r1 = p.w1 + (long long)i * hidden;
-  const uint16_t* r2 = p.w2 + (long long)i * hidden;
-  f16x8 a[NJ], b[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; ++j) {
-    a[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(r1 + 512 * j + 8 * lane));
-    b[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(r2 + 512 * j + 8 * lane));
-  }
+  f16x8 xv[NJ], nv[NJ], a[NJ], b[NJ];
+  issue_input<NJ>(p.x, p.norm_w, lane, xv, nv);
+  issue_row<NJ>(p.w1 + (long long)i * hidden, lane, a);
+  issue_row<NJ>(p.w2 + (long long)i * hidden, lane, b);
+  __builtin_amdgcn_sched_barrier(0);
+  normalise<NJ>(xv, nv, p.eps);
   float ga = 0.0f, ua = 0.0f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
@@ -252,17 +248,18 @@ __global__ __launch_bounds__(kLmWaves * 64) void lm_head_kernel(LmHeadParams p) 
   const int row0 = (blockIdx.x * kLmWaves + wave) * kLmRowsPerWave;
   unsigned long long key = 0ull;
   if (row0 < p.vocab) {
-    f16x8 xv[NJ];
-    load_input<NJ>(p.x, p.norm_w, p.eps, lane, xv);
+    f16x8 xv[NJ], nv[NJ];
+    issue_input<NJ>(p.x, p.norm_w, lane, xv, nv);
 #pragma unroll
     for (int r = 0; r < kLmRowsPerWave; r += 2) {
       const int ra = min(row0 + r, p.vocab - 1);
       const int rb = min(row0 + r + 1, p.vocab - 1);
       f16x8 a[NJ], b[NJ];
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        a[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p.w + (long long)ra * hidden + 512 * j + 8 * lane));
-        b[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p.w + (long long)rb * hidden + 512 * j + 8 * lane));
+      issue_row<NJ>(p.w + (long long)ra * hidden, lane, a);
+      issue_row<NJ>(p.w + (long long)rb * hidden, lane, b);
+      if (r == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        normalise<NJ>(xv, nv, p.eps);
       }
       float sa = 0.0f, sb = 0.0f;
 #pragma unroll
@@ -341,7 +338,16 @@ hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream) {
 namespace qd {
 
 hipError_t launch_proj_residual(const ProjResidualParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL(proj_residual_kernel, dim3((p.n_out + 3) / 4), dim3(256), 0, stream, p);
+  const dim3 grid((p.n_out + 3) / 4), block(256);
+  switch ((p.k_in + 511) / 512) {
+#define QD_PROJ_CASE(n) \
+    case n: hipLaunchKernelGGL(proj_residual_kernel<n>, grid, block, 0, stream, p); break;
+    QD_PROJ_CASE(1) QD_PROJ_CASE(2) QD_PROJ_CASE(3) QD_PROJ_CASE(4) QD_PROJ_CASE(5) QD_PROJ_CASE(6)
+    QD_PROJ_CASE(7) QD_PROJ_CASE(8) QD_PROJ_CASE(9) QD_PROJ_CASE(10) QD_PROJ_CASE(11)
+    QD_PROJ_CASE(12) QD_PROJ_CASE(13) QD_PROJ_CASE(14) QD_PROJ_CASE(15) QD_PROJ_CASE(16)
+#undef QD_PROJ_CASE
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -45,7 +45,7 @@ bool cfg_valid(const qd_model_cfg* c) {
          c->hidden_size == c->num_heads * (uint32_t)QD_HEAD_DIM && c->hidden_size % 512 == 0 &&
          c->hidden_size <= 4096 && c->intermediate_size >= 8 && c->intermediate_size % 8 == 0 &&
          c->max_seqlen >= 1 && c->vocab_size < (1u << 30) && c->num_layers <= 4096 &&
-         c->intermediate_size <= (1u << 20);
+         c->intermediate_size <= 8192;
 }
 
 ModelLayout layout_of(const qd_model_cfg& c) {
@@ -213,7 +213,8 @@ int qd_proj_residual(const uint16_t* x, const uint16_t* w, const uint16_t* resid
   if (!aligned16(x) || !aligned16(w)) return fail(QD_EINVAL, "x and w must be 16-byte aligned");
   if (!aligned2(residual) || !aligned2(out)) return fail(QD_EINVAL, "residual and out must be 2-byte aligned");
   if (n_out < 1) return fail(QD_EINVAL, "n_out %d must be >= 1", n_out);
-  if (k_in < 8 || k_in % 8 != 0) return fail(QD_EINVAL, "k_in %d must be a positive multiple of 8", k_in);
+  if (k_in < 8 || k_in % 8 != 0 || k_in > 8192)
+    return fail(QD_EINVAL, "k_in %d must be a multiple of 8 in [8, 8192]", k_in);
   qd::ProjResidualParams p{x, w, residual, out, n_out, k_in};
   hipError_t e = qd::launch_proj_residual(p, stream);
   return e == hipSuccess ? QD_OK : hip_fail(e, "proj_residual launch");
