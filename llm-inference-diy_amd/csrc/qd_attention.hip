@@ -207,10 +207,13 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
   const int t = lane & 15;
   const int h = blockIdx.x % p.num_heads;
   const int c = blockIdx.x / p.num_heads;
-  const int r0 = c * p.rows_per_split;
-  const int nrows = min(p.seqlen - r0, p.rows_per_split);
+  const int b = blockIdx.y;                   // query of a batched fused call, else 0
+  const int seqlen = p.seqlen + b;
+  const int rows_per_split = kSplit ? p.rows_per_split : seqlen;
+  const int r0 = c * rows_per_split;
+  const int nrows = min(seqlen - r0, rows_per_split);
 
-  const f16x8 qv = *reinterpret_cast<const f16x8*>(p.q + h * kD + t * 8);
+  const f16x8 qv = *reinterpret_cast<const f16x8*>(p.q + b * p.q_batch_stride + h * kD + t * 8);
   const long long off = h * p.head_stride + (long long)r0 * p.row_stride;
   GroupState st;
   init_state(st);
@@ -244,7 +247,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
       p.part_o[slot * kD + tid] = O;
       if (tid == 0) p.part_ml[slot] = float2{M, L};
     } else {
-      reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = to_f16(O / L);
+      reinterpret_cast<_Float16*>(p.out + b * p.out_batch_stride)[h * kD + tid] = to_f16(O / L);
     }
   }
 }
@@ -339,6 +342,12 @@ static void launch_scan(const AttnParams& p, int rows_per_tile, dim3 grid, hipSt
       hipLaunchKernelGGL((decode_attention_scan_kernel<NW, 2, kSplit>), grid, dim3(NW * 64), 0, stream, p);
       break;
   }
+}
+
+hipError_t launch_decode_attention_fused_batch(const AttnParams& p, int tokens, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_attention_scan_kernel<16, 4, false>), dim3(p.num_heads, tokens),
+                     dim3(16 * 64), 0, stream, p);
+  return hipGetLastError();
 }
 
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream) {

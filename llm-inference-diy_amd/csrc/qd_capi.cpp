@@ -1,5 +1,6 @@
 // C ABI of the decode-attention hot path: context lifetime, argument checks,
 // launch planning.  Declared in include/qdiy/attn.h.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -119,6 +120,8 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.splits = plan.splits;
   p.rows_per_split = plan.rows_per_split;
   p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));  // log2(e)/sqrt(128)
+  p.q_batch_stride = 0;
+  p.out_batch_stride = 0;
   return p;
 }
 
@@ -132,6 +135,35 @@ int run_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint1
 }
 
 }  // namespace
+
+namespace qd {
+
+int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k,
+                      const uint16_t* v, uint16_t* out, long long out_stride, int pos0, int tokens,
+                      hipStream_t stream) {
+  if (tokens < 1) return QD_OK;
+  int rc = check_attention_args(ctx, q, k, v, out, pos0 + 1, ctx ? ctx->cfg.num_heads : 0, QD_HEAD_DIM);
+  if (rc != QD_OK) return rc;
+  if (pos0 + tokens > ctx->cfg.max_seqlen)
+    return fail(QD_EINVAL, "positions up to %d exceed max_seqlen %d", pos0 + tokens, ctx->cfg.max_seqlen);
+  // queries whose length plan_auto makes fused: one launch for all of them
+  const int n_fused = std::max(0, std::min(tokens, kFusedMaxRows - pos0));
+  if (n_fused > 0) {
+    qd::AttnParams p = make_params(ctx, q, k, v, out, pos0 + 1, plan_fused(pos0 + 1));
+    p.q_batch_stride = q_stride;
+    p.out_batch_stride = out_stride;
+    const hipError_t e = qd::launch_decode_attention_fused_batch(p, n_fused, stream);
+    if (e != hipSuccess) return hip_fail(e, "batched fused attention launch");
+  }
+  for (int t = n_fused; t < tokens; ++t) {
+    rc = run_attention(ctx, q + t * q_stride, k, v, out + t * out_stride, pos0 + t + 1,
+                       plan_auto(ctx, pos0 + t + 1), stream);
+    if (rc != QD_OK) return rc;
+  }
+  return QD_OK;
+}
+
+}  // namespace qd
 
 extern "C" {
 

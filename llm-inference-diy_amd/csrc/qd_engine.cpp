@@ -115,6 +115,7 @@ void fill_range(uint16_t* t, long long begin, long long end, uint64_t seed, floa
 }
 
 constexpr float kEps = 1e-6f;      // qwen_infer.cu:620
+constexpr int kPrefillChunk = 256; // prompt tokens per batched prefill pass
 constexpr int kEosA = 151645;      // <|im_end|>, qwen_infer.cu:801
 constexpr int kEosB = 151643;      // <|endoftext|>
 
@@ -139,6 +140,10 @@ struct qd_engine {
   int* d_token = nullptr;
   int* h_token = nullptr;               // pinned
   long long kv_bytes = 0;
+  // batched prefill scratch, kPrefillChunk tokens
+  int* p_tokens = nullptr;
+  uint16_t *p_x = nullptr, *p_xn = nullptr, *p_qkv = nullptr, *p_att = nullptr;
+  uint16_t *p_g = nullptr, *p_u = nullptr, *p_act = nullptr;
 
   const uint16_t* w(long long off) const { return weights + off; }
   uint16_t* kc(int l) const { return k_cache + (long long)l * cfg.max_seqlen * cfg.hidden_size; }
@@ -163,6 +168,9 @@ void engine_free(qd_engine* e) {
   (void)hipFree(e->logits);
   (void)hipFree(e->lm_ws);
   (void)hipFree(e->d_token);
+  for (void* q : {(void*)e->p_tokens, (void*)e->p_x, (void*)e->p_xn, (void*)e->p_qkv, (void*)e->p_att,
+                  (void*)e->p_g, (void*)e->p_u, (void*)e->p_act})
+    (void)hipFree(q);
   if (e->h_token) (void)hipHostFree(e->h_token);
   if (e->attn) qd_ctx_destroy(e->attn);
   if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -191,6 +199,42 @@ int run_layers(qd_engine* e, int token, int pos) {
     xin = e->x;
   }
   return QD_OK;
+}
+
+// Prompt tokens at positions pos0.. through all layers in batches, in the
+// decode kernels' arithmetic (qd_prefill.hip): the KV rows written are
+// bit-identical to run_layers() token by token.
+int prefill_batched(qd_engine* e, const int* tokens, int T, int pos0) {
+  const qd_model_cfg& c = e->cfg;
+  const int H = (int)c.hidden_size, I = (int)c.intermediate_size, NH = (int)c.num_heads;
+  hipError_t he = hipMemcpyAsync(e->p_tokens, tokens, sizeof(int) * (size_t)T, hipMemcpyHostToDevice,
+                                 e->stream);
+  if (he == hipSuccess) he = qd::launch_embed(e->w(e->lay.wte), e->p_tokens, e->p_x, H, T, e->stream);
+  auto gemv = [&](const uint16_t* x, long long ldx, const uint16_t* w, int n, int k, uint16_t* y,
+                  long long ldy, int epi) {
+    qd::BatchedGemvParams p{x, ldx, w, n, k, T, y, ldy, y};
+    return qd::launch_gemv_batched(p, epi, e->stream);
+  };
+  for (uint32_t l = 0; l < c.num_layers && he == hipSuccess; ++l) {
+    const LayerOff& f = e->lay.layers[l];
+    he = qd::launch_rmsnorm_batched(e->p_x, e->w(f.ln_1), kEps, e->p_xn, H, T, e->stream);
+    if (he == hipSuccess) he = gemv(e->p_xn, H, e->w(f.qkv_w), 3 * H, H, e->p_qkv, 3 * H, 0);
+    if (he == hipSuccess)
+      he = qd::launch_rope_batched(e->p_qkv, e->w(f.qkv_b), e->kc(l), e->vc(l), e->attn->rope_cs,
+                                   e->attn->cfg.kv_row_stride, e->attn->cfg.kv_head_stride, pos0, NH,
+                                   T, e->stream);
+    if (he != hipSuccess) break;
+    const int rc = qd::attention_prefill(e->attn, e->p_qkv, 3 * H, e->kc(l), e->vc(l), e->p_att, H,
+                                         pos0, T, e->stream);
+    if (rc != QD_OK) return rc;
+    he = gemv(e->p_att, H, e->w(f.proj_w), H, H, e->p_x, H, 1);
+    if (he == hipSuccess) he = qd::launch_rmsnorm_batched(e->p_x, e->w(f.ln_2), kEps, e->p_xn, H, T, e->stream);
+    if (he == hipSuccess) he = gemv(e->p_xn, H, e->w(f.w1), I, H, e->p_g, I, 0);
+    if (he == hipSuccess) he = gemv(e->p_xn, H, e->w(f.w2), I, H, e->p_u, I, 0);
+    if (he == hipSuccess) he = qd::launch_swiglu_batched(e->p_g, e->p_u, e->p_act, (long long)T * I, e->stream);
+    if (he == hipSuccess) he = gemv(e->p_act, I, e->w(f.w_down), H, I, e->p_x, H, 1);
+  }
+  return he == hipSuccess ? QD_OK : hip_fail(he, "prefill launch");
 }
 
 int check_engine(const qd_engine* e) {
@@ -361,7 +405,15 @@ int qd_engine_create_from_image(const void* image, long long bytes, qd_engine** 
       {(void**)&e->weights, wbytes},  {(void**)&e->k_cache, e->kv_bytes}, {(void**)&e->v_cache, e->kv_bytes},
       {(void**)&e->x, H * 2},         {(void**)&e->qkv, 3 * H * 2},     {(void**)&e->attn_out, H * 2},
       {(void**)&e->act, I * 2},       {(void**)&e->logits, V * 2},      {&e->lm_ws, (long long)e->lm_ws_bytes},
-      {(void**)&e->d_token, 4}};
+      {(void**)&e->d_token, 4},
+      {(void**)&e->p_tokens, (long long)kPrefillChunk * 4},
+      {(void**)&e->p_x, (long long)kPrefillChunk * H * 2},
+      {(void**)&e->p_xn, (long long)kPrefillChunk * H * 2},
+      {(void**)&e->p_qkv, (long long)kPrefillChunk * 3 * H * 2},
+      {(void**)&e->p_att, (long long)kPrefillChunk * H * 2},
+      {(void**)&e->p_g, (long long)kPrefillChunk * I * 2},
+      {(void**)&e->p_u, (long long)kPrefillChunk * I * 2},
+      {(void**)&e->p_act, (long long)kPrefillChunk * I * 2}};
   for (auto& a : allocs) {
     if ((he = hipMalloc(a.p, (size_t)a.n)) != hipSuccess) {
       engine_free(e);
@@ -441,8 +493,13 @@ int qd_engine_prefill(qd_engine* e, const int* tokens, int n, int* pos) {
   for (int i = 0; i < n; ++i)
     if (tokens[i] < 0 || (uint32_t)tokens[i] >= e->cfg.vocab_size)
       return fail(QD_EINVAL, "token %d outside [0, %u)", tokens[i], e->cfg.vocab_size);
-  for (int i = 0; i < n; ++i)
-    if ((rc = run_layers(e, tokens[i], *pos + i)) != QD_OK) return rc;
+  for (int i = 0; i < n; i += kPrefillChunk) {
+    const int T = std::min(kPrefillChunk, n - i);
+    if ((rc = prefill_batched(e, tokens + i, T, *pos + i)) != QD_OK) return rc;
+    // the token upload of the next chunk reuses p_tokens: finish this chunk first
+    hipError_t he = hipStreamSynchronize(e->stream);
+    if (he != hipSuccess) return hip_fail(he, "prefill");
+  }
   hipError_t he = hipStreamSynchronize(e->stream);
   if (he != hipSuccess) return hip_fail(he, "prefill");
   *pos += n;

@@ -29,6 +29,11 @@ struct AttnParams {
   int splits;             // workgroups per head
   int rows_per_split;
   float scale_log2;       // log2(e) / sqrt(128)
+  // Batched single-workgroup-per-head calls (prefill): grid.y = tokens; token b
+  // reads q + b*q_batch_stride, writes out + b*out_batch_stride and attends
+  // over seqlen + b rows.  Zero strides and grid.y = 1 for a single call.
+  long long q_batch_stride;
+  long long out_batch_stride;
 };
 
 struct RopeParams {
@@ -107,6 +112,22 @@ inline int lm_head_parts(int vocab) {
   return (vocab + rows - 1) / rows;
 }
 
+// Batched GEMV of the prefill: Y[t][n] = sum_k X[t][k] W[n][k] for t < t_count,
+// n < n, in the decode kernels' summation order; X rows ldx elements apart, Y
+// (and the residual R, read at the same offsets) ldy apart.  k a multiple of 8,
+// at most 8192.
+struct BatchedGemvParams {
+  const uint16_t* x;
+  long long ldx;
+  const uint16_t* w;
+  int n;
+  int k;
+  int t;
+  uint16_t* y;
+  long long ldy;
+  const uint16_t* res;    // epilogue 1 only
+};
+
 // Launch plan of one decode-attention call.
 struct AttnPlan {
   int variant;            // 0 fused, 1 split
@@ -123,6 +144,10 @@ int hip_fail(hipError_t e, const char* what);
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream);
+// Fused (one 16-wave workgroup per head, 4-row tiles) attention of `tokens`
+// queries at once, token b over p.seqlen + b rows: the arithmetic of the fused
+// plan of qd_decode_attention, query by query.
+hipError_t launch_decode_attention_fused_batch(const AttnParams& p, int tokens, hipStream_t stream);
 hipError_t launch_qkv_bias_rope_cache(const RopeParams& p, hipStream_t stream);
 hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream);
 hipError_t launch_proj_residual(const ProjResidualParams& p, hipStream_t stream);
@@ -130,6 +155,32 @@ hipError_t launch_ffn_up(const FfnUpParams& p, hipStream_t stream);
 // lm_head kernel, then the one-workgroup reduction of its keys into *token.
 hipError_t launch_lm_head_argmax(const LmHeadParams& p, int* token, hipStream_t stream);
 
+// Prefill kernels (qd_prefill.hip).  epi 0: Y = half(sum); epi 1: Y = half(R + half(sum)).
+hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float eps, uint16_t* xn,
+                                  int hidden, int T, hipStream_t stream);
+hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t stream);
+hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_layer,
+                               uint16_t* v_layer, const float2* rope_cs, long long row_stride,
+                               long long head_stride, int pos0, int num_heads, int T,
+                               hipStream_t stream);
+hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t* act, long long n,
+                                 hipStream_t stream);
+hipError_t launch_embed(const uint16_t* wte, const int* tokens, uint16_t* x, int hidden, int T,
+                        hipStream_t stream);
+
+}  // namespace qd
+
+struct qd_ctx;
+
+namespace qd {
+// Attention of `tokens` consecutive queries at positions pos0, pos0 + 1, ...
+// (query t over pos0 + t + 1 rows; q and out rows q_stride / out_stride
+// elements apart), each with the arithmetic of qd_decode_attention's own plan
+// for its length: the fused-plan queries in one batched launch, the others one
+// call each.
+int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k,
+                      const uint16_t* v, uint16_t* out, long long out_stride, int pos0, int tokens,
+                      hipStream_t stream);
 }  // namespace qd
 
 struct qd_ctx {

@@ -1,0 +1,288 @@
+// Batched prompt processing (prefill) for gfx950 in the decode step's exact
+// arithmetic.
+//
+// Role: QwenEngine::prefill (framework_src/qwen_infer.cu:372-611) runs the
+// prompt's tokens 0..N-2 through the layers at once to fill the KV cache.  The
+// reference does it with MMA GEMMs and FlashAttention, whose summation order
+// differs from its own decode step.  Here every output of every token is the
+// same fp32 sum, in the same order, as the single-token decode kernels compute
+// (lane l of a 64-lane wave adds k = 512j + 8l + e sequentially, then the fixed
+// wave64 tree), so the KV cache a prompt leaves is bit-identical to feeding the
+// tokens one by one, and greedy decoding after a prompt stays reproducible on
+// the host.  The GEMMs therefore run on the FMA pipes, not MFMA (whose internal
+// summation order is not specified): each weight row is read from memory once
+// per group of tokens and kept in registers while the tokens stream through LDS.
+//
+// Kernels (per layer, T tokens):
+//   rmsnorm_batched_kernel     T waves: xn[t] = RMSNorm(x[t]) * w
+//   gemv_batched_kernel        Y[t][n] = sum_k X[t][k] W[n][k], with an epilogue
+//                              (store as half, or residual add into the stream)
+//   rope_batched_kernel        bias + RoPE + KV append per token (qd_rope_cache)
+//   swiglu_batched_kernel      act = half(g * (u / (1 + exp(-u))))
+// Attention runs per token with qd_decode_attention's plan for that length.
+#include "qd_device.h"
+#include "qd_internal.h"
+
+namespace qd {
+namespace {
+
+constexpr float kLog2e = 1.44269504088896340736f;
+
+// Tokens per workgroup of the batched GEMV; tokens per LDS tile (up to 8, so
+// that a tile of NJ * 512 fp16 elements per token stays within 64 KB).
+constexpr int kTokPerWg = 32;
+constexpr int kGemvWaves = 8;           // two rows per wave: 16 rows per workgroup
+constexpr int tok_tile(int nj) { return nj <= 8 ? 8 : 64 / nj; }
+
+// One wave per token: the same normalisation as the decode kernels' normalise()
+// (qd_decode_ops.hip), written out as fp16.
+template <int NJ>
+__global__ __launch_bounds__(256) void rmsnorm_batched_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ w,
+                                                             float eps, uint16_t* __restrict__ xn,
+                                                             int T) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  constexpr int hidden = NJ * 512;
+  const uint16_t* xr = x + (long long)t * hidden;
+  f16x8 xv[NJ], nv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    xv[j] = *reinterpret_cast<const f16x8*>(xr + 512 * j + 8 * lane);
+    nv[j] = *reinterpret_cast<const f16x8*>(w + 512 * j + 8 * lane);
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = (float)xv[j][e];
+      acc = __builtin_fmaf(v, v, acc);
+    }
+  const float var = wave64_sum(acc) / (float)hidden;
+  const float r = 1.0f / __builtin_sqrtf(var + eps);
+  uint16_t* out = xn + (long long)t * hidden;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = to_f16(((float)xv[j][e] * r) * (float)nv[j][e]);
+    *reinterpret_cast<f16x8*>(out + 512 * j + 8 * lane) = o;
+  }
+}
+
+// Y[t][n] for n in this workgroup's 16 rows and t in its kTokPerWg tokens.
+// Wave w holds rows n0 = 16*bx + 2w and n0 + 1 (NJ chunks of 8 per lane, the
+// last one masked when K is not a multiple of 512).  Token tiles of kTokTile
+// rows of X are staged in LDS; each lane reads its 16-byte chunks from them
+// (consecutive lanes, consecutive 16 B: conflict-free).  Two tokens and two
+// rows are summed at a time: four independent sequential sums per lane, each
+// in the decode order, then four wave64 reductions.
+//   kEpi 0: Y[t][n] = half(sum)
+//   kEpi 1: Y[t][n] = half(R[t][n] + half(sum))     (residual add; R may be Y)
+template <int NJ, int kEpi>
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_batched_kernel(BatchedGemvParams p) {
+  extern __shared__ __align__(16) uint16_t xs[];        // [kTokTile][NJ * 512]
+  constexpr int kTokTile = tok_tile(NJ);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int K = p.k;
+  const int rem = K - 512 * (NJ - 1);                    // elements in the last chunk
+  const bool tail = 8 * lane < rem;
+  const int n0 = blockIdx.x * (2 * kGemvWaves) + 2 * wave;
+  const int na = min(n0, p.n - 1), nb = min(n0 + 1, p.n - 1);
+  f16x8 wa[NJ], wb[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    if (j < NJ - 1 || tail) {
+      wa[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p.w + (long long)na * K + 512 * j + 8 * lane));
+      wb[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p.w + (long long)nb * K + 512 * j + 8 * lane));
+    }
+  }
+  const int t_begin = blockIdx.y * kTokPerWg;
+  const int t_end = min(p.t, t_begin + kTokPerWg);
+  const int chunks = K / 8;                              // 16-byte chunks per token row
+  for (int t0 = t_begin; t0 < t_end; t0 += kTokTile) {
+    const int nt = min(kTokTile, t_end - t0);
+    __syncthreads();                                     // previous tile fully consumed
+    for (int c = threadIdx.x; c < nt * chunks; c += kGemvWaves * 64) {
+      const int tt = c / chunks, kc = c - tt * chunks;
+      *reinterpret_cast<f16x8*>(xs + tt * (NJ * 512) + kc * 8) =
+          *reinterpret_cast<const f16x8*>(p.x + (long long)(t0 + tt) * p.ldx + kc * 8);
+    }
+    __syncthreads();
+    for (int tt = 0; tt < nt; tt += 2) {
+      const bool two = tt + 1 < nt;
+      const uint16_t* x0 = xs + tt * (NJ * 512);
+      const uint16_t* x1 = xs + (two ? tt + 1 : tt) * (NJ * 512);
+      float a0 = 0.0f, a1 = 0.0f, b0 = 0.0f, b1 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if (j < NJ - 1 || tail) {
+          const f16x8 u0 = *reinterpret_cast<const f16x8*>(x0 + 512 * j + 8 * lane);
+          const f16x8 u1 = *reinterpret_cast<const f16x8*>(x1 + 512 * j + 8 * lane);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            a0 = __builtin_fmaf((float)wa[j][e], (float)u0[e], a0);
+            a1 = __builtin_fmaf((float)wa[j][e], (float)u1[e], a1);
+            b0 = __builtin_fmaf((float)wb[j][e], (float)u0[e], b0);
+            b1 = __builtin_fmaf((float)wb[j][e], (float)u1[e], b1);
+          }
+        }
+      }
+      a0 = wave64_sum(a0);
+      a1 = wave64_sum(a1);
+      b0 = wave64_sum(b0);
+      b1 = wave64_sum(b1);
+      if (lane == 0 && n0 < p.n) {
+        const float sums[4] = {a0, b0, a1, b1};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int t = t0 + tt + (q >> 1);
+          const int n = n0 + (q & 1);
+          if ((q >> 1) == 1 && !two) continue;
+          if (n >= p.n) continue;
+          const _Float16 y = to_f16(sums[q]);
+          _Float16* dst = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
+          if constexpr (kEpi == 0) {
+            *dst = y;
+          } else {
+            const float r = (float)reinterpret_cast<const _Float16*>(p.res)[(long long)t * p.ldy + n];
+            *dst = (_Float16)(r + (float)y);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Bias, rotate-half RoPE and KV append for token t at position pos0 + t: one
+// thread per (head, rotation pair), as qkv_bias_rope_cache_kernel
+// (qd_rope_cache.hip) does for a single token.
+__global__ __launch_bounds__(64) void rope_batched_kernel(uint16_t* qkv, const uint16_t* bias,
+                                                          uint16_t* k_layer, uint16_t* v_layer,
+                                                          const float2* rope_cs, long long row_stride,
+                                                          long long head_stride, int pos0,
+                                                          int num_heads) {
+  const int t = blockIdx.y;
+  const int h = blockIdx.x;
+  const int i = threadIdx.x;
+  const int hid = num_heads * 128;
+  const int pos = pos0 + t;
+  _Float16* q = reinterpret_cast<_Float16*>(qkv) + (long long)t * 3 * hid;
+  const _Float16* b = reinterpret_cast<const _Float16*>(bias);
+  const int idx1 = h * 128 + i, idx2 = idx1 + 64;
+  _Float16 hq1 = q[idx1], hq2 = q[idx2], hk1 = q[hid + idx1], hk2 = q[hid + idx2];
+  _Float16 hv1 = q[2 * hid + idx1], hv2 = q[2 * hid + idx2];
+  if (b) {
+    hq1 = (_Float16)((float)hq1 + (float)b[idx1]);
+    hq2 = (_Float16)((float)hq2 + (float)b[idx2]);
+    hk1 = (_Float16)((float)hk1 + (float)b[hid + idx1]);
+    hk2 = (_Float16)((float)hk2 + (float)b[hid + idx2]);
+    hv1 = (_Float16)((float)hv1 + (float)b[2 * hid + idx1]);
+    hv2 = (_Float16)((float)hv2 + (float)b[2 * hid + idx2]);
+  }
+  const float2 cs = rope_cs[pos * 64 + i];
+  const float q1 = (float)hq1, q2 = (float)hq2, k1 = (float)hk1, k2 = (float)hk2;
+  const float q1c = q1 * cs.x, q2s = q2 * cs.y, q2c = q2 * cs.x, q1s = q1 * cs.y;
+  const float k1c = k1 * cs.x, k2s = k2 * cs.y, k2c = k2 * cs.x, k1s = k1 * cs.y;
+  q[idx1] = to_f16(q1c - q2s);
+  q[idx2] = to_f16(q2c + q1s);
+  q[hid + idx1] = hk1;
+  q[hid + idx2] = hk2;
+  q[2 * hid + idx1] = hv1;
+  q[2 * hid + idx2] = hv2;
+  const long long base = (long long)pos * row_stride + (long long)h * head_stride;
+  _Float16* kc = reinterpret_cast<_Float16*>(k_layer) + base;
+  _Float16* vc = reinterpret_cast<_Float16*>(v_layer) + base;
+  kc[i] = to_f16(k1c - k2s);
+  kc[64 + i] = to_f16(k2c + k1s);
+  vc[i] = hv1;
+  vc[64 + i] = hv2;
+}
+
+// act = half(g * (u / (1 + exp2_rep(-u * log2 e)))) on fp16 g, u: the decode
+// kernel's SwiGLU epilogue (qd_decode_ops.hip), elementwise over T * inter.
+__global__ __launch_bounds__(256) void swiglu_batched_kernel(const uint16_t* __restrict__ g,
+                                                            const uint16_t* __restrict__ u,
+                                                            uint16_t* __restrict__ act,
+                                                            long long n) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float gh = (float)reinterpret_cast<const _Float16*>(g)[i];
+  const float uh = (float)reinterpret_cast<const _Float16*>(u)[i];
+  const float e = exp2_rep(-uh * kLog2e);
+  const float silu = uh / (1.0f + e);
+  reinterpret_cast<_Float16*>(act)[i] = to_f16(gh * silu);
+}
+
+// Embedding rows: x[t] = wte[tokens[t]].
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__ wte,
+                                                    const int* __restrict__ tokens,
+                                                    uint16_t* __restrict__ x, int hidden) {
+  const int t = blockIdx.x;
+  const uint16_t* src = wte + (long long)tokens[t] * hidden;
+  uint16_t* dst = x + (long long)t * hidden;
+  for (int c = threadIdx.x; c < hidden / 8; c += 256)
+    *reinterpret_cast<f16x8*>(dst + 8 * c) = *reinterpret_cast<const f16x8*>(src + 8 * c);
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float eps, uint16_t* xn,
+                                  int hidden, int T, hipStream_t stream) {
+  const dim3 grid((T + 3) / 4), block(256);
+  switch (hidden / 512) {
+#define QD_CASE(n) \
+    case n: hipLaunchKernelGGL(rmsnorm_batched_kernel<n>, grid, block, 0, stream, x, w, eps, xn, T); break;
+    QD_CASE(1) QD_CASE(2) QD_CASE(3) QD_CASE(4) QD_CASE(5) QD_CASE(6) QD_CASE(7) QD_CASE(8)
+#undef QD_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t stream) {
+  const int nj = (p.k + 511) / 512;
+  const dim3 grid((p.n + 2 * kGemvWaves - 1) / (2 * kGemvWaves), (p.t + kTokPerWg - 1) / kTokPerWg);
+  const size_t lds = (size_t)tok_tile(nj) * nj * 512 * sizeof(uint16_t);
+  switch (nj * 2 + epi) {
+#define QD_CASE(n)                                                                                  \
+    case 2 * n:                                                                                      \
+      hipLaunchKernelGGL((gemv_batched_kernel<n, 0>), grid, dim3(kGemvWaves * 64), lds, stream, p); \
+      break;                                                                                         \
+    case 2 * n + 1:                                                                                  \
+      hipLaunchKernelGGL((gemv_batched_kernel<n, 1>), grid, dim3(kGemvWaves * 64), lds, stream, p); \
+      break;
+    QD_CASE(1) QD_CASE(2) QD_CASE(3) QD_CASE(4) QD_CASE(5) QD_CASE(6) QD_CASE(7) QD_CASE(8)
+    QD_CASE(9) QD_CASE(10) QD_CASE(11) QD_CASE(12) QD_CASE(13) QD_CASE(14) QD_CASE(15) QD_CASE(16)
+#undef QD_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_layer,
+                               uint16_t* v_layer, const float2* rope_cs, long long row_stride,
+                               long long head_stride, int pos0, int num_heads, int T,
+                               hipStream_t stream) {
+  hipLaunchKernelGGL(rope_batched_kernel, dim3(num_heads, T), dim3(64), 0, stream, qkv, bias, k_layer,
+                     v_layer, rope_cs, row_stride, head_stride, pos0, num_heads);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t* act, long long n,
+                                 hipStream_t stream) {
+  hipLaunchKernelGGL(swiglu_batched_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     g, u, act, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed(const uint16_t* wte, const int* tokens, uint16_t* x, int hidden, int T,
+                        hipStream_t stream) {
+  hipLaunchKernelGGL(embed_kernel, dim3(T), dim3(256), 0, stream, wte, tokens, x, hidden);
+  return hipGetLastError();
+}
+
+}  // namespace qd

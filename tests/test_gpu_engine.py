@@ -161,6 +161,35 @@ def test_engine_long_context_split_plans(qdiy):
     assert one == oracle.generate(img, [17], 5, _plans(qdiy, cfg, 6))[0]
 
 
+def test_prefill_batches_equal_token_by_token(qdiy):
+    """The batched prefill (qd_prefill.hip) leaves the same KV cache as feeding the
+    tokens one at a time: the next step's logits agree bit for bit, for one
+    batch, uneven chunks and single tokens, and with the oracle."""
+    cfg = qdiy.model_cfg(**TINY)
+    img = qdiy.random_model_image(cfg, 25, 0.05)
+    prompt = [int(t) for t in np.random.default_rng(7).integers(0, 1000, 77)]
+    outs = []
+    with qdiy.Engine(image=img) as eng:
+        for split in ([77], [1, 30, 46], [1] * 77):
+            eng.reset()
+            pos, i = 0, 0
+            for n in split:
+                pos = eng.prefill(prompt[i:i + n], pos)
+                i += n
+            assert pos == 77
+            tok = eng.step(5, 77)
+            outs.append((tok, eng.logits()))
+    for tok, lg in outs[1:]:
+        assert tok == outs[0][0] and _same(lg, outs[0][1])
+    m = oracle.Model(img, 78)
+    plans = _plans(qdiy, cfg, 78)
+    for p_, t_ in enumerate(prompt):
+        m.forward(t_, p_, plans[p_], want_logits=False)
+    tok, lg = m.forward(5, 77, plans[77])
+    m.close()
+    assert tok == outs[0][0] and _same(lg, outs[0][1])
+
+
 def test_engine_rejects_bad_input(qdiy, tmp_path):
     cfg = qdiy.model_cfg(**TINY)
     img = qdiy.random_model_image(cfg, 23)
