@@ -37,17 +37,17 @@ using qd::aligned16;
 using qd::fail;
 using qd::hip_fail;
 
-// Launch planner, from measured sweeps on MI355X (16 heads, cold KV, 4-wave
-// workgroups, non-temporal KV loads):
+// Launch planner, from measured sweeps on MI355X (16 heads, cold KV, the
+// bit-reproducible kernels):
 //   * up to kFusedMaxRows rows: one 16-wave workgroup per head, no merge
-//     (3.3-5.3 us, below the ~5.3 us floor of two launches);
-//   * up to kMidRows rows: two split workgroups per CU in total;
-//   * longer: one split workgroup per CU (at 16 heads: 16 splits, 14.3 us at
-//     L=8192, 42.4 us at L=32768), the per-workgroup scan loop hides latency.
+//     (4.8 us at 128 rows, 5.6 at 192; every split plan costs ~6 us there,
+//     the floor of two dependent launches);
+//   * longer: one split workgroup per CU in total (16 splits at 16 heads), each
+//     looping over its rows (6.0 us at 256-512 rows, 15.3 at 8192, 42.2 at
+//     32768); more splits or more waves per workgroup measured no better.
 // Each split keeps at least kMinRowsPerSplit rows.
-constexpr int kFusedMaxRows = 256;
-constexpr int kMidRows = 2048;
-constexpr int kMinRowsPerSplit = 32;
+constexpr int kFusedMaxRows = 224;
+constexpr int kMinRowsPerSplit = 16;
 
 qd::AttnPlan plan_fused(int seqlen) {
   qd::AttnPlan plan;
@@ -62,8 +62,7 @@ qd::AttnPlan plan_fused(int seqlen) {
 qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
   int splits = requested;
   if (splits <= 0) {
-    const int wgs = seqlen <= kMidRows ? 2 * ctx->num_cus : ctx->num_cus;
-    splits = wgs / ctx->cfg.num_heads;
+    splits = ctx->num_cus / ctx->cfg.num_heads;
     const int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
     if (splits > by_rows) splits = by_rows;
   }
