@@ -44,10 +44,13 @@ using qd::hip_fail;
 //     the floor of two dependent launches);
 //   * longer: one split workgroup per CU in total (16 splits at 16 heads), each
 //     looping over its rows (6.0 us at 256-512 rows, 15.3 at 8192, 42.2 at
-//     32768); more splits or more waves per workgroup measured no better.
+//     32768), except two per CU between 1025 and 2048 rows; other split counts
+//     or more waves per workgroup measured no better.
 // Each split keeps at least kMinRowsPerSplit rows.
 constexpr int kFusedMaxRows = 224;
 constexpr int kMinRowsPerSplit = 16;
+constexpr int kTwoPerCuMin = 1024;   // (1024, 2048] rows: two split workgroups per CU
+constexpr int kTwoPerCuMax = 2048;   // (8.1 vs 8.5 us at 2048)
 
 qd::AttnPlan plan_fused(int seqlen) {
   qd::AttnPlan plan;
@@ -62,7 +65,7 @@ qd::AttnPlan plan_fused(int seqlen) {
 qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
   int splits = requested;
   if (splits <= 0) {
-    splits = ctx->num_cus / ctx->cfg.num_heads;
+    splits = (seqlen > kTwoPerCuMin && seqlen <= kTwoPerCuMax ? 2 : 1) * ctx->num_cus / ctx->cfg.num_heads;
     const int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
     if (splits > by_rows) splits = by_rows;
   }

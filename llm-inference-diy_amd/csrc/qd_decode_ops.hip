@@ -18,11 +18,13 @@
 // fp32, so the result depends only on that order, which the CPU oracle
 // restates (QD_ORDER_WAVE64) -- outputs are bit-identical to it.
 //
-// Work split: one workgroup per (head h, rotation pair i < 64): six waves
-// compute rows q1 = h*128+i, q2 = q1+64 and the matching K and V rows; one
-// thread then adds the bias, rotates and appends, so no value crosses
-// workgroups.  The RMSNorm of x (when requested) is recomputed by every wave
-// from its own 32 elements and one wave64 reduction.
+// Work split: one wave per (head h, rotation pair i < 64), four pairs per
+// workgroup.  The wave computes rows q1 = h*128+i, q2 = q1+64 and the matching
+// K and V rows, then its lane 0 adds the bias, rotates and appends, so no
+// value leaves the wave.  The RMSNorm of x (when requested) is computed once
+// per wave from its lanes' elements and one wave64 reduction.  (Six waves per
+// pair with an LDS hand-off measured ~1 us slower per launch at hidden 2048:
+// the per-wave normalisation and the barrier, not the weight stream.)
 #include "qd_device.h"
 #include "qd_internal.h"
 
@@ -120,36 +122,55 @@ __device__ __forceinline__ void qkv_front_epilogue(const QkvFrontParams& p, int 
   vc[64 + i] = v6[5];
 }
 
-template <int NJ>
-__global__ __launch_bounds__(384) void qkv_front_kernel(QkvFrontParams p) {
-  __shared__ _Float16 y[6];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;          // 0..5: q1 q2 k1 k2 v1 v2
-  const int h = blockIdx.x >> 6;
-  const int i = blockIdx.x & 63;
-  const int hidden = NJ * 512;
-  const int row = (wave >> 1) * hidden + h * 128 + i + (wave & 1) * 64;
+// Rows of one pair in flight per phase: at most 24 16-byte chunks per lane
+// (all six rows up to hidden 2048, then two phases of three rows).
+constexpr int qkv_rows_per_phase(int nj) { return nj <= 4 ? 6 : 3; }
+constexpr int kQkvPairsPerBlock = 4;
 
-  // the epilogue's operands, fetched at the start so their latency overlaps the GEMV
-  _Float16 bias6[6] = {};
-  float2 cs = {0.0f, 0.0f};
-  if (threadIdx.x == 0) {
-    cs = p.rope_cs[p.pos * 64 + i];
-    if (p.bias) {
+template <int NJ>
+__global__ __launch_bounds__(kQkvPairsPerBlock * 64) void qkv_front_kernel(QkvFrontParams p) {
+  constexpr int RG = qkv_rows_per_phase(NJ);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
+  const int pair = blockIdx.x * kQkvPairsPerBlock + wave;              // grid covers num_heads*64 exactly
+  const int h = pair >> 6;
+  const int i = pair & 63;
+  const int hidden = NJ * 512;
+  // row r: (r >> 1) selects Q, K, V; (r & 1) the rotation half
+  auto row_ptr = [&](int r) {
+    return p.w + (long long)((r >> 1) * hidden + h * 128 + i + (r & 1) * 64) * hidden;
+  };
+  f16x8 xv[NJ], nv[NJ], wv[RG][NJ];
+  issue_input<NJ>(p.x, p.norm_w, lane, xv, nv);
 #pragma unroll
-      for (int r = 0; r < 6; ++r)
-        bias6[r] = reinterpret_cast<const _Float16*>(p.bias)[(r >> 1) * hidden + h * 128 + i + (r & 1) * 64];
+  for (int r = 0; r < RG; ++r) issue_row<NJ>(row_ptr(r), lane, wv[r]);
+  __builtin_amdgcn_sched_barrier(0);
+  // The epilogue's operands are wave-uniform (scalar loads), fetched while the
+  // weight rows are in flight.  bias is read as the aligned 32-bit word that
+  // holds the fp16 value.
+  _Float16 bias6[6] = {};
+  const float2 cs = p.rope_cs[p.pos * 64 + i];
+  if (p.bias) {
+    const uint32_t* bw = reinterpret_cast<const uint32_t*>(p.bias);
+#pragma unroll
+    for (int r = 0; r < 6; ++r) {
+      const int idx = (r >> 1) * hidden + h * 128 + i + (r & 1) * 64;
+      bias6[r] = __builtin_bit_cast(_Float16, (uint16_t)(bw[idx >> 1] >> (16 * (idx & 1))));
     }
   }
-  f16x8 xv[NJ], nv[NJ], wv[NJ];
-  issue_input<NJ>(p.x, p.norm_w, lane, xv, nv);
-  issue_row<NJ>(p.w + (long long)row * hidden, lane, wv);
   __builtin_amdgcn_sched_barrier(0);
   if (p.norm_w) normalise<NJ>(xv, nv, p.eps);
-  const float acc = wave64_sum(lane_sum<NJ>(wv, xv));
-  if (lane == 0) y[wave] = to_f16(acc);       // hgemv's half output
-  __syncthreads();
-  if (threadIdx.x == 0) qkv_front_epilogue(p, h, i, hidden, y, bias6, cs);
+  _Float16 y[6];                               // hgemv's half outputs
+#pragma unroll
+  for (int r = 0; r < RG; ++r) y[r] = to_f16(wave64_sum(lane_sum<NJ>(wv[r], xv)));
+  if constexpr (RG < 6) {
+#pragma unroll
+    for (int r = 0; r < 6 - RG; ++r) issue_row<NJ>(row_ptr(RG + r), lane, wv[r]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < 6 - RG; ++r) y[RG + r] = to_f16(wave64_sum(lane_sum<NJ>(wv[r], xv)));
+  }
+  if (lane == 0) qkv_front_epilogue(p, h, i, hidden, y, bias6, cs);
 }
 
 // Output projection + residual add (qwen_infer.cu:701-704 and :718-721:
@@ -318,7 +339,7 @@ __global__ __launch_bounds__(1024) void argmax_reduce_kernel(const unsigned long
 }  // namespace
 
 hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream) {
-  const dim3 grid(p.num_heads * 64), block(384);
+  const dim3 grid(p.num_heads * 64 / kQkvPairsPerBlock), block(kQkvPairsPerBlock * 64);
   switch (p.num_heads * 128 / 512) {
     case 1: hipLaunchKernelGGL(qkv_front_kernel<1>, grid, block, 0, stream, p); break;
     case 2: hipLaunchKernelGGL(qkv_front_kernel<2>, grid, block, 0, stream, p); break;

@@ -67,6 +67,31 @@ def test_bit_exact_vs_oracle(qdiy, weights, with_norm, with_bias, pos):
         assert _same(w, g), name
 
 
+@pytest.mark.parametrize("heads", [4, 8, 20, 32])
+def test_bit_exact_other_widths(qdiy, heads):
+    """hidden 512 / 1024 keep all six rows of a pair in flight at once; 2560
+    and 4096 load them in two phases of three rows."""
+    hid = heads * D
+    rng = np.random.default_rng(900 + heads)
+    W, b = normal_f16(rng, (3 * hid, hid), 0.02), normal_f16(rng, 3 * hid, 0.02)
+    nw = (1.0 + normal_f16(rng, hid, 0.1).astype(np.float32)).astype(np.float16)
+    x = normal_f16(rng, hid)
+    S, pos = 16, 11
+    o_qkv = np.zeros(3 * hid, np.float16)
+    o_k = np.full(S * hid, SENT, np.float16)
+    o_v = o_k.copy()
+    oracle.qkv_front(x, nw, W, b, o_qkv, o_k, o_v, pos, heads)
+    g_qkv = torch.zeros(3 * hid, dtype=torch.float16, device="cuda")
+    g_k = torch.full((S * hid,), float(SENT), dtype=torch.float16, device="cuda")
+    g_v = g_k.clone()
+    with qdiy.Context(num_heads=heads, max_seqlen=S) as ctx:
+        ctx.qkv_proj_rope_cache(torch.from_numpy(x).cuda(), torch.from_numpy(nw).cuda(), torch.from_numpy(W).cuda(),
+                                torch.from_numpy(b).cuda(), g_qkv, g_k, g_v, pos)
+        torch.cuda.synchronize()
+    for name, w, g in zip(("qkv", "k_cache", "v_cache"), (o_qkv, o_k, o_v), (g_qkv, g_k, g_v)):
+        assert _same(w, g.cpu().numpy()), name
+
+
 def test_head_major_layout(qdiy, weights):
     rng = np.random.default_rng(3)
     x = normal_f16(rng, HID)
