@@ -127,7 +127,9 @@ __device__ __forceinline__ void qkv_front_epilogue(const QkvFrontParams& p, int 
 constexpr int qkv_rows_per_phase(int nj) { return nj <= 4 ? 6 : 3; }
 constexpr int kQkvPairsPerBlock = 4;
 
-template <int NJ>
+// kBiasWords: the bias pointer is 4-byte aligned (checked by the launcher),
+// so each bias value is read with a scalar load of its 32-bit word.
+template <int NJ, bool kBiasWords>
 __global__ __launch_bounds__(kQkvPairsPerBlock * 64) void qkv_front_kernel(QkvFrontParams p) {
   constexpr int RG = qkv_rows_per_phase(NJ);
   const int lane = threadIdx.x & 63;
@@ -145,17 +147,21 @@ __global__ __launch_bounds__(kQkvPairsPerBlock * 64) void qkv_front_kernel(QkvFr
 #pragma unroll
   for (int r = 0; r < RG; ++r) issue_row<NJ>(row_ptr(r), lane, wv[r]);
   __builtin_amdgcn_sched_barrier(0);
-  // The epilogue's operands are wave-uniform (scalar loads), fetched while the
-  // weight rows are in flight.  bias is read as the aligned 32-bit word that
-  // holds the fp16 value.
-  _Float16 bias6[6] = {};
+  // The epilogue's operands (wave-uniform), fetched while the weight rows are
+  // in flight: a 4-byte-aligned bias with scalar loads of the 32-bit word
+  // holding each value, any other 2-byte-aligned one 16 bits at a time into
+  // registers that stay untouched until the epilogue.  Either way nothing here
+  // waits for the weight stream.
+  uint32_t bias_bits[6] = {};
   const float2 cs = p.rope_cs[p.pos * 64 + i];
   if (p.bias) {
-    const uint32_t* bw = reinterpret_cast<const uint32_t*>(p.bias);
 #pragma unroll
     for (int r = 0; r < 6; ++r) {
       const int idx = (r >> 1) * hidden + h * 128 + i + (r & 1) * 64;
-      bias6[r] = __builtin_bit_cast(_Float16, (uint16_t)(bw[idx >> 1] >> (16 * (idx & 1))));
+      if constexpr (kBiasWords)
+        bias_bits[r] = (reinterpret_cast<const uint32_t*>(p.bias)[idx >> 1] >> (16 * (idx & 1))) & 0xFFFFu;
+      else
+        bias_bits[r] = p.bias[idx];
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -170,7 +176,12 @@ __global__ __launch_bounds__(kQkvPairsPerBlock * 64) void qkv_front_kernel(QkvFr
 #pragma unroll
     for (int r = 0; r < 6 - RG; ++r) y[RG + r] = to_f16(wave64_sum(lane_sum<NJ>(wv[r], xv)));
   }
-  if (lane == 0) qkv_front_epilogue(p, h, i, hidden, y, bias6, cs);
+  if (lane == 0) {
+    _Float16 bias6[6];
+#pragma unroll
+    for (int r = 0; r < 6; ++r) bias6[r] = __builtin_bit_cast(_Float16, (uint16_t)bias_bits[r]);
+    qkv_front_epilogue(p, h, i, hidden, y, bias6, cs);
+  }
 }
 
 // Output projection + residual add (qwen_infer.cu:701-704 and :718-721:
@@ -338,20 +349,23 @@ __global__ __launch_bounds__(1024) void argmax_reduce_kernel(const unsigned long
 
 }  // namespace
 
-hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream) {
+template <bool kBiasWords>
+static hipError_t launch_qkv_front_t(const QkvFrontParams& p, hipStream_t stream) {
   const dim3 grid(p.num_heads * 64 / kQkvPairsPerBlock), block(kQkvPairsPerBlock * 64);
   switch (p.num_heads * 128 / 512) {
-    case 1: hipLaunchKernelGGL(qkv_front_kernel<1>, grid, block, 0, stream, p); break;
-    case 2: hipLaunchKernelGGL(qkv_front_kernel<2>, grid, block, 0, stream, p); break;
-    case 3: hipLaunchKernelGGL(qkv_front_kernel<3>, grid, block, 0, stream, p); break;
-    case 4: hipLaunchKernelGGL(qkv_front_kernel<4>, grid, block, 0, stream, p); break;
-    case 5: hipLaunchKernelGGL(qkv_front_kernel<5>, grid, block, 0, stream, p); break;
-    case 6: hipLaunchKernelGGL(qkv_front_kernel<6>, grid, block, 0, stream, p); break;
-    case 7: hipLaunchKernelGGL(qkv_front_kernel<7>, grid, block, 0, stream, p); break;
-    case 8: hipLaunchKernelGGL(qkv_front_kernel<8>, grid, block, 0, stream, p); break;
+#define QD_QKV_CASE(n) \
+    case n: hipLaunchKernelGGL((qkv_front_kernel<n, kBiasWords>), grid, block, 0, stream, p); break;
+    QD_QKV_CASE(1) QD_QKV_CASE(2) QD_QKV_CASE(3) QD_QKV_CASE(4)
+    QD_QKV_CASE(5) QD_QKV_CASE(6) QD_QKV_CASE(7) QD_QKV_CASE(8)
+#undef QD_QKV_CASE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream) {
+  const bool words = (reinterpret_cast<uintptr_t>(p.bias) & 3u) == 0;   // also true for no bias
+  return words ? launch_qkv_front_t<true>(p, stream) : launch_qkv_front_t<false>(p, stream);
 }
 
 }  // namespace qd

@@ -92,6 +92,30 @@ def test_bit_exact_other_widths(qdiy, heads):
         assert _same(w, g.cpu().numpy()), name
 
 
+def test_bias_and_outputs_at_odd_offsets(qdiy, weights):
+    """bias, qkv and the caches need only 2-byte alignment: views one element
+    into larger buffers give the same bits as aligned ones."""
+    S, pos = 32, 9
+    rng = np.random.default_rng(4242)
+    x = normal_f16(rng, HID)
+    o_qkv = np.zeros(3 * HID, np.float16)
+    o_k = np.full(S * HID, SENT, np.float16)
+    o_v = o_k.copy()
+    oracle.qkv_front(x, weights["nw"], weights["W"], weights["b"], o_qkv, o_k, o_v, pos, H)
+
+    def odd(n, fill=0.0):
+        return torch.full((n + 1,), float(fill), dtype=torch.float16, device="cuda")[1:]
+    g_b = odd(3 * HID)
+    g_b.copy_(torch.from_numpy(weights["b"]).cuda())
+    g_qkv, g_k, g_v = odd(3 * HID), odd(S * HID, SENT), odd(S * HID, SENT)
+    with qdiy.Context(num_heads=H, max_seqlen=S) as ctx:
+        ctx.qkv_proj_rope_cache(torch.from_numpy(x).cuda(), torch.from_numpy(weights["nw"]).cuda(),
+                                torch.from_numpy(weights["W"]).cuda(), g_b, g_qkv, g_k, g_v, pos)
+        torch.cuda.synchronize()
+    for name, w, g in zip(("qkv", "k_cache", "v_cache"), (o_qkv, o_k, o_v), (g_qkv, g_k, g_v)):
+        assert _same(w, g.cpu().numpy()), name
+
+
 def test_head_major_layout(qdiy, weights):
     rng = np.random.default_rng(3)
     x = normal_f16(rng, HID)

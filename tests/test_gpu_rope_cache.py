@@ -65,6 +65,30 @@ def test_bit_exact_vs_oracle(qdiy, layout, with_bias, pos):
         assert _same(w, g), name
 
 
+def test_odd_element_offsets_bit_exact(qdiy):
+    """qkv and bias need only 2-byte alignment: views one element into larger
+    buffers give the same bits as aligned ones."""
+    S, pos = 64, 17
+    rng = np.random.default_rng(77)
+    qkv = normal_f16(rng, 3 * HID)
+    bias = normal_f16(rng, 3 * HID, 0.02)
+    o_qkv = qkv.copy()
+    o_k = np.full(S * HID, SENTINEL, np.float16)
+    o_v = o_k.copy()
+    oracle.qkv_bias_rope_cache(o_qkv, bias, o_k, o_v, pos, H)
+    qbuf = torch.zeros(3 * HID + 1, dtype=torch.float16, device="cuda")
+    bbuf = torch.zeros(3 * HID + 1, dtype=torch.float16, device="cuda")
+    qbuf[1:] = torch.from_numpy(qkv).cuda()
+    bbuf[1:] = torch.from_numpy(bias).cuda()
+    g_k = torch.full((S * HID,), float(SENTINEL), dtype=torch.float16, device="cuda")
+    g_v = g_k.clone()
+    with qdiy.Context(num_heads=H, max_seqlen=S) as ctx:
+        ctx.qkv_bias_rope_cache(qbuf[1:], bbuf[1:], g_k, g_v, pos)
+        torch.cuda.synchronize()
+    assert _same(o_qkv, qbuf[1:].cpu().numpy())
+    assert _same(o_k, g_k.cpu().numpy()) and _same(o_v, g_v.cpu().numpy())
+
+
 def test_long_context_positions_bit_exact(qdiy):
     S = 32768
     rng = np.random.default_rng(99)
