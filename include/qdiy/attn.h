@@ -100,7 +100,8 @@ int qd_qkv_bias_rope_cache(qd_ctx* ctx, uint16_t* qkv, const uint16_t* bias,
  *   norm_w: [H*128] RMSNorm weight (ln_1) or NULL to use x as given
  *   w_qkv:  [3*H*128][H*128] QKV weight in the .bin file's [out][in] layout
  *           (c_attn.weight, convert_weights.py:133-137), 16-byte aligned
- *   qkv:    [3*H*128] out: rotated Q, biased K and V (the reference's d_qkv)
+ *   qkv:    [3*H*128] out: rotated Q, biased K and V (the reference's d_qkv);
+ *           must not overlap x, norm_w, w_qkv or qkv_bias (QD_EINVAL)
  * H*128 must be a multiple of 512, at most 4096.  The GEMV sums each row in a
  * fixed order (per-lane sequential, then a fixed 64-lane tree), so results
  * are deterministic and reproducible on the host. */
@@ -116,7 +117,8 @@ int qd_qkv_proj_rope_cache(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_
  * the 16-32 per-head launches of qwen_infer.cu:646-678 with one launch
  * (fused) or two (split: stage 1 + merge), covering all heads.
  * Requires 1 <= seqlen <= max_seqlen; q, out, k_layer, v_layer 16-byte
- * aligned; kv strides multiples of 8 elements. */
+ * aligned; kv strides multiples of 8 elements.  out may be q itself but must
+ * not overlap the cache rows read (QD_EINVAL). */
 int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
                         const uint16_t* v_layer, uint16_t* out, int seqlen,
                         int num_heads, int head_dim, hipStream_t stream);

@@ -49,7 +49,8 @@ extern "C" {
  * W is [n_out][k_in] fp16; k_in a multiple of 8, at most 8192; x, w 16-byte
  * aligned.
  * residual and out may be the same buffer (the reference adds in place into
- * d_x).  Replaces hgemv_kernel + add_bias_kernel (hgemm_final.cuh:274-295,
+ * d_x); otherwise they must not overlap, and out must not overlap x or w
+ * (QD_EINVAL).  Replaces hgemv_kernel + add_bias_kernel (hgemm_final.cuh:274-295,
  * bias.cuh:6-11; qwen_infer.cu:701-704 and :718-721). */
 int qd_proj_residual(const uint16_t* x, const uint16_t* w, const uint16_t* residual,
                      uint16_t* out, int n_out, int k_in, hipStream_t stream);
@@ -58,7 +59,8 @@ int qd_proj_residual(const uint16_t* x, const uint16_t* w, const uint16_t* resid
  * u_i = half(W2[i] . xn), xn = half(x * (1/sqrt(mean(x^2) + eps)) * norm_w),
  * for i < inter.  W1 (gate, ffn_w1) and W2 (up, ffn_w2) are [inter][hidden];
  * hidden a multiple of 512, at most 4096.  exp(-u) is computed as
- * 2^(-u * log2 e) by a polynomial the host can repeat exactly.  Replaces
+ * 2^(-u * log2 e) by a polynomial the host can repeat exactly.  act must
+ * not overlap x, norm_w, w1 or w2 (QD_EINVAL).  Replaces
  * rmsnorm_kernel + 2 x hgemv_kernel + swiglu_kernel (rmsnorm.cuh:6-57,
  * swiglu.cuh:6-15; qwen_infer.cu:708-715). */
 int qd_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* w1,
@@ -73,7 +75,9 @@ size_t qd_lm_head_workspace_bytes(int vocab);
  * logit.  Ties go to the lowest index; -0 equals +0; NaN never wins.  (The
  * reference's argmax_kernel breaks ties by its thread and lane order,
  * argmax.cuh:19-66.)  W is [vocab][hidden].  workspace: device memory of
- * qd_lm_head_workspace_bytes(vocab) bytes, 8-byte aligned.  Replaces
+ * qd_lm_head_workspace_bytes(vocab) bytes, 8-byte aligned.  logits,
+ * workspace and token must not overlap each other or x, norm_w, w
+ * (QD_EINVAL).  Replaces
  * rmsnorm_kernel + hgemv_kernel + argmax_kernel (qwen_infer.cu:725-731). */
 int qd_lm_head_argmax(const uint16_t* x, const uint16_t* norm_w, float eps, const uint16_t* w,
                       uint16_t* logits, int vocab, int hidden, void* workspace,

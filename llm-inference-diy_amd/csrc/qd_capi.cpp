@@ -100,6 +100,13 @@ int check_attention_args(const qd_ctx* ctx, const uint16_t* q, const uint16_t* k
     return fail(QD_EINVAL, "num_heads %d differs from the context's %d", num_heads, ctx->cfg.num_heads);
   if (seqlen < 1 || seqlen > ctx->cfg.max_seqlen)
     return fail(QD_EINVAL, "seqlen %d outside [1, %d]", seqlen, ctx->cfg.max_seqlen);
+  // out may alias q (each head reads its q before any output is written) but
+  // not the cache rows other workgroups are still reading
+  const size_t ob = (size_t)num_heads * QD_HEAD_DIM * 2;
+  const size_t kvb = ((size_t)(seqlen - 1) * ctx->cfg.kv_row_stride +
+                      (size_t)(num_heads - 1) * ctx->cfg.kv_head_stride + QD_HEAD_DIM) * 2;
+  if (qd::overlaps(out, ob, k, kvb) || qd::overlaps(out, ob, v, kvb))
+    return fail(QD_EINVAL, "out overlaps the k_layer or v_layer rows being read");
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
     return fail(QD_EINVAL, "current device %d is not the context's device %d", dev, ctx->device);
@@ -300,6 +307,12 @@ int qd_qkv_proj_rope_cache(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_
   if (max_seqlen < 1 || max_seqlen > ctx->cfg.max_seqlen)
     return fail(QD_EINVAL, "max_seqlen %d outside [1, %d]", max_seqlen, ctx->cfg.max_seqlen);
   if (pos < 0 || pos >= max_seqlen) return fail(QD_EINVAL, "pos %d outside [0, %d)", pos, max_seqlen);
+  {
+    const size_t qb = (size_t)3 * hidden * 2, hb = (size_t)hidden * 2;
+    if (qd::overlaps(qkv, qb, x, hb) || qd::overlaps(qkv, qb, norm_w, hb) ||
+        qd::overlaps(qkv, qb, w_qkv, qb * hidden) || qd::overlaps(qkv, qb, qkv_bias, qb))
+      return fail(QD_EINVAL, "qkv overlaps x, norm_w, w_qkv or qkv_bias");
+  }
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
     return fail(QD_EINVAL, "current device %d is not the context's device %d", dev, ctx->device);

@@ -18,13 +18,14 @@
 #include "qdiy/engine.h"
 
 using qd::aligned16;
+using qd::aligned2;
+using qd::aligned8;
 using qd::fail;
+using qd::overlaps;
 using qd::hip_fail;
 
 namespace {
 
-bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
-bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 // ---------------------------------------------------------------------------
 // .bin layout (model_weights/convert_weights.py:105-185): element offsets of
@@ -259,6 +260,10 @@ int qd_proj_residual(const uint16_t* x, const uint16_t* w, const uint16_t* resid
   if (n_out < 1) return fail(QD_EINVAL, "n_out %d must be >= 1", n_out);
   if (k_in < 8 || k_in % 8 != 0 || k_in > 8192)
     return fail(QD_EINVAL, "k_in %d must be a multiple of 8 in [8, 8192]", k_in);
+  const size_t ob = (size_t)n_out * 2;
+  if (overlaps(out, ob, x, (size_t)k_in * 2) || overlaps(out, ob, w, (size_t)n_out * k_in * 2) ||
+      (residual != out && overlaps(out, ob, residual, ob)))
+    return fail(QD_EINVAL, "out overlaps x, w or (other than exactly) residual");
   qd::ProjResidualParams p{x, w, residual, out, n_out, k_in};
   hipError_t e = qd::launch_proj_residual(p, stream);
   return e == hipSuccess ? QD_OK : hip_fail(e, "proj_residual launch");
@@ -275,6 +280,10 @@ int qd_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps, const
     return fail(QD_EINVAL, "hidden %d unsupported (multiple of 512, at most 4096)", hidden);
   if (inter < 1) return fail(QD_EINVAL, "inter %d must be >= 1", inter);
   if (!(eps >= 0.0f)) return fail(QD_EINVAL, "eps must be >= 0");
+  const size_t ab = (size_t)inter * 2, hb = (size_t)hidden * 2, wb = (size_t)inter * hidden * 2;
+  if (overlaps(act, ab, x, hb) || overlaps(act, ab, norm_w, hb) || overlaps(act, ab, w1, wb) ||
+      overlaps(act, ab, w2, wb))
+    return fail(QD_EINVAL, "act overlaps x, norm_w, w1 or w2");
   qd::FfnUpParams p{x, norm_w, eps, w1, w2, act, hidden, inter};
   hipError_t e = qd::launch_ffn_up(p, stream);
   return e == hipSuccess ? QD_OK : hip_fail(e, "ffn_up launch");
@@ -300,6 +309,19 @@ int qd_lm_head_argmax(const uint16_t* x, const uint16_t* norm_w, float eps, cons
     return fail(QD_EINVAL, "workspace of %zu bytes below the %zu needed", workspace_bytes,
                 qd_lm_head_workspace_bytes(vocab));
   if (!(eps >= 0.0f)) return fail(QD_EINVAL, "eps must be >= 0");
+  {
+    const size_t lb = (size_t)vocab * 2, hb = (size_t)hidden * 2, wb = (size_t)vocab * hidden * 2;
+    const size_t kb = qd_lm_head_workspace_bytes(vocab);
+    const void* in[3] = {x, norm_w, w};
+    const size_t in_b[3] = {hb, hb, wb};
+    for (int j = 0; j < 3; ++j)
+      if (overlaps(logits, lb, in[j], in_b[j]) || overlaps(workspace, kb, in[j], in_b[j]) ||
+          overlaps(token, sizeof(int), in[j], in_b[j]))
+        return fail(QD_EINVAL, "logits, workspace or token overlaps x, norm_w or w");
+    if (overlaps(logits, lb, workspace, kb) || overlaps(token, sizeof(int), logits, lb) ||
+        overlaps(token, sizeof(int), workspace, kb))
+      return fail(QD_EINVAL, "logits, workspace and token must not overlap each other");
+  }
   qd::LmHeadParams p{x, norm_w, eps, w, logits, static_cast<unsigned long long*>(workspace), vocab,
                      hidden};
   hipError_t e = qd::launch_lm_head_argmax(p, token, stream);

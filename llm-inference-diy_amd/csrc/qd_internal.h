@@ -142,6 +142,16 @@ struct AttnPlan {
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_fail(hipError_t e, const char* what);
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+inline bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
+// Whether byte ranges [a, a + na) and [b, b + nb) share a byte (null or empty
+// ranges never do).  The entry points reject outputs that overlap inputs other
+// workgroups are still reading.
+inline bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
+  if (!a || !b || na == 0 || nb == 0) return false;
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + nb && y < x + na;
+}
 
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream);
 // Fused (one 16-wave workgroup per head, 4-row tiles) attention of `tokens`

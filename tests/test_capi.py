@@ -72,3 +72,38 @@ def test_calls_reject_null_context(qdiy):
     v, s = ctypes.c_int(), ctypes.c_int()
     assert lib.qd_decode_attention_plan(None, 1, ctypes.byref(v), ctypes.byref(s)) == qdiy.QD_EINVAL
     assert lib.qd_ctx_destroy(None) == qdiy.QD_OK
+
+
+def _host_buf(nbytes):
+    """A host buffer and its first 256-byte-aligned address (argument checks
+    run before any HIP call, so host addresses exercise them without a GPU)."""
+    buf = ctypes.create_string_buffer(nbytes + 256)
+    base = (ctypes.addressof(buf) + 255) & ~255
+    return buf, base
+
+
+def test_decode_ops_reject_overlapping_outputs_without_a_gpu(qdiy):
+    lib = qdiy.load()
+    P = ctypes.c_void_p
+    _keep, b = _host_buf(1 << 20)
+    n, k = 64, 512
+    x, w, res = b, b + 4096, b + 4096 + n * k * 2
+    # out inside x, inside w, and straddling residual (not equal to it)
+    for out in (x + 16, w + 64, res + 2):
+        assert lib.qd_proj_residual(P(x), P(w), P(res), P(out), n, k, None) == qdiy.QD_EINVAL
+        assert b"overlaps" in lib.qd_last_error()
+    H, I = 512, 32
+    xs, nw, w1, w2 = b, b + 1024, b + 2048, b + 2048 + I * H * 2
+    for act in (xs + 2, nw, w1 + 100, w2 + I * H * 2 - 2):
+        assert lib.qd_ffn_up_swiglu(P(xs), P(nw), ctypes.c_float(1e-6), P(w1), P(w2), P(act), H, I,
+                                    None) == qdiy.QD_EINVAL
+        assert b"overlaps" in lib.qd_last_error()
+    V = 64
+    ws_n = lib.qd_lm_head_workspace_bytes(V)
+    wl = b + 2048
+    logits, ws, tok = b + 2048 + V * H * 2, b + 4096 + V * H * 2, b + 8192 + V * H * 2
+    bad = [(xs, ws, tok), (logits, logits + 8, tok), (logits, ws, ws), (logits, ws, wl + 64)]
+    for lg, wk, tk in bad:
+        assert lib.qd_lm_head_argmax(P(xs), P(nw), ctypes.c_float(1e-6), P(wl), P(lg), V, H, P(wk),
+                                     ctypes.c_size_t(ws_n), P(tk), None) == qdiy.QD_EINVAL
+        assert b"overlap" in lib.qd_last_error()

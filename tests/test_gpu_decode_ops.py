@@ -181,6 +181,13 @@ def test_invalid_arguments(qdiy, weights):
         xbig = torch.zeros(HID + 8, dtype=torch.float16, device="cuda")
         with pytest.raises(qdiy.QdError):
             ctx.qkv_proj_rope_cache(xbig[1:HID + 1], None, W, None, qkv, kc, kc, 0)   # misaligned x
+        big = torch.zeros(4 * HID, dtype=torch.float16, device="cuda")
+        with pytest.raises(qdiy.QdError, match="overlap"):                    # x inside qkv
+            ctx.qkv_proj_rope_cache(big[HID:2 * HID], None, W, None, big[:3 * HID], kc, kc, 0)
+        with pytest.raises(qdiy.QdError, match="overlap"):                    # out inside the V rows
+            ctx.decode_attention(qkv[:HID], kc, kc, kc[HID:2 * HID], 4)
+        ctx.decode_attention(qkv[:HID], kc, kc, qkv[:HID], 4)                  # out == q is allowed
+        torch.cuda.synchronize()
     with qdiy.Context(num_heads=3, max_seqlen=8) as ctx3:                      # hidden 384
         x = torch.zeros(384, dtype=torch.float16, device="cuda")
         W = torch.zeros(3 * 384 * 384, dtype=torch.float16, device="cuda")
