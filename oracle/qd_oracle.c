@@ -562,15 +562,15 @@ static void wave_merge4(gstate* g) {
   g[0].m = M;
 }
 
-/* The score of one row for one 16-lane group: lane t adds its 8 exact
- * products as ((p0+p1)+(p2+p3)) + ((p4+p5)+(p6+p7)), then the 16-lane tree of
- * row16_sum. */
+/* The score of one row for one 16-lane group: lane t starts from the exact
+ * product k0*q0 and adds its other 7 products with fmaf in element order
+ * (decode_attention_scan_kernel's dot8), then the 16-lane tree of row16_sum. */
 static float group_score(const float* qf, const uint16_t* krow) {
   float lanes[16];
   for (int t = 0; t < 16; ++t) {
-    float pr[8];
-    for (int e = 0; e < 8; ++e) pr[e] = qd_oracle_h2f(krow[8 * t + e]) * qf[8 * t + e];   /* exact */
-    lanes[t] = ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+    float acc = qd_oracle_h2f(krow[8 * t]) * qf[8 * t];   /* exact */
+    for (int e = 1; e < 8; ++e) acc = fmaf(qd_oracle_h2f(krow[8 * t + e]), qf[8 * t + e], acc);
+    lanes[t] = acc;
   }
   float q4[4];
   for (int i = 0; i < 4; ++i) q4[i] = (lanes[4 * i] + lanes[4 * i + 1]) + (lanes[4 * i + 2] + lanes[4 * i + 3]);
