@@ -195,6 +195,44 @@ def test_head_independence(qdiy):
     g.close()
 
 
+@pytest.mark.parametrize("variant", ["auto", "fused", "split"])
+def test_non_finite_inputs_match_the_oracle(qdiy, variant):
+    """A NaN key element makes its row's exponent NaN, which the exponential
+    maps to 0: the row drops out and the head stays finite.  An inf in a V row
+    makes the head inf/NaN; an inf key element makes the head's maximum inf and
+    its output NaN (0/0).  The GPU must give the oracle's NaN positions and
+    the oracle's bits everywhere else (NaN payloads differ between GPU and
+    host), and a clean head must not change."""
+    L, H, S = 700, 4, 720
+    clean = AttnCase(L, H=H, seed=31, max_seqlen=S)
+    case = AttnCase(L, H=H, seed=31, max_seqlen=S)
+    kc = case.kc.copy().reshape(S, H, 128)
+    vc = case.vc.copy().reshape(S, H, 128)
+    kc[123, 0, 17] = np.float16(np.nan)
+    vc[456, 1, 3] = np.float16(np.inf)
+    kc[321, 2, 40] = np.float16(np.inf) * np.sign(case.q.reshape(H, 128)[2, 40] or 1)
+    case.kc, case.vc = kc.reshape(-1), vc.reshape(-1)
+    ctx = qdiy.Context(num_heads=H, max_seqlen=S)
+    outs = {}
+    for name, c in (("clean", clean), ("planted", case)):
+        out = torch.empty(H * 128, dtype=torch.float16, device="cuda")
+        ctx.decode_attention(torch.from_numpy(c.q.reshape(-1)).cuda(), torch.from_numpy(c.kc).cuda(),
+                             torch.from_numpy(c.vc).cuda(), out, L, variant, 5 if variant == "split" else 0)
+        torch.cuda.synchronize()
+        outs[name] = out.cpu().numpy().reshape(H, 128)
+    plan = ctx.plan_detail(L, variant, 5 if variant == "split" else 0)
+    ctx.close()
+    want = oracle.attention_planned(case.q, case.kc, case.vc, L, H, case.row_stride, case.head_stride,
+                                    oracle.Plan(*plan.as_tuple()), nthreads=8)
+    got = outs["planted"]
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.uint16), want[fin].view(np.uint16))
+    assert np.isfinite(got[0]).all()                      # the NaN key row dropped out
+    assert not np.isfinite(got[1]).all() and np.isnan(got[2]).all()
+    assert np.array_equal(got[3].view(np.uint16), outs["clean"][3].view(np.uint16))
+
+
 def test_invalid_arguments_raise(qdiy):
     case = AttnCase(64, H=16, seed=10)
     g = GpuCase(qdiy, case)
