@@ -198,11 +198,12 @@ def test_head_independence(qdiy):
 @pytest.mark.parametrize("variant", ["auto", "fused", "split"])
 def test_non_finite_inputs_match_the_oracle(qdiy, variant):
     """A NaN key element makes its row's exponent NaN, which the exponential
-    maps to 0: the row drops out and the head stays finite.  An inf in a V row
-    makes the head inf/NaN; an inf key element makes the head's maximum inf and
-    its output NaN (0/0).  The GPU must give the oracle's NaN positions and
-    the oracle's bits everywhere else (NaN payloads differ between GPU and
-    host), and a clean head must not change."""
+    maps to 0: the row drops out and the head stays finite (the reference's
+    expf would make that head NaN; this deviation is deliberate).  An inf in a
+    V row makes the head inf/NaN; an inf key element makes the head's maximum
+    inf and its output NaN (0/0), as in the reference.  The GPU must give the
+    kernel-order oracle's NaN positions and bits everywhere else (NaN payloads
+    differ between GPU and host), and a clean head must not change."""
     L, H, S = 700, 4, 720
     clean = AttnCase(L, H=H, seed=31, max_seqlen=S)
     case = AttnCase(L, H=H, seed=31, max_seqlen=S)
@@ -229,6 +230,10 @@ def test_non_finite_inputs_match_the_oracle(qdiy, variant):
     fin = ~np.isnan(want)
     assert np.array_equal(got[fin].view(np.uint16), want[fin].view(np.uint16))
     assert np.isfinite(got[0]).all()                      # the NaN key row dropped out
+    ref = _oracle(case)                                    # the reference kernels' order (expf)
+    assert np.isnan(ref[0]).all()                          # ... where expf poisons the head
+    assert np.array_equal(np.isnan(got[1:]), np.isnan(ref[1:]))
+    assert np.array_equal(np.isinf(got[1:]), np.isinf(ref[1:]))
     assert not np.isfinite(got[1]).all() and np.isnan(got[2]).all()
     assert np.array_equal(got[3].view(np.uint16), outs["clean"][3].view(np.uint16))
 
