@@ -138,8 +138,8 @@ struct qd_engine {
   uint16_t* logits = nullptr;           // [vocab]
   void* lm_ws = nullptr;
   size_t lm_ws_bytes = 0;
-  int* d_token = nullptr;
-  int* h_token = nullptr;               // pinned
+  int* h_token = nullptr;               // pinned, mapped: the argmax writes it directly
+  int* h_token_dev = nullptr;           // h_token's device address
   long long kv_bytes = 0;
   // batched prefill scratch, kPrefillChunk tokens
   int* p_tokens = nullptr;
@@ -168,7 +168,6 @@ void engine_free(qd_engine* e) {
   (void)hipFree(e->act);
   (void)hipFree(e->logits);
   (void)hipFree(e->lm_ws);
-  (void)hipFree(e->d_token);
   for (void* q : {(void*)e->p_tokens, (void*)e->p_x, (void*)e->p_xn, (void*)e->p_qkv, (void*)e->p_att,
                   (void*)e->p_g, (void*)e->p_u, (void*)e->p_act})
     (void)hipFree(q);
@@ -427,7 +426,6 @@ int qd_engine_create_from_image(const void* image, long long bytes, qd_engine** 
       {(void**)&e->weights, wbytes},  {(void**)&e->k_cache, e->kv_bytes}, {(void**)&e->v_cache, e->kv_bytes},
       {(void**)&e->x, H * 2},         {(void**)&e->qkv, 3 * H * 2},     {(void**)&e->attn_out, H * 2},
       {(void**)&e->act, I * 2},       {(void**)&e->logits, V * 2},      {&e->lm_ws, (long long)e->lm_ws_bytes},
-      {(void**)&e->d_token, 4},
       {(void**)&e->p_tokens, (long long)kPrefillChunk * 4},
       {(void**)&e->p_x, (long long)kPrefillChunk * H * 2},
       {(void**)&e->p_xn, (long long)kPrefillChunk * H * 2},
@@ -442,7 +440,10 @@ int qd_engine_create_from_image(const void* image, long long bytes, qd_engine** 
       return fail(QD_ENOMEM, "hipMalloc of %lld bytes failed: %s", a.n, hipGetErrorString(he));
     }
   }
-  if ((he = hipHostMalloc((void**)&e->h_token, sizeof(int), hipHostMallocDefault)) != hipSuccess ||
+  // The next token goes straight from the argmax kernel into mapped pinned
+  // memory: no device-to-host copy (a blit kernel of its own) per token.
+  if ((he = hipHostMalloc((void**)&e->h_token, sizeof(int), hipHostMallocMapped)) != hipSuccess ||
+      (he = hipHostGetDevicePointer((void**)&e->h_token_dev, e->h_token, 0)) != hipSuccess ||
       (he = hipStreamCreate(&e->stream)) != hipSuccess ||
       (he = hipMemcpy(e->weights, static_cast<const char*>(image) + QD_MODEL_HEADER_BYTES,
                       (size_t)wbytes, hipMemcpyHostToDevice)) != hipSuccess) {
@@ -499,7 +500,6 @@ int qd_engine_reset(qd_engine* e) {
       (he = hipMemsetAsync(e->attn_out, 0, (size_t)H * 2, e->stream)) != hipSuccess ||
       (he = hipMemsetAsync(e->act, 0, (size_t)e->cfg.intermediate_size * 2, e->stream)) != hipSuccess ||
       (he = hipMemsetAsync(e->logits, 0, (size_t)e->cfg.vocab_size * 2, e->stream)) != hipSuccess ||
-      (he = hipMemsetAsync(e->d_token, 0, 4, e->stream)) != hipSuccess ||
       (he = hipStreamSynchronize(e->stream)) != hipSuccess)
     return hip_fail(he, "engine reset");
   return QD_OK;
@@ -539,14 +539,11 @@ int qd_engine_step(qd_engine* e, int token, int pos, int* next_token) {
   if ((rc = run_layers(e, token, pos)) != QD_OK) return rc;
   rc = qd_lm_head_argmax(e->x, e->w(e->lay.ln_f), kEps, e->w(e->lay.lm_head), e->logits,
                          (int)e->cfg.vocab_size, (int)e->cfg.hidden_size, e->lm_ws, e->lm_ws_bytes,
-                         e->d_token, e->stream);
+                         e->h_token_dev, e->stream);
   if (rc != QD_OK) return rc;
-  hipError_t he;
-  if ((he = hipMemcpyAsync(e->h_token, e->d_token, sizeof(int), hipMemcpyDeviceToHost, e->stream)) !=
-          hipSuccess ||
-      (he = hipStreamSynchronize(e->stream)) != hipSuccess)
-    return hip_fail(he, "decode step");
-  *next_token = *e->h_token;
+  const hipError_t he = hipStreamSynchronize(e->stream);
+  if (he != hipSuccess) return hip_fail(he, "decode step");
+  *next_token = *static_cast<volatile int*>(e->h_token);
   return QD_OK;
 }
 
