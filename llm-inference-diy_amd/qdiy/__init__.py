@@ -152,7 +152,7 @@ def _ptr(t: torch.Tensor, name: str, contiguous: bool = True) -> ctypes.c_void_p
 
 
 class Context:
-    """Owns a qd_ctx (split scratch, merge counters, RoPE table) on the current device."""
+    """Owns a qd_ctx (split-KV partials and the RoPE cos/sin table) on the current device."""
 
     def __init__(self, num_heads: int = 16, max_seqlen: int = 2048, kv_row_stride: int | None = None,
                  kv_head_stride: int = HEAD_DIM, rope_base: float = 10000.0,

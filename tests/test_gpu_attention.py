@@ -157,7 +157,7 @@ def test_bench_constant_inputs_bit_exact(qdiy, L):
     g.close()
 
 
-def test_repeat_calls_are_deterministic_and_counters_reset(qdiy):
+def test_repeat_calls_are_deterministic_and_scratch_is_reused(qdiy):
     case = AttnCase(5000, H=16, seed=7)
     g = GpuCase(qdiy, case)
     a = g.run(variant="split", num_splits=40)
