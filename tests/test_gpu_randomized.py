@@ -171,3 +171,36 @@ def test_qkv_front_random_shapes(qdiy, seed):
     case = f"H={H} S={S} pos={pos} norm={with_norm} bias={with_bias}"
     for name, w, g in zip(("qkv", "k_cache", "v_cache"), (o_qkv, o_k, o_v), (g_qkv, g_k, g_v)):
         assert _same(w, g.cpu().numpy()), f"{name}: {case}"
+
+
+def _engine_plans(qdiy, cfg, n):
+    """The engine's attention plans at lengths 1..n (its context has the same
+    heads, cache layout and device, hence the same planner decisions)."""
+    with qdiy.Context(num_heads=cfg.num_heads, max_seqlen=cfg.max_seqlen,
+                      kv_row_stride=cfg.hidden_size, kv_head_stride=D) as ctx:
+        return [oracle.Plan(*ctx.plan_detail(L).as_tuple()) for L in range(1, n + 1)]
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_engine_random_models(qdiy, seed):
+    """Random model shapes and prompt lengths, some crossing the fused/split
+    boundary (224 rows) and the 256-token prefill chunk: greedy tokens and the
+    last step's logits equal the oracle's."""
+    rng = np.random.default_rng(75000 + seed)
+    heads = 4 * int(rng.integers(1, 3))
+    n_prompt = int(rng.integers(1, 41) if rng.random() < 0.5 else rng.integers(200, 301))
+    n_new = int(rng.integers(4, 13))
+    cfg = qdiy.model_cfg(vocab_size=int(rng.integers(50, 3000)), hidden_size=heads * D,
+                         num_layers=int(rng.integers(1, 3)), num_heads=heads,
+                         intermediate_size=8 * int(rng.integers(16, 257)),
+                         max_seqlen=n_prompt + n_new + int(rng.integers(0, 20)))
+    img = qdiy.random_model_image(cfg, 1000 + seed, float(rng.uniform(0.02, 0.1)))
+    prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, n_prompt)]
+    with qdiy.Engine(image=img) as eng:
+        got = eng.generate(prompt, n_new, stop_at_eos=False)
+        got_logits = eng.logits()
+    want, want_logits = oracle.generate(img, prompt, n_new, _engine_plans(qdiy, cfg, n_prompt + n_new))
+    case = (f"heads={heads} layers={cfg.num_layers} inter={cfg.intermediate_size} "
+            f"vocab={cfg.vocab_size} prompt={n_prompt} new={n_new}")
+    assert got == want, case
+    assert _same(got_logits, want_logits), case
