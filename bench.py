@@ -355,8 +355,12 @@ def main() -> int:
             "config4_front_end": front,
             "config5_e2e": e2e,
         },
-        "roofline": {"bound": "hbm", "achieved": round(head["gbps"], 1), "peak": PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": traffic},
+        "roofline": {"bound": "hbm",
+                     "kernel": f"qd_decode_attention call ({head['plan']}: "
+                               "decode_attention_scan_kernel + decode_attention_merge_kernel)",
+                     "achieved": round(head["gbps"], 1), "peak": PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": traffic,
+                     "per_kernel_trace": "profiles/decode_attention_kernel_trace_L512_L8192_L32768.md"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
