@@ -174,7 +174,7 @@ def measure_front(lib, steps: int, warmup: int):
     del w, kc, vc
     torch.cuda.empty_cache()
     front_bytes = w_elems * 2 + HID * 2 + 3 * HID * 2 + 2 * HID * 2
-    all_bytes = front_bytes + 2 * L * HID * 2 + HID * 2      # 41,971,712
+    all_bytes = front_bytes + 2 * L * HID * 2 + HID * 2      # config 4 (L=2048): 41,971,712 B
     log(f"[bench] config 4 (L=2048, pos 2047): front end {us_front:.2f} us "
         f"({front_bytes / us_front / 1e3:.0f} GB/s), front end + attention {us_all:.2f} us "
         f"({all_bytes / us_all / 1e3:.0f} GB/s), {n_layers} layers rotated")
