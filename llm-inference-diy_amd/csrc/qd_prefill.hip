@@ -72,19 +72,68 @@ __global__ __launch_bounds__(256) void rmsnorm_batched_kernel(const uint16_t* __
   }
 }
 
+// 16-byte chunks of one token tile that each thread stages into LDS: a tile
+// holds tok_tile(NJ) rows of at most NJ * 64 chunks, spread over the
+// workgroup's threads.
+constexpr int stage_chunks(int nj) { return (tok_tile(nj) * nj * 64 + kGemvWaves * 64 - 1) / (kGemvWaves * 64); }
+
+// DPP row rotations (gfx9 encodings): lane i of a 16-lane row reads lane
+// (i - n) mod 16.
+constexpr int kDppRowRor4 = 0x124;
+constexpr int kDppRowRor8 = 0x128;
+
+// The four sums of a 2-token x 2-row block, s0 = (t, na), s1 = (t+1, na),
+// s2 = (t, nb), s3 = (t+1, nb), reduced over the wave in one transposed
+// butterfly.  Afterwards lane 12 + q (q = token bit + 2 * row bit) of row 0
+// holds block output q's total.  Every total is the sum wave64_sum forms,
+// node for node, so the bits are the decode kernels':
+//   lanes i, i^1  -- even lanes keep token t's two sums, odd lanes token t+1's;
+//   lanes i, i^2  -- the quad's lanes with bit 1 clear keep row na, set row nb;
+//                    every lane now holds a quad sum Q of its own output;
+//   row_ror 4     -- lanes 4..7 and 12..15 add the quad before: Q1 + Q0 and
+//                    Q3 + Q2 (wave64_sum pairs the same quads by a half-row
+//                    mirror, whose lanes all hold the same quad sum);
+//   row_ror 8     -- lanes 12..15 add lanes 4..7: the row sum (the mirror
+//                    step of wave64_sum);
+//   xor 16, xor 32 -- the rows, as in wave64_sum.
+// IEEE addition is commutative, so the operand order inside a node does not
+// change its bits.
+__device__ __forceinline__ float block4_sum(float s0, float s1, float s2, float s3, int lane) {
+  const bool odd = lane & 1;
+  float k0 = odd ? s1 : s0;
+  float k1 = odd ? s3 : s2;
+  const float g0 = odd ? s0 : s1;
+  const float g1 = odd ? s2 : s3;
+  k0 += dpp_mov<kDppQuadSwap1>(g0);
+  k1 += dpp_mov<kDppQuadSwap1>(g1);
+  const bool hi = lane & 2;
+  float k = hi ? k1 : k0;
+  const float g = hi ? k0 : k1;
+  k += dpp_mov<kDppQuadSwap2>(g);
+  k += dpp_mov<kDppRowRor4>(k);
+  k += dpp_mov<kDppRowRor8>(k);
+  k += __shfl_xor(k, 16);
+  k += __shfl_xor(k, 32);
+  return k;
+}
+
 // Y[t][n] for n in this workgroup's 16 rows and t in its kTokPerWg tokens.
 // Wave w holds rows n0 = 16*bx + 2w and n0 + 1 (NJ chunks of 8 per lane, the
 // last one masked when K is not a multiple of 512).  Token tiles of kTokTile
 // rows of X are staged in LDS; each lane reads its 16-byte chunks from them
-// (consecutive lanes, consecutive 16 B: conflict-free).  Two tokens and two
+// (consecutive lanes, consecutive 16 B: conflict-free).  The next tile's
+// global loads are issued into registers before the current tile is
+// consumed, so their latency hides behind its arithmetic.  Two tokens and two
 // rows are summed at a time: four independent sequential sums per lane, each
-// in the decode order, then four wave64 reductions.
+// in the decode order, then one transposed wave reduction (block4_sum) whose
+// four totals four lanes store.
 //   kEpi 0: Y[t][n] = half(sum)
 //   kEpi 1: Y[t][n] = half(R[t][n] + half(sum))     (residual add; R may be Y)
 template <int NJ, int kEpi>
 __global__ __launch_bounds__(kGemvWaves * 64) void gemv_batched_kernel(BatchedGemvParams p) {
   extern __shared__ __align__(16) uint16_t xs[];        // [kTokTile][NJ * 512]
   constexpr int kTokTile = tok_tile(NJ);
+  constexpr int kStage = stage_chunks(NJ);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int K = p.k;
@@ -102,16 +151,51 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_batched_kernel(BatchedGe
   }
   const int t_begin = blockIdx.y * kTokPerWg;
   const int t_end = min(p.t, t_begin + kTokPerWg);
-  const int chunks = K / 8;                              // 16-byte chunks per token row
+  // This thread's staging chunks: chunk c = tid + 512 i is token c / chunks of
+  // the tile, 16-byte chunk c % chunks of its row.  Up to NJ = 11 the map is
+  // kept in registers and the next tile's loads are in flight while the
+  // current tile is consumed.  Above that the registers are not there (the
+  // weights alone take 16 * NJ), so each chunk is loaded and stored in turn.
+  constexpr bool kPrefetch = NJ <= 11;
+  const int chunks = K / 8;
+  constexpr int kMap = kPrefetch ? kStage : 1;
+  int st_tok[kMap], st_kc[kMap];
+  f16x8 stage[kMap];
+  if constexpr (kPrefetch) {
+#pragma unroll
+    for (int i = 0; i < kStage; ++i) {
+      const int c = threadIdx.x + i * kGemvWaves * 64;
+      st_tok[i] = c / chunks;
+      st_kc[i] = c - st_tok[i] * chunks;
+    }
+  }
+  // Loads are unconditional (a chunk past the tile reloads the tile's last
+  // token), so they form one straight run with no wait between them; only the
+  // LDS stores are predicated.
+  auto fetch = [&](int t0, int nt) {
+#pragma unroll
+    for (int i = 0; i < kMap; ++i) {
+      const int tk = min(st_tok[i], nt - 1);
+      stage[i] = *reinterpret_cast<const f16x8*>(p.x + (long long)(t0 + tk) * p.ldx + st_kc[i] * 8);
+    }
+  };
+  if (kPrefetch && t_begin < t_end) fetch(t_begin, min(kTokTile, t_end - t_begin));
   for (int t0 = t_begin; t0 < t_end; t0 += kTokTile) {
     const int nt = min(kTokTile, t_end - t0);
     __syncthreads();                                     // previous tile fully consumed
-    for (int c = threadIdx.x; c < nt * chunks; c += kGemvWaves * 64) {
-      const int tt = c / chunks, kc = c - tt * chunks;
-      *reinterpret_cast<f16x8*>(xs + tt * (NJ * 512) + kc * 8) =
-          *reinterpret_cast<const f16x8*>(p.x + (long long)(t0 + tt) * p.ldx + kc * 8);
+    if constexpr (kPrefetch) {
+#pragma unroll
+      for (int i = 0; i < kStage; ++i)
+        if (st_tok[i] < nt) *reinterpret_cast<f16x8*>(xs + st_tok[i] * (NJ * 512) + st_kc[i] * 8) = stage[i];
+    } else {
+      for (int c = threadIdx.x; c < nt * chunks; c += kGemvWaves * 64) {
+        const int tt = c / chunks, kc = c - tt * chunks;
+        *reinterpret_cast<f16x8*>(xs + tt * (NJ * 512) + kc * 8) =
+            *reinterpret_cast<const f16x8*>(p.x + (long long)(t0 + tt) * p.ldx + kc * 8);
+      }
     }
     __syncthreads();
+    if (kPrefetch && t0 + kTokTile < t_end) fetch(t0 + kTokTile, min(kTokTile, t_end - t0 - kTokTile));
     for (int tt = 0; tt < nt; tt += 2) {
       const bool two = tt + 1 < nt;
       const uint16_t* x0 = xs + tt * (NJ * 512);
@@ -131,19 +215,13 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_batched_kernel(BatchedGe
           }
         }
       }
-      a0 = wave64_sum(a0);
-      a1 = wave64_sum(a1);
-      b0 = wave64_sum(b0);
-      b1 = wave64_sum(b1);
-      if (lane == 0 && n0 < p.n) {
-        const float sums[4] = {a0, b0, a1, b1};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int t = t0 + tt + (q >> 1);
-          const int n = n0 + (q & 1);
-          if ((q >> 1) == 1 && !two) continue;
-          if (n >= p.n) continue;
-          const _Float16 y = to_f16(sums[q]);
+      const float sum = block4_sum(a0, a1, b0, b1, lane);
+      const int q = lane - 12;                           // lanes 12..15 store
+      if (q >= 0 && q < 4) {
+        const int t = t0 + tt + (q & 1);
+        const int n = n0 + (q >> 1);
+        if ((two || (q & 1) == 0) && n < p.n) {
+          const _Float16 y = to_f16(sum);
           _Float16* dst = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
           if constexpr (kEpi == 0) {
             *dst = y;
