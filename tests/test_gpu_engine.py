@@ -190,6 +190,26 @@ def test_prefill_batches_equal_token_by_token(qdiy):
     assert tok == outs[0][0] and _same(lg, outs[0][1])
 
 
+@pytest.mark.parametrize("hidden,inter", [(2560, 2600), (3584, 4104), (4096, 5120), (512, 5640),
+                                          (1024, 8192)])
+def test_prefill_gemm_widths(qdiy, hidden, inter):
+    """The batched prefill GEMM at every row width the engine accepts: K = hidden
+    takes 5, 7 or 8 chunks of 512 per lane, K = inter 6-10 (with a ragged last
+    chunk, next-tile prefetch) and 12 or 16 (no prefetch: the registers are not
+    there).  41 prompt tokens span two 32-token groups and partial token tiles.
+    Greedy tokens and the last logits equal the oracle's bit for bit."""
+    cfg = qdiy.model_cfg(vocab_size=300, hidden_size=hidden, num_layers=1, num_heads=hidden // 128,
+                         intermediate_size=inter, max_seqlen=48)
+    img = qdiy.random_model_image(cfg, 31 + hidden + inter, 0.03, nthreads=8)
+    prompt = [int(t) for t in np.random.default_rng(hidden + inter).integers(0, 300, 41)]
+    with qdiy.Engine(image=img) as eng:
+        got = eng.generate(prompt, 3, stop_at_eos=False)
+        got_logits = eng.logits()
+    want, want_logits = oracle.generate(img, prompt, 3, _plans(qdiy, cfg, 44))
+    assert got == want, f"hidden={hidden} inter={inter}"
+    assert _same(got_logits, want_logits), f"hidden={hidden} inter={inter}"
+
+
 def test_engine_rejects_bad_input(qdiy, tmp_path):
     cfg = qdiy.model_cfg(**TINY)
     img = qdiy.random_model_image(cfg, 23)
