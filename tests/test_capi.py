@@ -39,6 +39,32 @@ def test_library_exports_every_declared_symbol(qdiy):
     assert set(_declared()) == set(qdiy.EXPORTS)
 
 
+def test_missing_library_fails_loudly(qdiy, monkeypatch):
+    """Without libqdiy.so the package raises; there is no other code path."""
+    monkeypatch.setattr(qdiy, "_lib", None)
+    monkeypatch.setattr(qdiy, "LIB_PATH", os.path.join(ROOT, "no_such_dir", "libqdiy.so"))
+    with pytest.raises(RuntimeError, match="is not built"):
+        qdiy.load()
+    with pytest.raises(RuntimeError, match="is not built"):
+        qdiy.Context(num_heads=16, max_seqlen=8)
+
+
+def test_product_sources_do_not_reach_the_oracle():
+    """The package (Python binding and native sources) never imports, includes or
+    links the oracle: it is test infrastructure only."""
+    pkg = os.path.join(ROOT, "llm-inference-diy_amd")
+    pat = re.compile(r"^\s*(?:from\s+oracle\b|import\s+oracle\b|#\s*include\s*[<\"][^>\"]*qd_oracle)"
+                     r"|libqd_oracle|oracle/", re.M)
+    hits = []
+    for d, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".h")):
+                path = os.path.join(d, f)
+                if pat.search(open(path, errors="replace").read()):
+                    hits.append(os.path.relpath(path, ROOT))
+    assert hits == []
+
+
 def test_version_and_limits(qdiy):
     assert re.match(r"^\d+\.\d+\.\d+$", qdiy.version())
     assert qdiy.max_splits() >= 64
