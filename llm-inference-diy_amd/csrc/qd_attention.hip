@@ -215,8 +215,12 @@ __device__ __forceinline__ void wave_merge(GroupState& st) {
 // folded in LDS by threads 0..127, one dim each.  kSplit = false is the
 // single-workgroup-per-head path (fd_v5_fused_kernel's role): it writes the
 // normalised fp16 output.  kSplit = true writes the workgroup's unnormalised
-// fp32 partial (m, l, O[128]) to slot h * splits + c.
-template <int NW, int U, bool kSplit>
+// fp32 partial (m, l, O[128]) to slot h * splits + c.  kBatch (with kSplit):
+// query b = blockIdx.y over seqlen + b rows plans itself (auto_split), the
+// workgroups past its split count exit, and its partials go to slots
+// (b * num_heads + h) * split_stride + c; every workgroup that runs does
+// exactly the work of the same workgroup of that query's single call.
+template <int NW, int U, bool kSplit, bool kBatch = false>
 __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnParams p) {
   __shared__ float so[NW][kD];
   __shared__ float sm[NW];
@@ -228,9 +232,14 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
   const int t = lane & 15;
   const int h = blockIdx.x % p.num_heads;
   const int c = blockIdx.x / p.num_heads;
-  const int b = blockIdx.y;                   // query of a batched fused call, else 0
+  const int b = blockIdx.y;                   // query of a batched call, else 0
   const int seqlen = p.seqlen + b;
-  const int rows_per_split = kSplit ? p.rows_per_split : seqlen;
+  int rows_per_split = kSplit ? p.rows_per_split : seqlen;
+  int splits = p.splits;
+  if constexpr (kBatch) {
+    auto_split(seqlen, p.num_cus, p.num_heads, &splits, &rows_per_split);
+    if (c >= splits) return;                  // workgroup-uniform: this query has fewer splits
+  }
   const int r0 = c * rows_per_split;
   const int nrows = min(seqlen - r0, rows_per_split);
 
@@ -264,7 +273,8 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
       O = __builtin_fmaf(wt, so[w][tid], O);
     }
     if constexpr (kSplit) {
-      const long long slot = (long long)h * p.splits + c;
+      const long long slot = kBatch ? ((long long)b * p.num_heads + h) * p.split_stride + c
+                                    : (long long)h * splits + c;
       p.part_o[slot * kD + tid] = O;
       if (tid == 0) p.part_ml[slot] = float2{M, L};
     } else {
@@ -275,6 +285,8 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
 
 // Stage 2: one workgroup per head folds the head's p.splits partials with the
 // log-sum-exp rule (fd_opt_stage2_kernel's role) and writes the fp16 output.
+// kBatch: workgroup (h, b = blockIdx.y) folds query b's auto_split partials
+// from its slots (see the scan kernel) into out + b * out_batch_stride.
 // Max-first: thread (dq = tid % 32 -> dims 4dq..4dq+3, slice = tid / 32)
 // takes splits slice, slice + P, ...; the slices' maxima meet in LDS, so all
 // threads share the head's maximum M before any exponential.  Each thread
@@ -282,7 +294,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
 // ascending order with fmaf, issuing B splits' loads at a time, and the P
 // slice sums are added in LDS (slice order).  The kernel boundary after
 // stage 1 makes every partial visible on every XCD.
-template <int NT>
+template <int NT, bool kBatch = false>
 __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p) {
   constexpr int P = NT / 32;
   constexpr int B = 8;
@@ -293,23 +305,33 @@ __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p
   const int h = blockIdx.x;
   const int dq = tid & 31;
   const int slice = tid >> 5;
-  const float* po = p.part_o + (long long)h * p.splits * kD + dq * 4;
-  const float2* pml = p.part_ml + (long long)h * p.splits;
+  int splits = p.splits;
+  long long first = (long long)h * p.splits;  // this head's first partial slot
+  _Float16* out = reinterpret_cast<_Float16*>(p.out);
+  if constexpr (kBatch) {
+    const int b = blockIdx.y;
+    int rows;
+    auto_split(p.seqlen + b, p.num_cus, p.num_heads, &splits, &rows);
+    first = ((long long)b * p.num_heads + h) * p.split_stride;
+    out += b * p.out_batch_stride;
+  }
+  const float* po = p.part_o + first * kD + dq * 4;
+  const float2* pml = p.part_ml + first;
   // First batch of this thread's splits (slice, slice + P, ..., B of them),
   // loaded before the maximum is known so one memory round trip serves both.
   float2 ml[B];
   f32x4 ov[B];
 #pragma unroll
   for (int j = 0; j < B; ++j) {
-    const int cc = min(slice + j * P, p.splits - 1);
+    const int cc = min(slice + j * P, splits - 1);
     ml[j] = pml[cc];
     ov[j] = *reinterpret_cast<const f32x4*>(po + (long long)cc * kD);
   }
   float mm = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < B; ++j)
-    if (slice + j * P < p.splits) mm = fmaxf(mm, ml[j].x);
-  for (int c = slice + B * P; c < p.splits; c += P) mm = fmaxf(mm, pml[c].x);
+    if (slice + j * P < splits) mm = fmaxf(mm, ml[j].x);
+  for (int c = slice + B * P; c < splits; c += P) mm = fmaxf(mm, pml[c].x);
   if (dq == 0) sm[slice] = mm;
   __syncthreads();
   float M = sm[0];
@@ -321,7 +343,7 @@ __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p
   for (int c0 = slice;;) {
 #pragma unroll
     for (int j = 0; j < B; ++j) {
-      if (c0 + j * P < p.splits) {
+      if (c0 + j * P < splits) {
         const float w = exp2_rep_nonpos(ml[j].x - base);
         ll = __builtin_fmaf(w, ml[j].y, ll);
 #pragma unroll
@@ -329,10 +351,10 @@ __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p
       }
     }
     c0 += B * P;
-    if (c0 >= p.splits) break;
+    if (c0 >= splits) break;
 #pragma unroll
     for (int j = 0; j < B; ++j) {
-      const int cc = min(c0 + j * P, p.splits - 1);
+      const int cc = min(c0 + j * P, splits - 1);
       ml[j] = pml[cc];
       ov[j] = *reinterpret_cast<const f32x4*>(po + (long long)cc * kD);
     }
@@ -347,7 +369,7 @@ __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p
       L += sl[s];
       O += so[s][tid];
     }
-    reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = to_f16(O / L);
+    out[h * kD + tid] = to_f16(O / L);
   }
 }
 
@@ -368,6 +390,20 @@ static void launch_scan(const AttnParams& p, int rows_per_tile, dim3 grid, hipSt
 hipError_t launch_decode_attention_fused_batch(const AttnParams& p, int tokens, hipStream_t stream) {
   hipLaunchKernelGGL((decode_attention_scan_kernel<16, 4, false>), dim3(p.num_heads, tokens),
                      dim3(16 * 64), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_attention_split_batch(const AttnParams& p, int rows_per_tile, int tokens,
+                                               hipStream_t stream) {
+  const dim3 scan_grid(p.num_heads * p.split_stride, tokens);
+  if (rows_per_tile == 4)
+    hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, true>), scan_grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_attention_scan_kernel<4, 2, true, true>), scan_grid, dim3(256), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((decode_attention_merge_kernel<256, true>), dim3(p.num_heads, tokens), dim3(256), 0,
+                     stream, p);
   return hipGetLastError();
 }
 

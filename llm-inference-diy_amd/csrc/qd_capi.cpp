@@ -45,12 +45,9 @@ using qd::hip_fail;
 //   * longer: one split workgroup per CU in total (16 splits at 16 heads), each
 //     looping over its rows (6.0 us at 256-512 rows, 15.3 at 8192, 42.2 at
 //     32768), except two per CU between 1025 and 2048 rows; other split counts
-//     or more waves per workgroup measured no better.
-// Each split keeps at least kMinRowsPerSplit rows.
+//     or more waves per workgroup measured no better (qd::auto_split).
 constexpr int kFusedMaxRows = 224;
-constexpr int kMinRowsPerSplit = 16;
-constexpr int kTwoPerCuMin = 1024;   // (1024, 2048] rows: two split workgroups per CU
-constexpr int kTwoPerCuMax = 2048;   // (8.1 vs 8.5 us at 2048)
+constexpr int kPrefillBatch = 256;   // split-plan prefill queries per batched launch pair
 
 qd::AttnPlan plan_fused(int seqlen) {
   qd::AttnPlan plan;
@@ -63,20 +60,19 @@ qd::AttnPlan plan_fused(int seqlen) {
 }
 
 qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
-  int splits = requested;
-  if (splits <= 0) {
-    splits = (seqlen > kTwoPerCuMin && seqlen <= kTwoPerCuMax ? 2 : 1) * ctx->num_cus / ctx->cfg.num_heads;
-    const int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
-    if (splits > by_rows) splits = by_rows;
+  int splits, rows;
+  if (requested <= 0) {
+    qd::auto_split(seqlen, ctx->num_cus, ctx->cfg.num_heads, &splits, &rows);
+  } else {
+    splits = std::min(requested, qd::kMaxSplits);
+    rows = (seqlen + splits - 1) / splits;
+    rows = (rows + 3) & ~3;                    // one load instruction covers 4 rows
+    splits = (seqlen + rows - 1) / rows;       // no empty workgroups
   }
-  if (splits < 1) splits = 1;
-  if (splits > qd::kMaxSplits) splits = qd::kMaxSplits;
-  int rows = (seqlen + splits - 1) / splits;
-  rows = (rows + 3) & ~3;                      // one load instruction covers 4 rows
   qd::AttnPlan plan;
   plan.variant = 1;
   plan.rows_per_split = rows;
-  plan.splits = (seqlen + rows - 1) / rows;    // no empty workgroups
+  plan.splits = splits;
   plan.waves = 4;
   plan.rows_per_tile = rows >= 64 ? 4 : 2;
   return plan;
@@ -131,6 +127,8 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));  // log2(e)/sqrt(128)
   p.q_batch_stride = 0;
   p.out_batch_stride = 0;
+  p.num_cus = ctx->num_cus;
+  p.split_stride = plan.splits;
   return p;
 }
 
@@ -164,10 +162,45 @@ int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const 
     const hipError_t e = qd::launch_decode_attention_fused_batch(p, n_fused, stream);
     if (e != hipSuccess) return hip_fail(e, "batched fused attention launch");
   }
-  for (int t = n_fused; t < tokens; ++t) {
-    rc = run_attention(ctx, q + t * q_stride, k, v, out + t * out_stride, pos0 + t + 1,
-                       plan_auto(ctx, pos0 + t + 1), stream);
-    if (rc != QD_OK) return rc;
+  // The others take split plans.  Runs of consecutive queries whose plans
+  // share a tile depth go out as one batched split launch pair, every query
+  // under its own plan (at most kPrefillBatch queries per pair).
+  if (n_fused >= tokens) return QD_OK;
+  if (!ctx->pf_part_o) {
+    // slots for kPrefillBatch queries x H heads x the largest automatic split count
+    const int stride = std::max(1, std::min(qd::kMaxSplits, 2 * ctx->num_cus / ctx->cfg.num_heads));
+    const size_t slots = (size_t)kPrefillBatch * ctx->cfg.num_heads * stride;
+    hipError_t e = hipMalloc(&ctx->pf_part_o, slots * 128 * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(&ctx->pf_part_ml, slots * sizeof(float2));
+    if (e != hipSuccess) {
+      (void)hipFree(ctx->pf_part_o);
+      ctx->pf_part_o = nullptr;
+      ctx->pf_part_ml = nullptr;
+      return fail(QD_ENOMEM, "hipMalloc of %zu bytes of prefill attention scratch failed", slots * 130 * 4);
+    }
+    ctx->pf_tokens = kPrefillBatch;
+    ctx->pf_stride = stride;
+  }
+  for (int t = n_fused; t < tokens;) {
+    const qd::AttnPlan first = plan_auto(ctx, pos0 + t + 1);
+    int t1 = t + 1, max_splits = first.splits;
+    for (; t1 < tokens && t1 - t < ctx->pf_tokens; ++t1) {
+      const qd::AttnPlan pl = plan_auto(ctx, pos0 + t1 + 1);
+      if (pl.rows_per_tile != first.rows_per_tile) break;
+      max_splits = std::max(max_splits, pl.splits);
+    }
+    if (max_splits > ctx->pf_stride)
+      return fail(QD_EINVAL, "internal: %d splits above the prefill scratch's %d", max_splits, ctx->pf_stride);
+    qd::AttnParams p = make_params(ctx, q + t * q_stride, k, v, out + t * out_stride, pos0 + t + 1, first);
+    p.q_batch_stride = q_stride;
+    p.out_batch_stride = out_stride;
+    p.part_o = ctx->pf_part_o;
+    p.part_ml = ctx->pf_part_ml;
+    p.num_cus = ctx->num_cus;
+    p.split_stride = max_splits;
+    const hipError_t e = qd::launch_decode_attention_split_batch(p, first.rows_per_tile, t1 - t, stream);
+    if (e != hipSuccess) return hip_fail(e, "batched split attention launch");
+    t = t1;
   }
   return QD_OK;
 }
@@ -250,6 +283,8 @@ int qd_ctx_destroy(qd_ctx* ctx) {
   if (ctx->part_o) (void)hipFree(ctx->part_o);
   if (ctx->part_ml) (void)hipFree(ctx->part_ml);
   if (ctx->rope_cs) (void)hipFree(ctx->rope_cs);
+  if (ctx->pf_part_o) (void)hipFree(ctx->pf_part_o);
+  if (ctx->pf_part_ml) (void)hipFree(ctx->pf_part_ml);
   if (switch_dev) (void)hipSetDevice(dev);
   delete ctx;
   return QD_OK;

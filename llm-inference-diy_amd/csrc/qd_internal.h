@@ -13,6 +13,32 @@ namespace qd {
 // num_heads * kMaxSplits * (128 + 2) floats (2.1 MB at 16 heads).
 constexpr int kMaxSplits = 256;
 
+// Split planner constants, from measured sweeps on MI355X (16 heads, cold KV):
+// one split workgroup per CU in total, two per CU between kTwoPerCuMin and
+// kTwoPerCuMax rows (8.1 vs 8.5 us at 2048), each split at least
+// kMinRowsPerSplit rows.
+constexpr int kMinRowsPerSplit = 16;
+constexpr int kTwoPerCuMin = 1024;   // (1024, 2048] rows: two split workgroups per CU
+constexpr int kTwoPerCuMax = 2048;
+
+// The split plan of a query over `seqlen` rows when the caller names no split
+// count: num_cus / num_heads workgroups per head ((2 * num_cus) / num_heads in
+// (kTwoPerCuMin, kTwoPerCuMax]), at most one per kMinRowsPerSplit rows, rows
+// per split rounded up to a multiple of 4 (one load instruction covers 4 rows)
+// and no empty workgroups.  The host planner and the batched prefill kernels,
+// which plan every query for itself, both evaluate this one function.
+__host__ __device__ inline void auto_split(int seqlen, int num_cus, int num_heads, int* splits, int* rows) {
+  int s = (seqlen > kTwoPerCuMin && seqlen <= kTwoPerCuMax ? 2 : 1) * num_cus / num_heads;
+  const int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
+  if (s > by_rows) s = by_rows;
+  if (s < 1) s = 1;
+  if (s > kMaxSplits) s = kMaxSplits;
+  int r = (seqlen + s - 1) / s;
+  r = (r + 3) & ~3;
+  *rows = r;
+  *splits = (seqlen + r - 1) / r;
+}
+
 // Per-launch arguments of the decode-attention kernels.  Offsets are in fp16
 // elements.
 struct AttnParams {
@@ -29,11 +55,16 @@ struct AttnParams {
   int splits;             // workgroups per head
   int rows_per_split;
   float scale_log2;       // log2(e) / sqrt(128)
-  // Batched single-workgroup-per-head calls (prefill): grid.y = tokens; token b
-  // reads q + b*q_batch_stride, writes out + b*out_batch_stride and attends
-  // over seqlen + b rows.  Zero strides and grid.y = 1 for a single call.
+  // Batched calls (prefill): grid.y = tokens; token b reads q + b*q_batch_stride,
+  // writes out + b*out_batch_stride and attends over seqlen + b rows.  Zero
+  // strides and grid.y = 1 for a single call.
   long long q_batch_stride;
   long long out_batch_stride;
+  // Batched split calls only: each token plans itself with auto_split(seqlen +
+  // b, num_cus, num_heads, ...); its partials sit at slots (b * num_heads + h) *
+  // split_stride + c.
+  int num_cus;
+  int split_stride;
 };
 
 struct RopeParams {
@@ -158,6 +189,13 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
 // queries at once, token b over p.seqlen + b rows: the arithmetic of the fused
 // plan of qd_decode_attention, query by query.
 hipError_t launch_decode_attention_fused_batch(const AttnParams& p, int tokens, hipStream_t stream);
+// Split attention of `tokens` queries at once, token b over p.seqlen + b rows,
+// each under its own auto_split plan (the plan qd_decode_attention picks for
+// that length): one scan launch of num_heads * p.split_stride workgroups per
+// token (those past a token's split count exit at once) and one merge launch.
+// Every token's plan must have rows_per_tile tile rows.
+hipError_t launch_decode_attention_split_batch(const AttnParams& p, int rows_per_tile, int tokens,
+                                               hipStream_t stream);
 hipError_t launch_qkv_bias_rope_cache(const RopeParams& p, hipStream_t stream);
 hipError_t launch_qkv_front(const QkvFrontParams& p, hipStream_t stream);
 hipError_t launch_proj_residual(const ProjResidualParams& p, hipStream_t stream);
@@ -186,8 +224,9 @@ namespace qd {
 // Attention of `tokens` consecutive queries at positions pos0, pos0 + 1, ...
 // (query t over pos0 + t + 1 rows; q and out rows q_stride / out_stride
 // elements apart), each with the arithmetic of qd_decode_attention's own plan
-// for its length: the fused-plan queries in one batched launch, the others one
-// call each.
+// for its length: the fused-plan queries in one batched launch, the split-plan
+// queries in batched scan + merge pairs, one per run of queries that share a
+// tile depth.
 int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k,
                       const uint16_t* v, uint16_t* out, long long out_stride, int pos0, int tokens,
                       hipStream_t stream);
@@ -200,4 +239,10 @@ struct qd_ctx {
   float2* rope_cs;        // [max_seqlen][64]
   float* part_o;          // [H][kMaxSplits][128]
   float2* part_ml;        // [H][kMaxSplits]
+  // Partials of batched split prefill attention, allocated on first use:
+  // [pf_tokens][H][pf_stride] slots of (128 + 2) floats.
+  float* pf_part_o;
+  float2* pf_part_ml;
+  int pf_tokens;
+  int pf_stride;
 };

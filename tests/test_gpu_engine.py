@@ -210,6 +210,29 @@ def test_prefill_gemm_widths(qdiy, hidden, inter):
     assert _same(got_logits, want_logits), f"hidden={hidden} inter={inter}"
 
 
+@pytest.mark.timeout(600)
+def test_long_prompt_batched_split_attention(qdiy):
+    """A 1100-token prompt on 16 heads: the prefill's attention runs fused up to
+    224 rows, then in batched split launches (one pair per run of queries with
+    one tile depth) across the planner's regimes -- 4-row tiles at 1009-1024
+    rows and two workgroups per CU from 1025 -- every query under its own
+    plan.  Greedy tokens and the last logits equal the oracle's, which
+    attends query by query."""
+    cfg = qdiy.model_cfg(vocab_size=300, hidden_size=2048, num_layers=1, num_heads=16,
+                         intermediate_size=512, max_seqlen=1112)
+    img = qdiy.random_model_image(cfg, 77, 0.03, nthreads=8)
+    prompt = [int(t) for t in np.random.default_rng(77).integers(0, 300, 1100)]
+    plans = _plans(qdiy, cfg, 1104)
+    assert {p.rows_per_tile for p in plans[224:]} == {2, 4}
+    assert max(p.num_splits for p in plans) > min(p.num_splits for p in plans[224:])
+    with qdiy.Engine(image=img) as eng:
+        got = eng.generate(prompt, 4, stop_at_eos=False)
+        got_logits = eng.logits()
+    want, want_logits = oracle.generate(img, prompt, 4, plans, nthreads=16)
+    assert got == want
+    assert _same(got_logits, want_logits)
+
+
 def test_engine_rejects_bad_input(qdiy, tmp_path):
     cfg = qdiy.model_cfg(**TINY)
     img = qdiy.random_model_image(cfg, 23)
