@@ -254,3 +254,38 @@ def test_invalid_arguments_raise(qdiy):
     with pytest.raises(ValueError):
         g.ctx.decode_attention(g.q, g.kc[:1000], g.vc, out, 64)       # cache too small (host check)
     g.close()
+
+
+def _planner_rules(L, H, cus, variant="auto", requested=0):
+    """The launch planner as its measured rules state it: fused (one 16-wave
+    workgroup per head, 4-row tiles) up to 224 rows; above, one split workgroup
+    per CU in total ((2 * CUs) // H per head in 1025-2048 rows), at most one per
+    16 rows, at most 256, rows per split rounded up to a multiple of 4, no
+    empty workgroups, 4 waves, 4-row tiles from 64 rows per split."""
+    if variant == "fused" or (variant == "auto" and L <= 224):
+        return (0, 1, L, 4, 16)
+    if requested > 0:
+        s = min(requested, 256)
+    else:
+        s = ((2 if 1024 < L <= 2048 else 1) * cus) // H
+        s = max(1, min(s, (L + 15) // 16, 256))
+    rows = -(-L // s)
+    rows = (rows + 3) & ~3
+    return (1, -(-L // rows), rows, 4 if rows >= 64 else 2, 4)
+
+
+@pytest.mark.parametrize("H", [1, 4, 12, 16, 24, 40])
+def test_planner_follows_its_rules(qdiy, H):
+    """Every plan the library reports equals the planner's stated rules at this
+    device's CU count, for automatic, fused and explicit split plans."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    lengths = sorted(set(list(range(1, 300)) + list(range(1000, 1100)) + list(range(2000, 2100)) +
+                         [4095, 4096, 4097, 8191, 8192, 8193, 16384, 32767, 32768]))
+    with qdiy.Context(num_heads=H, max_seqlen=32768) as ctx:
+        for L in lengths:
+            assert ctx.plan_detail(L).as_tuple() == _planner_rules(L, H, cus), (H, L)
+        for L in (1, 300, 8192):
+            assert ctx.plan_detail(L, "fused").as_tuple() == _planner_rules(L, H, cus, "fused"), L
+            for req in (1, 5, 16, 64, 300):
+                assert ctx.plan_detail(L, "split", min(req, qdiy.max_splits())).as_tuple() == \
+                    _planner_rules(L, H, cus, "split", min(req, qdiy.max_splits())), (L, req)
