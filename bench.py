@@ -11,8 +11,9 @@ enough layers (>= 1 GiB of K+V) that every call streams its rows from HBM, not
 from the 256 MB Infinity Cache.  The timed loop runs natively
 (libqdiy_bench.so) on torch's current stream between two HIP events; us/call
 = elapsed / steps.  L=8192 is measured first, then the other lengths in
-ascending order; each length allocates its own buffers.  achieved GB/s = algorithmic bytes per call / us per call
-with B(L) = 8192 + 8192*L (Q in, O out, K and V rows read once).
+ascending order; each length allocates its own buffers.  achieved GB/s =
+algorithmic bytes per call / us per call with B(L) = 8192 + 8192*L (Q in,
+O out, K and V rows read once).
 
 The CPU baseline is the repository's C restatement of the reference kernels
 (oracle/) on the host cores of the same box, on a bounded sample of the same
@@ -20,8 +21,9 @@ workload.
 
 Also measured and reported under `config`: config 4 (the fused QKV front end
 followed by attention at L=2048) and config 5 (greedy decode of a random-init
-Qwen-1.8B-shaped model through the engine: tokens/s and an estimate of the
-attention share of a decode step).
+Qwen-1.8B-shaped model through the engine: tokens/s, an estimate of the
+attention share of a decode step, and the prefill time of the 127-token prompt
+and of a 2048-token one).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
 """
@@ -190,7 +192,8 @@ def measure_e2e(lib, seed: int = 5, n_prompt: int = 128, n_new: int = 256):
     weights 1) in the .bin format, a prompt of n_prompt uniform-random ids, then
     n_new greedy tokens through qdiy.Engine (one synchronising step per token,
     as the reference engine).  Decode tokens/s is timed over the n_new steps;
-    the prompt runs through the decode path first and is timed separately."""
+    the prompt's first n_prompt - 1 tokens go through the batched prefill first
+    and are timed separately, and so, afterwards, is a 2048-token prompt."""
     import numpy as np
 
     import qdiy
@@ -215,6 +218,15 @@ def measure_e2e(lib, seed: int = 5, n_prompt: int = 128, n_new: int = 256):
         pos += 1
         toks.append(last)
     t_dec = time.perf_counter() - t0
+    # A long prompt: 2048 uniform-random ids through the batched exact prefill
+    # (fused attention up to 224 rows, batched split launches beyond), best of 2.
+    long_prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, 2048)]
+    t_long = float("inf")
+    for _ in range(2):
+        eng.reset()
+        t0 = time.perf_counter()
+        eng.prefill(long_prompt)
+        t_long = min(t_long, time.perf_counter() - t0)
     eng.close()
     ms_tok = t_dec * 1e3 / n_new
     # Attention per token: 24 qd_decode_attention calls at the mean KV length of
@@ -227,12 +239,14 @@ def measure_e2e(lib, seed: int = 5, n_prompt: int = 128, n_new: int = 256):
     tok_bytes = w_bytes + NL * 2 * mean_L * H_ * 2
     log(f"[bench] config 5: {n_new / t_dec:.1f} tokens/s ({ms_tok:.3f} ms/token, "
         f"{tok_bytes / (ms_tok * 1e-3) / 1e9:.0f} GB/s over {tok_bytes / 1e9:.3f} GB/token), "
-        f"prompt {n_prompt - 1} tokens in {t_prompt * 1e3:.1f} ms, attention share ~{100 * share:.1f}% "
+        f"prompt {n_prompt - 1} tokens in {t_prompt * 1e3:.1f} ms ({len(long_prompt)} in {t_long * 1e3:.0f} ms), "
+        f"attention share ~{100 * share:.1f}% "
         f"(24 x {att['us_cold']:.2f} us at L={mean_L}), image fill {t_fill:.1f} s")
     return {"model": "Qwen-1.8B shape, random init (library generator, std 0.02, norm weights 1)",
             "prompt_tokens": n_prompt, "generated_tokens": n_new,
             "tokens_per_s": round(n_new / t_dec, 2), "ms_per_token": round(ms_tok, 4),
-            "prompt_ms": round(t_prompt * 1e3, 2), "bytes_per_token": tok_bytes,
+            "prompt_ms": round(t_prompt * 1e3, 2),
+            "prompt_2048_ms": round(t_long * 1e3, 1), "bytes_per_token": tok_bytes,
             "gbps": round(tok_bytes / (ms_tok * 1e-3) / 1e9, 1),
             "attention_share_est": round(share, 4),
             "attention_us_per_call_at_mean_L": round(att["us_cold"], 3), "mean_L": mean_L,
