@@ -23,7 +23,7 @@ Also measured and reported under `config`: config 4 (the fused QKV front end
 followed by attention at L=2048) and config 5 (greedy decode of a random-init
 Qwen-1.8B-shaped model through the engine: tokens/s, an estimate of the
 attention share of a decode step, and the prefill time of the 127-token prompt
-and of a 2048-token one).
+and of a 2048-token one, exact and with the projections on the matrix cores).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
 """
@@ -219,14 +219,23 @@ def measure_e2e(lib, seed: int = 5, n_prompt: int = 128, n_new: int = 256):
         toks.append(last)
     t_dec = time.perf_counter() - t0
     # A long prompt: 2048 uniform-random ids through the batched exact prefill
-    # (fused attention up to 224 rows, batched split launches beyond), best of 2.
+    # (fused attention up to 224 rows, batched split launches beyond), best of 2;
+    # then both prompts with the projections on the matrix cores
+    # (qd_engine_set_prefill_mode(QD_GEMM_MFMA): not bit-identical to decode).
     long_prompt = [int(t) for t in rng.integers(0, cfg.vocab_size, 2048)]
-    t_long = float("inf")
-    for _ in range(2):
-        eng.reset()
-        t0 = time.perf_counter()
-        eng.prefill(long_prompt)
-        t_long = min(t_long, time.perf_counter() - t0)
+
+    def best_prefill(tokens):
+        best = float("inf")
+        for _ in range(2):
+            eng.reset()
+            t0 = time.perf_counter()
+            eng.prefill(tokens)
+            best = min(best, time.perf_counter() - t0)
+        return best
+
+    t_long = best_prefill(long_prompt)
+    eng.set_prefill_mode(qdiy.GEMM_MFMA)
+    t_prompt_mfma, t_long_mfma = best_prefill(prompt[:-1]), best_prefill(long_prompt)
     eng.close()
     ms_tok = t_dec * 1e3 / n_new
     # Attention per token: 24 qd_decode_attention calls at the mean KV length of
@@ -239,14 +248,17 @@ def measure_e2e(lib, seed: int = 5, n_prompt: int = 128, n_new: int = 256):
     tok_bytes = w_bytes + NL * 2 * mean_L * H_ * 2
     log(f"[bench] config 5: {n_new / t_dec:.1f} tokens/s ({ms_tok:.3f} ms/token, "
         f"{tok_bytes / (ms_tok * 1e-3) / 1e9:.0f} GB/s over {tok_bytes / 1e9:.3f} GB/token), "
-        f"prompt {n_prompt - 1} tokens in {t_prompt * 1e3:.1f} ms ({len(long_prompt)} in {t_long * 1e3:.0f} ms), "
+        f"prompt {n_prompt - 1} tokens in {t_prompt * 1e3:.1f} ms ({len(long_prompt)} in {t_long * 1e3:.0f} ms; "
+        f"MFMA prefill {t_prompt_mfma * 1e3:.1f} / {t_long_mfma * 1e3:.0f} ms), "
         f"attention share ~{100 * share:.1f}% "
         f"(24 x {att['us_cold']:.2f} us at L={mean_L}), image fill {t_fill:.1f} s")
     return {"model": "Qwen-1.8B shape, random init (library generator, std 0.02, norm weights 1)",
             "prompt_tokens": n_prompt, "generated_tokens": n_new,
             "tokens_per_s": round(n_new / t_dec, 2), "ms_per_token": round(ms_tok, 4),
             "prompt_ms": round(t_prompt * 1e3, 2),
-            "prompt_2048_ms": round(t_long * 1e3, 1), "bytes_per_token": tok_bytes,
+            "prompt_2048_ms": round(t_long * 1e3, 1),
+            "prompt_ms_mfma_prefill": round(t_prompt_mfma * 1e3, 2),
+            "prompt_2048_ms_mfma_prefill": round(t_long_mfma * 1e3, 1), "bytes_per_token": tok_bytes,
             "gbps": round(tok_bytes / (ms_tok * 1e-3) / 1e9, 1),
             "attention_share_est": round(share, 4),
             "attention_us_per_call_at_mean_L": round(att["us_cold"], 3), "mean_L": mean_L,

@@ -67,6 +67,29 @@ int qd_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps, const
                      const uint16_t* w2, uint16_t* act, int hidden, int inter,
                      hipStream_t stream);
 
+/* Batched projection of m rows (prompt tokens at once):
+ *   y[i][j] = half(sum_k x[i][k] * w[j][k])                        residual == NULL
+ *   y[i][j] = half(float(residual[i][j]) + float(half(sum)))       otherwise
+ * for i < m, j < n.  x rows are ldx elements apart, y and residual rows ldy
+ * apart; w is [n][k], the .bin file's layout (the reference transposes its
+ * weights at load and multiplies [k][n]).  Replaces QwenEngine::gemm for m > 1
+ * (qwen_infer.cu:359-367: hgemm_swizzle_nn) in prefill (:462, :542, :573-574,
+ * :593).
+ *   mode QD_GEMM_EXACT: every output is the decode step's sum for that row --
+ *     lane l of a wave adds k = 512j + 8l + e in order, then the fixed wave64
+ *     tree -- so a prompt's rows are bit-identical to qd_proj_residual and the
+ *     decode GEMVs token by token.  k a multiple of 8, at most 8192.
+ *   mode QD_GEMM_MFMA: the matrix cores (v_mfma_f32_16x16x32_f16); products
+ *     are exact and summed in fp32 in the hardware's order, so results are not
+ *     reproducible on the host.  k a multiple of 64.
+ * x and w 16-byte aligned, ldx a multiple of 8 and >= k, ldy >= n; y and
+ * residual 2-byte aligned.  residual may be y (in place); y must not overlap x
+ * or w (QD_EINVAL). */
+#define QD_GEMM_EXACT 0
+#define QD_GEMM_MFMA 1
+int qd_gemm_nt(const uint16_t* x, long long ldx, const uint16_t* w, const uint16_t* residual,
+               uint16_t* y, long long ldy, int m, int n, int k, int mode, hipStream_t stream);
+
 /* Device workspace (bytes) qd_lm_head_argmax needs for a vocabulary size. */
 size_t qd_lm_head_workspace_bytes(int vocab);
 

@@ -32,6 +32,7 @@
 #include <stdint.h>
 
 #include "qdiy/attn.h"
+#include "qdiy/decode.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -85,8 +86,18 @@ int qd_engine_reset(qd_engine* eng);
 /* Runs the n tokens at positions *pos, *pos + 1, ... through all layers,
  * filling their KV-cache rows, and advances *pos by n (the role of
  * QwenEngine::prefill, qwen_infer.cu:372-611, which the reference runs for
- * prompt tokens 0..N-2). */
+ * prompt tokens 0..N-2).  In the default mode (QD_GEMM_EXACT) the KV rows it
+ * writes are bit-identical to feeding the tokens one by one through
+ * qd_engine_step. */
 int qd_engine_prefill(qd_engine* eng, const int* tokens, int n, int* pos);
+
+/* Selects how qd_engine_prefill multiplies its projections (qd_gemm_nt's
+ * modes): QD_GEMM_EXACT (the default: bit-identical to token-by-token decode)
+ * or QD_GEMM_MFMA (the matrix cores, as the reference's prefill uses its tensor
+ * cores; the KV rows then differ from token-by-token decode by fp32 summation
+ * order, and greedy tokens after the prompt can differ at near-ties).
+ * Projections whose k is not a multiple of 64 stay exact. */
+int qd_engine_set_prefill_mode(qd_engine* eng, int mode);
 
 /* One greedy decode step for `token` at position `pos`
  * (QwenEngine::step, qwen_infer.cu:614-735): *next_token receives the argmax

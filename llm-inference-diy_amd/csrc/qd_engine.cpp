@@ -141,6 +141,7 @@ struct qd_engine {
   int* h_token = nullptr;               // pinned, mapped: the argmax writes it directly
   int* h_token_dev = nullptr;           // h_token's device address
   long long kv_bytes = 0;
+  int prefill_mode = QD_GEMM_EXACT;     // how qd_engine_prefill multiplies its projections
   // batched prefill scratch, kPrefillChunk tokens
   int* p_tokens = nullptr;
   uint16_t *p_x = nullptr, *p_xn = nullptr, *p_qkv = nullptr, *p_att = nullptr;
@@ -213,6 +214,7 @@ int prefill_batched(qd_engine* e, const int* tokens, int T, int pos0) {
   auto gemv = [&](const uint16_t* x, long long ldx, const uint16_t* w, int n, int k, uint16_t* y,
                   long long ldy, int epi) {
     qd::BatchedGemvParams p{x, ldx, w, n, k, T, y, ldy, y};
+    if (e->prefill_mode == QD_GEMM_MFMA && k % 64 == 0) return qd::launch_gemm_mfma(p, epi, e->stream);
     return qd::launch_gemv_batched(p, epi, e->stream);
   };
   for (uint32_t l = 0; l < c.num_layers && he == hipSuccess; ++l) {
@@ -286,6 +288,30 @@ int qd_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps, const
   qd::FfnUpParams p{x, norm_w, eps, w1, w2, act, hidden, inter};
   hipError_t e = qd::launch_ffn_up(p, stream);
   return e == hipSuccess ? QD_OK : hip_fail(e, "ffn_up launch");
+}
+
+int qd_gemm_nt(const uint16_t* x, long long ldx, const uint16_t* w, const uint16_t* residual,
+               uint16_t* y, long long ldy, int m, int n, int k, int mode, hipStream_t stream) {
+  if (!x || !w || !y) return fail(QD_EINVAL, "x, w and y must be non-NULL");
+  if (mode != QD_GEMM_EXACT && mode != QD_GEMM_MFMA) return fail(QD_EINVAL, "unknown mode %d", mode);
+  if (m < 1 || n < 1) return fail(QD_EINVAL, "m %d and n %d must be >= 1", m, n);
+  if (mode == QD_GEMM_EXACT && (k < 8 || k % 8 != 0 || k > 8192))
+    return fail(QD_EINVAL, "k %d must be a multiple of 8 in [8, 8192] (exact mode)", k);
+  if (mode == QD_GEMM_MFMA && (k < 64 || k % 64 != 0))
+    return fail(QD_EINVAL, "k %d must be a positive multiple of 64 (MFMA mode)", k);
+  if (ldx < k || ldx % 8 != 0 || ldy < n)
+    return fail(QD_EINVAL, "ldx %lld must be a multiple of 8 and at least k, ldy %lld at least n", ldx, ldy);
+  if (!aligned16(x) || !aligned16(w)) return fail(QD_EINVAL, "x and w must be 16-byte aligned");
+  if (!aligned2(y) || (residual && !aligned2(residual))) return fail(QD_EINVAL, "y and residual must be 2-byte aligned");
+  const size_t yb = ((size_t)(m - 1) * ldy + n) * 2;
+  if (overlaps(y, yb, x, ((size_t)(m - 1) * ldx + k) * 2) || overlaps(y, yb, w, (size_t)n * k * 2) ||
+      (residual && residual != y && overlaps(y, yb, residual, yb)))
+    return fail(QD_EINVAL, "y overlaps x, w or (other than exactly) residual");
+  qd::BatchedGemvParams p{x, ldx, w, n, k, m, y, ldy, residual ? residual : y};
+  const int epi = residual ? 1 : 0;
+  const hipError_t e = mode == QD_GEMM_MFMA ? qd::launch_gemm_mfma(p, epi, stream)
+                                            : qd::launch_gemv_batched(p, epi, stream);
+  return e == hipSuccess ? QD_OK : hip_fail(e, "gemm launch");
 }
 
 size_t qd_lm_head_workspace_bytes(int vocab) {
@@ -502,6 +528,13 @@ int qd_engine_reset(qd_engine* e) {
       (he = hipMemsetAsync(e->logits, 0, (size_t)e->cfg.vocab_size * 2, e->stream)) != hipSuccess ||
       (he = hipStreamSynchronize(e->stream)) != hipSuccess)
     return hip_fail(he, "engine reset");
+  return QD_OK;
+}
+
+int qd_engine_set_prefill_mode(qd_engine* e, int mode) {
+  if (!e) return fail(QD_EINVAL, "engine is NULL");
+  if (mode != QD_GEMM_EXACT && mode != QD_GEMM_MFMA) return fail(QD_EINVAL, "unknown prefill mode %d", mode);
+  e->prefill_mode = mode;
   return QD_OK;
 }
 

@@ -207,6 +207,9 @@ hipError_t launch_lm_head_argmax(const LmHeadParams& p, int* token, hipStream_t 
 hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float eps, uint16_t* xn,
                                   int hidden, int T, hipStream_t stream);
 hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t stream);
+// The same product on the matrix cores (fp32 accumulation in the hardware's
+// order, not bit-reproducible on the host); p.k must be a multiple of 64.
+hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream);
 hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_layer,
                                uint16_t* v_layer, const float2* rope_cs, long long row_stride,
                                long long head_stride, int pos0, int num_heads, int T,

@@ -306,6 +306,127 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
     *reinterpret_cast<f16x8*>(dst + 8 * c) = *reinterpret_cast<const f16x8*>(src + 8 * c);
 }
 
+// ---------------------------------------------------------------------------
+// MFMA prefill GEMM (the fast, not bit-reproducible mode): Y[t][n] = sum_k
+// X[t][k] W[n][k] on the matrix cores, fp16 x fp16 products accumulated in fp32
+// by v_mfma_f32_16x16x32_f16 in the hardware's own order (the role of the
+// reference's tensor-core hgemm_swizzle_nn in prefill, qwen_infer.cu:359-367).
+//
+// Operand layout of one 16x16x32 step (checked on gfx950): lane l holds
+// A[l % 16][8 (l / 16) .. +8] and B[8 (l / 16) .. +8][l % 16], and receives
+// D[4 (l / 16) + r][l % 16], r = 0..3.  With A = X (tokens x K) and B = W^T,
+// both fragments are 16 contiguous bytes of one row of X or W.
+//
+// Workgroup: 4 waves, a 64-token x 64-row tile; wave w takes tokens
+// 32 (w / 2) .. +32 and rows 32 (w % 2) .. +32 as 2 x 2 MFMA blocks.  K goes
+// in tiles of 256 staged through LDS (rows padded to 264 halves: the 16 lanes
+// of each 16-byte read fall on distinct banks).  The next tile's global loads
+// are in flight in registers while the current tile's 32 MFMAs per wave run;
+// at 8 tiles for K = 2048 the latency of each tile's loads is paid 8 times,
+// not 32.  Two workgroups fit a CU (2 x 67.6 KB of its 160 KB LDS).  Tokens
+// past t and rows past n load clamped rows and are not stored; the K past the
+// end of a partial last tile is staged as zeros, which add nothing.  K must be
+// a multiple of 64.
+constexpr int kMmTile = 64;                 // tokens and rows per workgroup
+constexpr int kMmK = 256;                   // K per LDS tile
+constexpr int kMmLd = kMmK + 8;             // LDS row stride in halves
+constexpr int kMmStage = kMmTile * kMmK / 8 / 256;   // 16-byte chunks per thread per operand
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int kEpi>
+__global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) {
+  __shared__ __align__(16) uint16_t xs[kMmTile * kMmLd];
+  __shared__ __align__(16) uint16_t ws[kMmTile * kMmLd];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n0 = blockIdx.x * kMmTile;
+  const int t0 = blockIdx.y * kMmTile;
+  // staging map: chunk c = tid + 256 i is row c / 32 of the tile, halves
+  // 8 (c % 32) .. +8 of its K tile
+  int sr[kMmStage], sc[kMmStage];
+  const uint16_t* xg[kMmStage];
+  const uint16_t* wg[kMmStage];
+#pragma unroll
+  for (int i = 0; i < kMmStage; ++i) {
+    const int c = tid + 256 * i;
+    sr[i] = c >> 5;
+    sc[i] = (c & 31) * 8;
+    xg[i] = p.x + (long long)min(t0 + sr[i], p.t - 1) * p.ldx + sc[i];
+    wg[i] = p.w + (long long)min(n0 + sr[i], p.n - 1) * p.k + sc[i];
+  }
+  f16x8 xr[kMmStage], wr[kMmStage];
+  const f16x8 zero = {};
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < kMmStage; ++i) {
+      if (k0 + sc[i] < p.k) {
+        xr[i] = *reinterpret_cast<const f16x8*>(xg[i] + k0);
+        wr[i] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(wg[i] + k0));
+      } else {
+        xr[i] = zero;
+        wr[i] = zero;
+      }
+    }
+  };
+  const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  f32x4_t acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const int ktiles = (p.k + kMmK - 1) / kMmK;
+  fetch(0);
+  for (int kt = 0; kt < ktiles; ++kt) {
+    __syncthreads();                           // every wave is done with the previous tile
+#pragma unroll
+    for (int i = 0; i < kMmStage; ++i) {
+      *reinterpret_cast<f16x8*>(&xs[sr[i] * kMmLd + sc[i]]) = xr[i];
+      *reinterpret_cast<f16x8*>(&ws[sr[i] * kMmLd + sc[i]]) = wr[i];
+    }
+    __syncthreads();
+    if (kt + 1 < ktiles) fetch((kt + 1) * kMmK);
+    const int kn = min(kMmK, p.k - kt * kMmK);   // a multiple of 64
+    for (int ks = 0; ks < kn; ks += 32) {
+      f16x8 a[2], b[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        a[i] = *reinterpret_cast<const f16x8*>(&xs[(wm + 16 * i + fr) * kMmLd + ks + fk]);
+        b[i] = *reinterpret_cast<const f16x8*>(&ws[(wn + 16 * i + fr) * kMmLd + ks + fk]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  // D[4 (l / 16) + r][l % 16] of block (i, j): token t0 + wm + 16 i + 4 (l / 16) + r,
+  // row n0 + wn + 16 j + l % 16
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wn + 16 * j + fr;
+      if (n >= p.n) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + wm + 16 * i + (lane >> 4) * 4 + r;
+        if (t >= p.t) continue;
+        const _Float16 y = to_f16(acc[i][j][r]);
+        _Float16* dst = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
+        if constexpr (kEpi == 0) {
+          *dst = y;
+        } else {
+          const float rr = (float)reinterpret_cast<const _Float16*>(p.res)[(long long)t * p.ldy + n];
+          *dst = (_Float16)(rr + (float)y);
+        }
+      }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float eps, uint16_t* xn,
@@ -354,6 +475,16 @@ hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t*
                                  hipStream_t stream) {
   hipLaunchKernelGGL(swiglu_batched_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                      g, u, act, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream) {
+  if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
+  const dim3 grid((p.n + kMmTile - 1) / kMmTile, (p.t + kMmTile - 1) / kMmTile);
+  if (epi == 0)
+    hipLaunchKernelGGL(gemm_nt_mfma_kernel<0>, grid, dim3(256), 0, stream, p);
+  else
+    hipLaunchKernelGGL(gemm_nt_mfma_kernel<1>, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

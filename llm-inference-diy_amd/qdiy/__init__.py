@@ -33,11 +33,15 @@ EXPORTS = (
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
+    "qd_gemm_nt",
     # qdiy/engine.h
     "qd_model_image_bytes", "qd_model_fill_random", "qd_model_write_random", "qd_engine_create",
     "qd_engine_create_from_image", "qd_engine_destroy", "qd_engine_config", "qd_engine_reset",
     "qd_engine_prefill", "qd_engine_step", "qd_engine_logits", "qd_engine_generate",
+    "qd_engine_set_prefill_mode",
 )
+
+GEMM_EXACT, GEMM_MFMA = 0, 1      # qd_gemm_nt / qd_engine_set_prefill_mode modes
 
 
 class QdError(RuntimeError):
@@ -101,6 +105,8 @@ def load() -> ctypes.CDLL:
     u16p = ctypes.POINTER(ctypes.c_uint16)
     ip = ctypes.POINTER(ctypes.c_int)
     L.qd_proj_residual.argtypes = [vp, vp, vp, vp, i, i, vp]
+    L.qd_gemm_nt.argtypes = [vp, ll, vp, vp, vp, ll, i, i, i, i, vp]
+    L.qd_engine_set_prefill_mode.argtypes = [vp, i]
     L.qd_ffn_up_swiglu.argtypes = [vp, vp, ctypes.c_float, vp, vp, vp, i, i, vp]
     L.qd_lm_head_workspace_bytes.argtypes = [i]
     L.qd_lm_head_workspace_bytes.restype = ctypes.c_size_t
@@ -285,6 +291,21 @@ def proj_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor, out:
     return out
 
 
+def gemm_nt(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, m: int, n: int, k: int,
+            residual: torch.Tensor | None = None, mode: int = GEMM_EXACT, ldx: int | None = None,
+            ldy: int | None = None, stream=None) -> torch.Tensor:
+    """y[i][j] = half(sum_k x[i][k] w[j][k]) (+ residual: half(r + half(sum))) for i < m,
+    j < n; w is [n][k]; x rows ldx (default k) and y rows ldy (default n) apart."""
+    ldx = k if ldx is None else ldx
+    ldy = n if ldy is None else ldy
+    if x.numel() < (m - 1) * ldx + k or w.numel() < n * k or y.numel() < (m - 1) * ldy + n:
+        raise ValueError("x, w or y too small for m, n, k and the strides")
+    _check(load().qd_gemm_nt(_ptr(x, "x"), ldx, _ptr(w, "w"),
+                             None if residual is None else _ptr(residual, "residual"), _ptr(y, "y"),
+                             ldy, m, n, k, mode, _stream(stream)))
+    return y
+
+
 def ffn_up_swiglu(x: torch.Tensor, norm_w: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
                   act: torch.Tensor, hidden: int, inter: int, eps: float = 1e-6,
                   stream=None) -> torch.Tensor:
@@ -382,6 +403,10 @@ class Engine:
 
     def reset(self) -> None:
         _check(load().qd_engine_reset(self._h))
+
+    def set_prefill_mode(self, mode: int) -> None:
+        """GEMM_EXACT (default; bit-identical to token-by-token decode) or GEMM_MFMA."""
+        _check(load().qd_engine_set_prefill_mode(self._h, mode))
 
     def prefill(self, tokens, pos: int = 0) -> int:
         t = (ctypes.c_int * len(tokens))(*tokens)

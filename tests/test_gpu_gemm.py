@@ -1,0 +1,126 @@
+"""GPU parity of the batched projection qd_gemm_nt (the prefill GEMM) in both
+modes, and of the engine's MFMA prefill mode.
+
+Bars:
+  * QD_GEMM_EXACT: every row bit-exact against the oracle's decode-order GEMV
+    (and against its projection + residual), i.e. the same bits as the decode
+    step computes token by token;
+  * QD_GEMM_MFMA: fp16 x fp16 products are exact in fp32 and the matrix cores
+    sum them in fp32 in their own order, so each output is within one fp16 ulp
+    of the float64 sum plus the fp32 summation bound k * 2^-23 * sum|x w|
+    (with a residual: plus one more fp16 rounding);
+  * engine, MFMA prefill: the KV rows differ from exact prefill only by that
+    summation order, so the next step's logits agree closely; decode steps
+    themselves are unchanged.
+"""
+import numpy as np
+import pytest
+import torch
+
+from common import normal_f16, ulp16
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def qdiy():
+    import qdiy as m
+    torch.cuda.set_device(0)
+    m.load()
+    return m
+
+
+def _same(a, b):
+    return np.array_equal(np.asarray(a).view(np.uint16), np.asarray(b).view(np.uint16))
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (37, 100, 520), (127, 6144, 2048), (256, 2048, 5504)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_exact_mode_is_the_decode_gemv(qdiy, m, n, k, with_res):
+    rng = np.random.default_rng(m * 1000 + n + k + with_res)
+    x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
+    y = torch.zeros(m * n, dtype=torch.float16, device="cuda")
+    qdiy.gemm_nt(_dev(x.reshape(-1)), _dev(W.reshape(-1)), y, m, n, k,
+                 residual=_dev(R.reshape(-1)) if with_res else None, mode=qdiy.GEMM_EXACT)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(m, n)
+    rows = [0, m // 2, m - 1] if m > 3 else range(m)
+    for i in rows:
+        if with_res:
+            want = oracle.proj_residual(x[i], W.reshape(-1), R[i], n, k)
+        else:
+            want = oracle.gemv(x[i], W.reshape(-1), n, k, 0, oracle.ORDER_WAVE64)
+        assert _same(got[i], want), f"row {i}"
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 64), (37, 100, 512), (127, 6144, 2048), (256, 2048, 5504),
+                                   (200, 5504, 2048)])
+@pytest.mark.parametrize("with_res", [False, True])
+def test_mfma_mode_within_fp32_summation_bound(qdiy, m, n, k, with_res):
+    rng = np.random.default_rng(7 * m + n + k + with_res)
+    x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
+    y = torch.full((m * n + 64,), 9.0, dtype=torch.float16, device="cuda")
+    qdiy.gemm_nt(_dev(x.reshape(-1)), _dev(W.reshape(-1)), y, m, n, k,
+                 residual=_dev(R.reshape(-1)) if with_res else None, mode=qdiy.GEMM_MFMA)
+    torch.cuda.synchronize()
+    out = y.cpu().numpy()
+    assert np.all(out[m * n:] == np.float16(9.0)), "write past the end of y"
+    got = out[:m * n].reshape(m, n).astype(np.float64)
+    x64, W64 = x.astype(np.float64), W.astype(np.float64)
+    s = x64 @ W64.T
+    bound = k * 2.0 ** -23 * (np.abs(x64) @ np.abs(W64).T)
+    if with_res:
+        h = s.astype(np.float16).astype(np.float64)
+        want = R.astype(np.float64) + h
+        tol = ulp16(want) + ulp16(h) + bound + ulp16(s)
+    else:
+        want, tol = s, ulp16(s) + bound
+    assert np.all(np.abs(got - want) <= tol), float(np.max(np.abs(got - want) - tol))
+
+
+def test_gemm_nt_rejects_bad_arguments(qdiy):
+    x = torch.zeros(4 * 96, dtype=torch.float16, device="cuda")
+    w = torch.zeros(16 * 96, dtype=torch.float16, device="cuda")
+    y = torch.zeros(4 * 16, dtype=torch.float16, device="cuda")
+    with pytest.raises(qdiy.QdError, match="multiple of 64"):
+        qdiy.gemm_nt(x, w, y, 4, 16, 96, mode=qdiy.GEMM_MFMA)
+    with pytest.raises(qdiy.QdError, match="unknown mode"):
+        qdiy.gemm_nt(x, w, y, 4, 16, 96, mode=7)
+    big = torch.zeros(4096, dtype=torch.float16, device="cuda")
+    with pytest.raises(qdiy.QdError, match="overlaps"):
+        qdiy.gemm_nt(big[:4 * 64], w, big[128:128 + 4 * 16], 4, 16, 64)
+    qdiy.gemm_nt(x, w, y, 4, 16, 64, mode=qdiy.GEMM_MFMA, ldx=96)     # strided x is fine
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("hidden,inter", [(512, 1368), (2048, 5504)])
+def test_engine_mfma_prefill(qdiy, hidden, inter):
+    """MFMA prefill against exact prefill on the same prompt (with c_proj exact
+    where inter is not a multiple of 64): the next step's logits agree to the
+    fp32-order difference, and plain decode steps are bit-identical in both
+    modes."""
+    cfg = qdiy.model_cfg(vocab_size=512, hidden_size=hidden, num_layers=2, num_heads=hidden // 128,
+                         intermediate_size=inter, max_seqlen=320)
+    img = qdiy.random_model_image(cfg, 41 + hidden, 0.03, nthreads=8)
+    prompt = [int(t) for t in np.random.default_rng(hidden).integers(0, 512, 300)]
+    res = {}
+    with qdiy.Engine(image=img) as eng:
+        for mode in (qdiy.GEMM_EXACT, qdiy.GEMM_MFMA):
+            eng.set_prefill_mode(mode)
+            eng.reset()
+            pos = eng.prefill(prompt[:-1])
+            eng.step(prompt[-1], pos)
+            prefilled = eng.logits().astype(np.float64)
+            eng.reset()
+            eng.step(prompt[0], 0)                     # no prefill: decode kernels only
+            res[mode] = (prefilled, eng.logits())
+    exact, mfma = res[qdiy.GEMM_EXACT], res[qdiy.GEMM_MFMA]
+    assert _same(exact[1], mfma[1]), "decode steps must not depend on the prefill mode"
+    d = np.abs(exact[0] - mfma[0])
+    assert float(np.max(d)) <= 0.02 * float(np.max(np.abs(exact[0]))) + 0.01, float(np.max(d))
+    assert float(np.corrcoef(exact[0], mfma[0])[0, 1]) > 0.999
