@@ -116,7 +116,11 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     us_hot = timed(steps, 1)
     if not torch.isfinite(out).all():
         raise RuntimeError("non-finite attention output")
-    plan = ctx.plan(L)
+    if variant == 1:
+        plan = ("fused", 1)
+    else:
+        d = ctx.plan_detail(L, "split" if variant == 2 else "auto", splits)
+        plan = ("fused" if d.variant == qdiy.FUSED else "split", d.num_splits)
     ctx.close()
     del kc, vc
     torch.cuda.empty_cache()

@@ -90,6 +90,31 @@ int qd_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps, const
 int qd_gemm_nt(const uint16_t* x, long long ldx, const uint16_t* w, const uint16_t* residual,
                uint16_t* y, long long ldy, int m, int n, int k, int mode, hipStream_t stream);
 
+/* Causal attention of `tokens` prompt queries at positions pos0 .. pos0 +
+ * tokens - 1 of one layer, all heads: query t attends over cache rows
+ * [0, pos0 + t] (rows written beforehand, K rotated).  Query t's row is
+ * q + t*q_stride (head h at + h*128: the rotated Q third of the prefill's QKV
+ * rows); its output row is out + t*out_stride.  Replaces the reference's
+ * prompt attention, qwen_infer.cu:484-527 (gather_q_from_qkv and
+ * gather_kv_from_cache into per-head buffers, flash_attn_tuned_A_kernel with
+ * the causal mask of flash_attn_causal.cuh once per head, then
+ * scatter_interleaved_kernel), reading Q and the cache in place.
+ *   mode QD_GEMM_EXACT: every query with the arithmetic qd_decode_attention
+ *     uses at its length, batched (one fused launch for the queries of up to
+ *     224 rows, scan + merge pairs for the others): outputs are bit-identical
+ *     to decoding the prompt token by token.  The first call with queries
+ *     beyond 224 rows allocates the context's prefill scratch.
+ *   mode QD_GEMM_MFMA: one causal FlashAttention launch on the matrix cores
+ *     (v_mfma_f32_16x16x32_f16, softmax weights rounded to fp16 for the
+ *     product, hardware exp2): within 2e-3 of the exact outputs for
+ *     N(0,1)-scale inputs, not reproducible on the host.
+ * Requires tokens >= 1, 0 <= pos0, pos0 + tokens <= max_seqlen; q, out,
+ * k_layer and v_layer 16-byte aligned; q_stride and out_stride multiples of 8
+ * and >= num_heads*128; out must not overlap q or the cache rows read. */
+int qd_prefill_attention(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k_layer,
+                         const uint16_t* v_layer, uint16_t* out, long long out_stride, int pos0,
+                         int tokens, int num_heads, int head_dim, int mode, hipStream_t stream);
+
 /* Device workspace (bytes) qd_lm_head_argmax needs for a vocabulary size. */
 size_t qd_lm_head_workspace_bytes(int vocab);
 

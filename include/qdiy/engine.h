@@ -91,12 +91,14 @@ int qd_engine_reset(qd_engine* eng);
  * qd_engine_step. */
 int qd_engine_prefill(qd_engine* eng, const int* tokens, int n, int* pos);
 
-/* Selects how qd_engine_prefill multiplies its projections (qd_gemm_nt's
- * modes): QD_GEMM_EXACT (the default: bit-identical to token-by-token decode)
- * or QD_GEMM_MFMA (the matrix cores, as the reference's prefill uses its tensor
- * cores; the KV rows then differ from token-by-token decode by fp32 summation
- * order, and greedy tokens after the prompt can differ at near-ties).
- * Projections whose k is not a multiple of 64 stay exact. */
+/* Selects how qd_engine_prefill multiplies its projections and computes its
+ * attention (the modes of qd_gemm_nt and qd_prefill_attention):
+ * QD_GEMM_EXACT (the default: bit-identical to token-by-token decode) or
+ * QD_GEMM_MFMA (the matrix cores for both, as the reference's prefill uses its
+ * tensor cores; the KV rows then differ from token-by-token decode by fp32
+ * summation order and fp16 softmax weights, and greedy tokens after the prompt
+ * can differ at near-ties).  Projections whose k is not a multiple of 64 stay
+ * exact. */
 int qd_engine_set_prefill_mode(qd_engine* eng, int mode);
 
 /* One greedy decode step for `token` at position `pos`

@@ -17,7 +17,8 @@ LIB = os.path.join(LIB_DIR, "libqdiy.so")
 BENCH_LIB = os.path.join(LIB_DIR, "libqdiy_bench.so")
 ENGINE_EXE = os.path.join(LIB_DIR, "qdiy_engine")
 
-SOURCES = ["qd_capi.cpp", "qd_engine.cpp", "qd_attention.hip", "qd_rope_cache.hip", "qd_decode_ops.hip", "qd_prefill.hip"]
+SOURCES = ["qd_capi.cpp", "qd_engine.cpp", "qd_attention.hip", "qd_rope_cache.hip", "qd_decode_ops.hip", "qd_prefill.hip",
+           "qd_flash_prefill.hip"]
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for all device code: plain float code is

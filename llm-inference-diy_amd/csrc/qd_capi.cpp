@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "qd_internal.h"
+#include "qdiy/decode.h"
 
 namespace {
 thread_local char g_err[512] = "";
@@ -203,6 +204,26 @@ int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const 
     t = t1;
   }
   return QD_OK;
+}
+
+int attention_prefill_mfma(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k,
+                           const uint16_t* v, uint16_t* out, long long out_stride, int pos0,
+                           int tokens, hipStream_t stream) {
+  FlashPrefillParams p;
+  p.q = q;
+  p.q_stride = q_stride;
+  p.k = k;
+  p.v = v;
+  p.row_stride = ctx->cfg.kv_row_stride;
+  p.head_stride = ctx->cfg.kv_head_stride;
+  p.out = out;
+  p.out_stride = out_stride;
+  p.pos0 = pos0;
+  p.tokens = tokens;
+  p.num_heads = ctx->cfg.num_heads;
+  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));
+  const hipError_t e = launch_flash_prefill(p, stream);
+  return e == hipSuccess ? QD_OK : hip_fail(e, "prefill attention launch");
 }
 
 }  // namespace qd
@@ -427,6 +448,42 @@ int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
     return fail(QD_EINVAL, "num_splits %d above the maximum %d", num_splits, qd::kMaxSplits);
   return run_attention(ctx, q, k_layer, v_layer, out, seqlen,
                        plan_split(ctx, seqlen, num_splits), stream);
+}
+
+int qd_prefill_attention(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k_layer,
+                         const uint16_t* v_layer, uint16_t* out, long long out_stride, int pos0,
+                         int tokens, int num_heads, int head_dim, int mode, hipStream_t stream) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  if (!q || !k_layer || !v_layer || !out)
+    return fail(QD_EINVAL, "q, k_layer, v_layer and out must be non-NULL");
+  if (!aligned16(q) || !aligned16(k_layer) || !aligned16(v_layer) || !aligned16(out))
+    return fail(QD_EINVAL, "q, k_layer, v_layer and out must be 16-byte aligned");
+  if (head_dim != QD_HEAD_DIM || head_dim != ctx->cfg.head_dim)
+    return fail(QD_EINVAL, "head_dim %d unsupported (must be %d)", head_dim, QD_HEAD_DIM);
+  if (num_heads != ctx->cfg.num_heads)
+    return fail(QD_EINVAL, "num_heads %d differs from the context's %d", num_heads, ctx->cfg.num_heads);
+  if (mode != QD_GEMM_EXACT && mode != QD_GEMM_MFMA) return fail(QD_EINVAL, "unknown mode %d", mode);
+  if (tokens < 1 || pos0 < 0 || (long long)pos0 + tokens > ctx->cfg.max_seqlen)
+    return fail(QD_EINVAL, "positions [%d, %lld) outside [0, %d) or no tokens", pos0,
+                (long long)pos0 + tokens, ctx->cfg.max_seqlen);
+  const long long row = (long long)num_heads * QD_HEAD_DIM;
+  if (q_stride < row || out_stride < row || (q_stride % 8) || (out_stride % 8))
+    return fail(QD_EINVAL, "q_stride and out_stride must be multiples of 8 and >= %lld", row);
+  const size_t ob = ((size_t)(tokens - 1) * out_stride + row) * 2;
+  const size_t qb = ((size_t)(tokens - 1) * q_stride + row) * 2;
+  const size_t kvb = ((size_t)(pos0 + tokens - 1) * ctx->cfg.kv_row_stride +
+                      (size_t)(num_heads - 1) * ctx->cfg.kv_head_stride + QD_HEAD_DIM) * 2;
+  if (qd::overlaps(out, ob, q, qb) || qd::overlaps(out, ob, k_layer, kvb) ||
+      qd::overlaps(out, ob, v_layer, kvb))
+    return fail(QD_EINVAL, "out overlaps q or the k_layer / v_layer rows being read");
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
+    return fail(QD_EINVAL, "current device %d is not the context's device %d", dev, ctx->device);
+  if (mode == QD_GEMM_MFMA)
+    return qd::attention_prefill_mfma(ctx, q, q_stride, k_layer, v_layer, out, out_stride, pos0,
+                                      tokens, stream);
+  return qd::attention_prefill(ctx, q, q_stride, k_layer, v_layer, out, out_stride, pos0, tokens,
+                               stream);
 }
 
 int qd_max_splits(void) { return qd::kMaxSplits; }

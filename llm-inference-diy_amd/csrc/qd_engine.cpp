@@ -141,7 +141,7 @@ struct qd_engine {
   int* h_token = nullptr;               // pinned, mapped: the argmax writes it directly
   int* h_token_dev = nullptr;           // h_token's device address
   long long kv_bytes = 0;
-  int prefill_mode = QD_GEMM_EXACT;     // how qd_engine_prefill multiplies its projections
+  int prefill_mode = QD_GEMM_EXACT;     // qd_engine_prefill's projections and attention
   // batched prefill scratch, kPrefillChunk tokens
   int* p_tokens = nullptr;
   uint16_t *p_x = nullptr, *p_xn = nullptr, *p_qkv = nullptr, *p_att = nullptr;
@@ -226,8 +226,11 @@ int prefill_batched(qd_engine* e, const int* tokens, int T, int pos0) {
                                    e->attn->cfg.kv_row_stride, e->attn->cfg.kv_head_stride, pos0, NH,
                                    T, e->stream);
     if (he != hipSuccess) break;
-    const int rc = qd::attention_prefill(e->attn, e->p_qkv, 3 * H, e->kc(l), e->vc(l), e->p_att, H,
-                                         pos0, T, e->stream);
+    const int rc = e->prefill_mode == QD_GEMM_MFMA
+                       ? qd::attention_prefill_mfma(e->attn, e->p_qkv, 3 * H, e->kc(l), e->vc(l),
+                                                    e->p_att, H, pos0, T, e->stream)
+                       : qd::attention_prefill(e->attn, e->p_qkv, 3 * H, e->kc(l), e->vc(l), e->p_att,
+                                               H, pos0, T, e->stream);
     if (rc != QD_OK) return rc;
     he = gemv(e->p_att, H, e->w(f.proj_w), H, H, e->p_x, H, 1);
     if (he == hipSuccess) he = qd::launch_rmsnorm_batched(e->p_x, e->w(f.ln_2), kEps, e->p_xn, H, T, e->stream);

@@ -1,0 +1,238 @@
+// Causal prefill attention on the matrix cores (gfx950 v_mfma_f32_16x16x32_f16):
+// the counterpart of the reference's prompt attention, qwen_infer.cu:484-527
+// (gather_q_from_qkv / gather_kv_from_cache into per-head buffers,
+// flash_attn_tuned_A_kernel with the causal mask of flash_attn_causal.cuh, one
+// launch per head, then scatter_interleaved_kernel), as one launch that reads
+// the rotated Q rows and the KV cache where they lie.
+//
+// Workgroup (h, tile) takes 16 consecutive queries of head h.  Its four waves
+// share the queries and split the keys: wave w takes key blocks w, w + 4, ...
+// of 32 keys each, keeps its own online-softmax state, and the four states
+// are folded in LDS at the end.  Per block a wave computes
+//   S^T = K Q^T   (M = 16 keys per tile, two tiles; N = 16 queries; K = 128 dims)
+//   O^T += V^T P^T (M = 16 dims per tile, eight tiles; N = 16 queries; K = 32 keys)
+// Transposing both products puts the query in the MFMA's column, which is the
+// lane's column l % 16 of every accumulator, so each lane's softmax state
+// (running max m, partial sum l) belongs to query l % 16 in every product and
+// rescaling O needs no lane exchange.  Operand lanes: A[l % 16][8 (l / 16) + e],
+// B[8 (l / 16) + e][l % 16]; accumulator D[4 (l / 16) + r][l % 16].
+//   - K rows feed A directly (the 8 dims of a lane are 16 contiguous bytes).
+//   - S^T's accumulator gives lane (g = l / 16, c = l % 16) the keys
+//     16 t + 4 g + r of query c, which become P^T's B operand as they are: the
+//     P.V product sums over its 32 keys in any order, so element e of the lane
+//     stands for key pi(8 g + e) = 16 (e / 4) + 4 g + e % 4, and the V^T
+//     operand is read in the same order.
+//   - V^T is V transposed through LDS: each wave writes its block as [dim][key]
+//     and reads, per tile, the 4 + 4 keys pi(8 g ..) of dim 16 n + c.
+// P is rounded to fp16 for the product (as the reference's MMA kernel does)
+// and the softmax denominator sums the rounded weights; exponentials are the
+// hardware's exp2.  Nothing here is bit-reproducible on
+// the host; the exact prefill path (the decode kernels batched) is.
+#include "qd_device.h"
+#include "qd_internal.h"
+
+namespace qd {
+namespace {
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFpQueries = 16;   // queries per workgroup: the MFMA's N
+constexpr int kFpKeys = 32;      // keys per block: the P.V product's K
+constexpr int kFpWaves = 4;
+// V^T row: 32 keys + 4 halves of padding (18 words), so the two dims one
+// transposed store writes (8 apart) fall 16 banks apart.
+constexpr int kVtLd = kFpKeys + 4;
+constexpr int kVtHalves = 128 * kVtLd;                    // per wave
+constexpr int kOLd = 128 + 4;                             // fp32 O row in the fold
+constexpr size_t kFpLdsBytes = (size_t)kFpWaves * kVtHalves * 2;
+static_assert((size_t)kFpWaves * kFpQueries * kOLd * 4 + 2 * kFpWaves * kFpQueries * 4 <= kFpLdsBytes,
+              "the fold's partials reuse the V^T buffers");
+
+__device__ __forceinline__ void wave_lds_fence() {
+  // Lanes of one wave hand data to each other through LDS: the wave's LDS
+  // operations execute in order, and these fences keep the compiler from
+  // moving the accesses across this point.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct FpBlock {
+  f16x8 k[2][4];   // K rows kb + 16 t + c, dims 32 s + 8 g .. +8
+  f16x8 v[8];      // V row kb + (l & 31), dims 16 i + 8 (l >> 5) .. +8
+};
+
+__global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefillParams p) {
+  __shared__ __align__(16) _Float16 lds[kFpWaves * kVtHalves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int g = lane >> 4;
+  const int h = blockIdx.x;
+  const int q0 = blockIdx.y * kFpQueries;
+  const int nq = min(kFpQueries, p.tokens - q0);
+  const int nkeys = p.pos0 + q0 + nq;           // keys [0, nkeys) reach the last query
+  const int nblk = (nkeys + kFpKeys - 1) / kFpKeys;
+  const int qpos = p.pos0 + q0 + c;             // this lane's query (beyond nq: unused)
+
+  // B operand of S^T: Q[q0 + c][32 s + 8 g .. +8] (rows past the last query
+  // repeat it; their outputs are not stored)
+  const uint16_t* qrow = p.q + (long long)(q0 + min(c, nq - 1)) * p.q_stride + h * 128 + 8 * g;
+  f16x8 qb[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qb[s] = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
+
+  const uint16_t* kbase = p.k + (long long)h * p.head_stride + 8 * g;
+  const uint16_t* vbase = p.v + (long long)h * p.head_stride + 8 * (lane >> 5);
+  // Loads of block j (clamped into [0, nblk) so every call issues them; keys
+  // past nkeys repeat key nkeys - 1 and are masked below).
+  auto load = [&](int j, FpBlock& b) {
+    j = min(j, nblk - 1);
+    const int kb = j * kFpKeys;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint16_t* kr = kbase + (long long)min(kb + 16 * t + c, nkeys - 1) * p.row_stride;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b.k[t][s] = *reinterpret_cast<const f16x8*>(kr + 32 * s);
+    }
+    const uint16_t* vr = vbase + (long long)min(kb + (lane & 31), nkeys - 1) * p.row_stride;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) b.v[i] = *reinterpret_cast<const f16x8*>(vr + 16 * i);
+  };
+
+  _Float16* vt = lds + wave * kVtHalves;
+  float m = -__builtin_inff();
+  float l = 0.0f;
+  f32x4 o[8];
+#pragma unroll
+  for (int n = 0; n < 8; ++n) o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](int j, const FpBlock& b) {
+    const int kb = j * kFpKeys;
+    // V^T into LDS: dim 16 i + 8 (l >> 5) + e, key l & 31
+    wave_lds_fence();                            // the previous block's V^T reads are done
+    {
+      const int kk = lane & 31, dh = 8 * (lane >> 5);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt[(16 * i + dh + e) * kVtLd + kk] = b.v[i][e];
+    }
+    f32x4 st[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) st[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[t][s], qb[s], st[t], 0, 0, 0);
+    }
+    // online softmax of query c over keys kb + 16 t + 4 g + r
+    float sv[8];
+    float bmax = -__builtin_inff();
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb + 16 * t + 4 * g + r;
+        const float s = key <= qpos ? st[t][r] * p.scale_log2 : -__builtin_inff();
+        sv[4 * t + r] = s;
+        bmax = fmaxf(bmax, s);
+      }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    const float mn = fmaxf(m, bmax);
+    const float mref = mn == -__builtin_inff() ? 0.0f : mn;   // no key yet: every weight is 0
+    const float alpha = __builtin_amdgcn_exp2f(m - mref);
+    f16x8 pb;
+    float ps = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // the sum takes the rounded weights the product uses, so O / l stays a
+      // weighted mean of V rows
+      pb[e] = (_Float16)__builtin_amdgcn_exp2f(sv[e] - mref);
+      ps += (float)pb[e];
+    }
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[n] *= alpha;
+    wave_lds_fence();                            // V^T stores visible to the wave
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const _Float16* row = vt + (16 * n + c) * kVtLd + 4 * g;
+      const f16x4 lo = *reinterpret_cast<const f16x4*>(row);
+      const f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16);
+      const f16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[n], 0, 0, 0);
+    }
+  };
+
+  // Wave-uniform loop over this wave's blocks, the next block's loads issued
+  // before the current block's arithmetic (two register sets, alternating).
+  int j = wave;
+  if (j < nblk) {
+    FpBlock b0, b1;
+    load(j, b0);
+    for (;;) {
+      load(j + kFpWaves, b1);
+      compute(j, b0);
+      j += kFpWaves;
+      if (j >= nblk) break;
+      load(j + kFpWaves, b0);
+      compute(j, b1);
+      j += kFpWaves;
+      if (j >= nblk) break;
+    }
+  }
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+
+  // Fold the four waves' states: O rows [wave][query][dim], then m and l.
+  __syncthreads();                               // every wave is done with its V^T
+  float* fo = reinterpret_cast<float*>(lds);
+  float* fm = fo + kFpWaves * kFpQueries * kOLd;
+  float* fl = fm + kFpWaves * kFpQueries;
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+    *reinterpret_cast<f32x4*>(fo + (wave * kFpQueries + c) * kOLd + 16 * n + 4 * g) = o[n];
+  if (g == 0) {
+    fm[wave * kFpQueries + c] = m;
+    fl[wave * kFpQueries + c] = l;
+  }
+  __syncthreads();
+  const int q = tid >> 4;                        // query of this thread
+  const int d0 = (tid & 15) * 8;                 // its 8 dims
+  if (q < nq) {
+    float mw[kFpWaves];
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < kFpWaves; ++w) {
+      mw[w] = fm[w * kFpQueries + q];
+      M = fmaxf(M, mw[w]);
+    }
+    float L = 0.0f;
+    float acc[8] = {};
+#pragma unroll
+    for (int w = 0; w < kFpWaves; ++w) {
+      const float sc = mw[w] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+      L += sc * fl[w * kFpQueries + q];
+      const float* row = fo + (w * kFpQueries + q) * kOLd + d0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += sc * row[e];
+    }
+    f16x8 outv;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) outv[e] = (_Float16)(acc[e] / L);
+    *reinterpret_cast<f16x8*>(p.out + (long long)(q0 + q) * p.out_stride + h * 128 + d0) = outv;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_flash_prefill(const FlashPrefillParams& p, hipStream_t stream) {
+  const dim3 grid(p.num_heads, (p.tokens + kFpQueries - 1) / kFpQueries);
+  hipLaunchKernelGGL(flash_prefill_kernel, grid, dim3(kFpWaves * 64), 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace qd

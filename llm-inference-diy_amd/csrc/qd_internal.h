@@ -159,6 +159,24 @@ struct BatchedGemvParams {
   const uint16_t* res;    // epilogue 1 only
 };
 
+// Causal prefill attention of `tokens` queries at positions pos0, pos0 + 1, ...
+// on the matrix cores: query t (Q row q + t*q_stride, head h at + h*128)
+// attends over cache rows [0, pos0 + t], its output row at out + t*out_stride.
+struct FlashPrefillParams {
+  const uint16_t* q;
+  long long q_stride;
+  const uint16_t* k;      // layer base; (pos, h, d) at pos*row_stride + h*head_stride + d
+  const uint16_t* v;
+  long long row_stride;
+  long long head_stride;
+  uint16_t* out;
+  long long out_stride;
+  int pos0;
+  int tokens;
+  int num_heads;
+  float scale_log2;       // log2(e) / sqrt(128)
+};
+
 // Launch plan of one decode-attention call.
 struct AttnPlan {
   int variant;            // 0 fused, 1 split
@@ -218,6 +236,8 @@ hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t*
                                  hipStream_t stream);
 hipError_t launch_embed(const uint16_t* wte, const int* tokens, uint16_t* x, int hidden, int T,
                         hipStream_t stream);
+// qd_flash_prefill.hip: one workgroup per (head, 16 queries).
+hipError_t launch_flash_prefill(const FlashPrefillParams& p, hipStream_t stream);
 
 }  // namespace qd
 
@@ -233,6 +253,10 @@ namespace qd {
 int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k,
                       const uint16_t* v, uint16_t* out, long long out_stride, int pos0, int tokens,
                       hipStream_t stream);
+// The same queries in one causal FlashAttention launch on the matrix cores.
+int attention_prefill_mfma(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k,
+                           const uint16_t* v, uint16_t* out, long long out_stride, int pos0,
+                           int tokens, hipStream_t stream);
 }  // namespace qd
 
 struct qd_ctx {

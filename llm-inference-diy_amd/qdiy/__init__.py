@@ -33,7 +33,7 @@ EXPORTS = (
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
-    "qd_gemm_nt",
+    "qd_gemm_nt", "qd_prefill_attention",
     # qdiy/engine.h
     "qd_model_image_bytes", "qd_model_fill_random", "qd_model_write_random", "qd_engine_create",
     "qd_engine_create_from_image", "qd_engine_destroy", "qd_engine_config", "qd_engine_reset",
@@ -41,7 +41,7 @@ EXPORTS = (
     "qd_engine_set_prefill_mode",
 )
 
-GEMM_EXACT, GEMM_MFMA = 0, 1      # qd_gemm_nt / qd_engine_set_prefill_mode modes
+GEMM_EXACT, GEMM_MFMA = 0, 1      # qd_gemm_nt / qd_prefill_attention / qd_engine_set_prefill_mode modes
 
 
 class QdError(RuntimeError):
@@ -106,6 +106,7 @@ def load() -> ctypes.CDLL:
     ip = ctypes.POINTER(ctypes.c_int)
     L.qd_proj_residual.argtypes = [vp, vp, vp, vp, i, i, vp]
     L.qd_gemm_nt.argtypes = [vp, ll, vp, vp, vp, ll, i, i, i, i, vp]
+    L.qd_prefill_attention.argtypes = [vp, vp, ll, vp, vp, vp, ll, i, i, i, i, i, vp]
     L.qd_engine_set_prefill_mode.argtypes = [vp, i]
     L.qd_ffn_up_swiglu.argtypes = [vp, vp, ctypes.c_float, vp, vp, vp, i, i, vp]
     L.qd_lm_head_workspace_bytes.argtypes = [i]
@@ -230,6 +231,29 @@ class Context:
             _check(L.qd_decode_attention_split(*args, num_splits, _stream(stream)))
         else:
             raise ValueError(f"unknown variant {variant!r}")
+        return out
+
+    def prefill_attention(self, q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                          out: torch.Tensor, pos0: int, tokens: int, mode: int = GEMM_EXACT,
+                          q_stride: int | None = None, out_stride: int | None = None,
+                          stream=None) -> torch.Tensor:
+        """Causal attention of prompt queries pos0 .. pos0+tokens-1, all heads: query t
+        (row t of q, q_stride apart) over cache rows [0, pos0 + t] into row t of out."""
+        H = self.num_heads
+        row = H * HEAD_DIM
+        q_stride = row if q_stride is None else q_stride
+        out_stride = row if out_stride is None else out_stride
+        if tokens >= 1 and (q.numel() < (tokens - 1) * q_stride + row
+                            or out.numel() < (tokens - 1) * out_stride + row):
+            raise ValueError("q and out need (tokens-1)*stride + num_heads*128 elements")
+        if tokens >= 1 and 0 <= pos0 and pos0 + tokens <= self.max_seqlen:
+            self._check_cache(k_layer, "k_layer", pos0 + tokens)
+            self._check_cache(v_layer, "v_layer", pos0 + tokens)
+        _check(load().qd_prefill_attention(self._h, _ptr(q, "q"), q_stride,
+                                           _ptr(k_layer, "k_layer", False),
+                                           _ptr(v_layer, "v_layer", False), _ptr(out, "out"),
+                                           out_stride, pos0, tokens, H, HEAD_DIM, mode,
+                                           _stream(stream)))
         return out
 
     def qkv_bias_rope_cache(self, qkv: torch.Tensor, bias, k_layer: torch.Tensor,
