@@ -98,7 +98,10 @@ int qd_engine_prefill(qd_engine* eng, const int* tokens, int n, int* pos);
  * tensor cores; the KV rows then differ from token-by-token decode by fp32
  * summation order and fp16 softmax weights, and greedy tokens after the prompt
  * can differ at near-ties).  Projections whose k is not a multiple of 64 stay
- * exact. */
+ * exact.  The matrix-core mode prefills up to 2048 tokens per pass (256 in the
+ * exact mode): selecting it first grows the engine's prefill scratch to that
+ * many tokens (~127 MB at Qwen-1.8B's shape) and returns QD_ENOMEM, keeping the
+ * previous mode and scratch, if that allocation fails. */
 int qd_engine_set_prefill_mode(qd_engine* eng, int mode);
 
 /* One greedy decode step for `token` at position `pos`

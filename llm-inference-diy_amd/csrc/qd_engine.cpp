@@ -116,7 +116,8 @@ void fill_range(uint16_t* t, long long begin, long long end, uint64_t seed, floa
 }
 
 constexpr float kEps = 1e-6f;      // qwen_infer.cu:620
-constexpr int kPrefillChunk = 256; // prompt tokens per batched prefill pass
+constexpr int kPrefillChunk = 256; // prompt tokens per batched prefill pass (exact mode)
+constexpr int kPrefillChunkMfma = 2048;  // ... in the matrix-core mode: M of its GEMMs
 constexpr int kEosA = 151645;      // <|im_end|>, qwen_infer.cu:801
 constexpr int kEosB = 151643;      // <|endoftext|>
 
@@ -142,7 +143,8 @@ struct qd_engine {
   int* h_token_dev = nullptr;           // h_token's device address
   long long kv_bytes = 0;
   int prefill_mode = QD_GEMM_EXACT;     // qd_engine_prefill's projections and attention
-  // batched prefill scratch, kPrefillChunk tokens
+  // batched prefill scratch for p_cap tokens
+  int p_cap = 0;
   int* p_tokens = nullptr;
   uint16_t *p_x = nullptr, *p_xn = nullptr, *p_qkv = nullptr, *p_att = nullptr;
   uint16_t *p_g = nullptr, *p_u = nullptr, *p_act = nullptr;
@@ -177,6 +179,41 @@ void engine_free(qd_engine* e) {
   if (e->stream) (void)hipStreamDestroy(e->stream);
   if (prev >= 0) (void)hipSetDevice(prev);
   delete e;
+}
+
+// (Re)allocates the batched prefill scratch for `cap` tokens.  The new buffers
+// are allocated before the old ones are freed, so on failure the engine keeps
+// its previous scratch.  The caller has synchronised the engine's stream.
+int resize_prefill_scratch(qd_engine* e, int cap) {
+  const long long H = e->cfg.hidden_size, I = e->cfg.intermediate_size;
+  int* tok = nullptr;
+  uint16_t *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *u = nullptr,
+           *act = nullptr;
+  struct { void** p; long long n; } allocs[] = {
+      {(void**)&tok, (long long)cap * 4},    {(void**)&x, cap * H * 2},   {(void**)&xn, cap * H * 2},
+      {(void**)&qkv, cap * 3 * H * 2},       {(void**)&att, cap * H * 2}, {(void**)&g, cap * I * 2},
+      {(void**)&u, cap * I * 2},             {(void**)&act, cap * I * 2}};
+  for (auto& a : allocs) {
+    const hipError_t he = hipMalloc(a.p, (size_t)a.n);
+    if (he != hipSuccess) {
+      for (auto& b : allocs) (void)hipFree(*b.p);
+      return fail(QD_ENOMEM, "hipMalloc of %lld bytes of prefill scratch failed: %s", a.n,
+                  hipGetErrorString(he));
+    }
+  }
+  for (void* q : {(void*)e->p_tokens, (void*)e->p_x, (void*)e->p_xn, (void*)e->p_qkv, (void*)e->p_att,
+                  (void*)e->p_g, (void*)e->p_u, (void*)e->p_act})
+    (void)hipFree(q);
+  e->p_tokens = tok;
+  e->p_x = x;
+  e->p_xn = xn;
+  e->p_qkv = qkv;
+  e->p_att = att;
+  e->p_g = g;
+  e->p_u = u;
+  e->p_act = act;
+  e->p_cap = cap;
+  return QD_OK;
 }
 
 // Per-layer path of one token at `pos` (qwen_infer.cu:622-722).
@@ -454,20 +491,16 @@ int qd_engine_create_from_image(const void* image, long long bytes, qd_engine** 
   struct { void** p; long long n; } allocs[] = {
       {(void**)&e->weights, wbytes},  {(void**)&e->k_cache, e->kv_bytes}, {(void**)&e->v_cache, e->kv_bytes},
       {(void**)&e->x, H * 2},         {(void**)&e->qkv, 3 * H * 2},     {(void**)&e->attn_out, H * 2},
-      {(void**)&e->act, I * 2},       {(void**)&e->logits, V * 2},      {&e->lm_ws, (long long)e->lm_ws_bytes},
-      {(void**)&e->p_tokens, (long long)kPrefillChunk * 4},
-      {(void**)&e->p_x, (long long)kPrefillChunk * H * 2},
-      {(void**)&e->p_xn, (long long)kPrefillChunk * H * 2},
-      {(void**)&e->p_qkv, (long long)kPrefillChunk * 3 * H * 2},
-      {(void**)&e->p_att, (long long)kPrefillChunk * H * 2},
-      {(void**)&e->p_g, (long long)kPrefillChunk * I * 2},
-      {(void**)&e->p_u, (long long)kPrefillChunk * I * 2},
-      {(void**)&e->p_act, (long long)kPrefillChunk * I * 2}};
+      {(void**)&e->act, I * 2},       {(void**)&e->logits, V * 2},      {&e->lm_ws, (long long)e->lm_ws_bytes}};
   for (auto& a : allocs) {
     if ((he = hipMalloc(a.p, (size_t)a.n)) != hipSuccess) {
       engine_free(e);
       return fail(QD_ENOMEM, "hipMalloc of %lld bytes failed: %s", a.n, hipGetErrorString(he));
     }
+  }
+  if ((rc = resize_prefill_scratch(e, std::min(kPrefillChunk, (int)cfg.max_seqlen))) != QD_OK) {
+    engine_free(e);
+    return rc;
   }
   // The next token goes straight from the argmax kernel into mapped pinned
   // memory: no device-to-host copy (a blit kernel of its own) per token.
@@ -537,6 +570,14 @@ int qd_engine_reset(qd_engine* e) {
 int qd_engine_set_prefill_mode(qd_engine* e, int mode) {
   if (!e) return fail(QD_EINVAL, "engine is NULL");
   if (mode != QD_GEMM_EXACT && mode != QD_GEMM_MFMA) return fail(QD_EINVAL, "unknown prefill mode %d", mode);
+  const int cap = std::min(kPrefillChunkMfma, (int)e->cfg.max_seqlen);
+  if (mode == QD_GEMM_MFMA && e->p_cap < cap) {
+    int rc = check_engine(e);
+    if (rc != QD_OK) return rc;
+    const hipError_t he = hipStreamSynchronize(e->stream);
+    if (he != hipSuccess) return hip_fail(he, "prefill mode");
+    if ((rc = resize_prefill_scratch(e, cap)) != QD_OK) return rc;
+  }
   e->prefill_mode = mode;
   return QD_OK;
 }
@@ -551,8 +592,9 @@ int qd_engine_prefill(qd_engine* e, const int* tokens, int n, int* pos) {
   for (int i = 0; i < n; ++i)
     if (tokens[i] < 0 || (uint32_t)tokens[i] >= e->cfg.vocab_size)
       return fail(QD_EINVAL, "token %d outside [0, %u)", tokens[i], e->cfg.vocab_size);
-  for (int i = 0; i < n; i += kPrefillChunk) {
-    const int T = std::min(kPrefillChunk, n - i);
+  const int chunk = e->prefill_mode == QD_GEMM_MFMA ? e->p_cap : std::min(kPrefillChunk, e->p_cap);
+  for (int i = 0; i < n; i += chunk) {
+    const int T = std::min(chunk, n - i);
     if ((rc = prefill_batched(e, tokens + i, T, *pos + i)) != QD_OK) return rc;
     // the token upload of the next chunk reuses p_tokens: finish this chunk first
     hipError_t he = hipStreamSynchronize(e->stream);

@@ -5,10 +5,16 @@
 // launch per head, then scatter_interleaved_kernel), as one launch that reads
 // the rotated Q rows and the KV cache where they lie.
 //
-// Workgroup (h, tile) takes 16 consecutive queries of head h.  Its four waves
-// share the queries and split the keys: wave w takes key blocks w, w + 4, ...
-// of 32 keys each, keeps its own online-softmax state, and the four states
-// are folded in LDS at the end.  Per block a wave computes
+// Workgroup (h, tile) takes 64 consecutive queries of head h, four tiles of
+// 16 (the MFMA's N).  Its four waves all take the 64 queries and split the
+// keys: wave w takes key blocks w, w + 4, ... of 32 keys each, so every K/V
+// row a wave loads serves 64 queries; each wave keeps its own online-softmax
+// state per query, and the four states are folded in LDS at the end.  The
+// grid is one-dimensional and its linear index is remapped so that, with
+// workgroups dealt to the 8 XCDs in turn, the tiles of a head run on one XCD
+// and share its L2 copy of the head's K/V rows; within a head the latest
+// tiles (the longest key ranges) start first.  Per block and query tile a
+// wave computes
 //   S^T = K Q^T   (M = 16 keys per tile, two tiles; N = 16 queries; K = 128 dims)
 //   O^T += V^T P^T (M = 16 dims per tile, eight tiles; N = 16 queries; K = 32 keys)
 // Transposing both products puts the query in the MFMA's column, which is the
@@ -36,17 +42,18 @@ namespace {
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kFpQueries = 16;   // queries per workgroup: the MFMA's N
-constexpr int kFpKeys = 32;      // keys per block: the P.V product's K
+constexpr int kQt = 4;                     // 16-query tiles per workgroup
+constexpr int kFpQueries = 16 * kQt;       // queries per workgroup
+constexpr int kFpKeys = 32;                // keys per block: the P.V product's K
 constexpr int kFpWaves = 4;
+constexpr int kXcds = 8;                   // MI355X: workgroups are dealt to 8 XCDs in turn
 // V^T row: 32 keys + 4 halves of padding (18 words), so the two dims one
 // transposed store writes (8 apart) fall 16 banks apart.
 constexpr int kVtLd = kFpKeys + 4;
-constexpr int kVtHalves = 128 * kVtLd;                    // per wave
-constexpr int kOLd = 128 + 4;                             // fp32 O row in the fold
-constexpr size_t kFpLdsBytes = (size_t)kFpWaves * kVtHalves * 2;
-static_assert((size_t)kFpWaves * kFpQueries * kOLd * 4 + 2 * kFpWaves * kFpQueries * 4 <= kFpLdsBytes,
-              "the fold's partials reuse the V^T buffers");
+constexpr int kVtHalves = 128 * kVtLd;     // per wave
+constexpr int kOLd = 128 + 4;              // fp32 O row in the fold
+static_assert((size_t)kFpWaves * 16 * kOLd * 4 <= (size_t)kFpWaves * kVtHalves * 2,
+              "one query tile's fold reuses the V^T buffers");
 
 __device__ __forceinline__ void wave_lds_fence() {
   // Lanes of one wave hand data to each other through LDS: the wave's LDS
@@ -57,180 +64,192 @@ __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-struct FpBlock {
-  f16x8 k[2][4];   // K rows kb + 16 t + c, dims 32 s + 8 g .. +8
-  f16x8 v[8];      // V row kb + (l & 31), dims 16 i + 8 (l >> 5) .. +8
-};
-
 __global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefillParams p) {
   __shared__ __align__(16) _Float16 lds[kFpWaves * kVtHalves];
+  __shared__ float fml[2][kFpWaves][kFpQueries];   // each wave's (m, l) per query
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15;
   const int g = lane >> 4;
-  const int h = blockIdx.x;
-  const int q0 = blockIdx.y * kFpQueries;
+  const int ntile = (p.tokens + kFpQueries - 1) / kFpQueries;
+  const int nwg = p.num_heads * ntile;
+  int pi = blockIdx.x;                          // XCD-major order: XCD x runs pi in [x nwg/8, (x+1) nwg/8)
+  if (nwg % kXcds == 0) pi = (pi % kXcds) * (nwg / kXcds) + pi / kXcds;
+  const int h = pi / ntile;
+  const int q0 = (ntile - 1 - pi % ntile) * kFpQueries;
   const int nq = min(kFpQueries, p.tokens - q0);
   const int nkeys = p.pos0 + q0 + nq;           // keys [0, nkeys) reach the last query
   const int nblk = (nkeys + kFpKeys - 1) / kFpKeys;
-  const int qpos = p.pos0 + q0 + c;             // this lane's query (beyond nq: unused)
 
-  // B operand of S^T: Q[q0 + c][32 s + 8 g .. +8] (rows past the last query
-  // repeat it; their outputs are not stored)
-  const uint16_t* qrow = p.q + (long long)(q0 + min(c, nq - 1)) * p.q_stride + h * 128 + 8 * g;
-  f16x8 qb[4];
+  // B operand of S^T per query tile u: Q[q0 + 16 u + c][32 s + 8 g .. +8]
+  // (rows past the last query repeat it; their outputs are not stored)
+  f16x8 qb[kQt][4];
+  int qpos[kQt];                                // this lane's query position per tile
 #pragma unroll
-  for (int s = 0; s < 4; ++s) qb[s] = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
+  for (int u = 0; u < kQt; ++u) {
+    const uint16_t* qrow = p.q + (long long)(q0 + min(16 * u + c, nq - 1)) * p.q_stride + h * 128 + 8 * g;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) qb[u][s4] = *reinterpret_cast<const f16x8*>(qrow + 32 * s4);
+    qpos[u] = p.pos0 + q0 + 16 * u + c;
+  }
 
   const uint16_t* kbase = p.k + (long long)h * p.head_stride + 8 * g;
   const uint16_t* vbase = p.v + (long long)h * p.head_stride + 8 * (lane >> 5);
-  // Loads of block j (clamped into [0, nblk) so every call issues them; keys
-  // past nkeys repeat key nkeys - 1 and are masked below).
-  auto load = [&](int j, FpBlock& b) {
+  // K rows kb + 16 t + c (dims 32 s + 8 g .. +8) and V row kb + (l & 31)
+  // (dims 16 i + 8 (l >> 5) .. +8) of block j, clamped into [0, nblk) so every
+  // call issues them; keys past nkeys repeat key nkeys - 1 and are masked.
+  f16x8 kr[2][4], vr[8];
+  auto load = [&](int j) {
     j = min(j, nblk - 1);
     const int kb = j * kFpKeys;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const uint16_t* kr = kbase + (long long)min(kb + 16 * t + c, nkeys - 1) * p.row_stride;
+      const uint16_t* row = kbase + (long long)min(kb + 16 * t + c, nkeys - 1) * p.row_stride;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) b.k[t][s] = *reinterpret_cast<const f16x8*>(kr + 32 * s);
+      for (int s4 = 0; s4 < 4; ++s4) kr[t][s4] = *reinterpret_cast<const f16x8*>(row + 32 * s4);
     }
-    const uint16_t* vr = vbase + (long long)min(kb + (lane & 31), nkeys - 1) * p.row_stride;
+    const uint16_t* row = vbase + (long long)min(kb + (lane & 31), nkeys - 1) * p.row_stride;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) b.v[i] = *reinterpret_cast<const f16x8*>(vr + 16 * i);
+    for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const f16x8*>(row + 16 * i);
   };
 
   _Float16* vt = lds + wave * kVtHalves;
-  float m = -__builtin_inff();
-  float l = 0.0f;
-  f32x4 o[8];
+  float m[kQt], l[kQt];
+  f32x4 o[kQt][8];
 #pragma unroll
-  for (int n = 0; n < 8; ++n) o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int u = 0; u < kQt; ++u) {
+    m[u] = -__builtin_inff();
+    l[u] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[u][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
 
-  auto compute = [&](int j, const FpBlock& b) {
+  int j = wave;
+  if (j < nblk) load(j);
+  for (; j < nblk; j += kFpWaves) {
     const int kb = j * kFpKeys;
-    // V^T into LDS: dim 16 i + 8 (l >> 5) + e, key l & 31
-    wave_lds_fence();                            // the previous block's V^T reads are done
+    // V^T into LDS (dim 16 i + 8 (l >> 5) + e, key l & 31), then S^T per tile;
+    // after that this block's K and V registers are free for the next block.
+    wave_lds_fence();                          // the previous block's V^T reads are done
     {
       const int kk = lane & 31, dh = 8 * (lane >> 5);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vt[(16 * i + dh + e) * kVtLd + kk] = b.v[i][e];
+        for (int e = 0; e < 8; ++e) vt[(16 * i + dh + e) * kVtLd + kk] = vr[i][e];
     }
-    f32x4 st[2];
+    f32x4 st[kQt][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u = 0; u < kQt; ++u)
 #pragma unroll
-      for (int s = 0; s < 4; ++s) st[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[t][s], qb[s], st[t], 0, 0, 0);
-    }
-    // online softmax of query c over keys kb + 16 t + 4 g + r
-    float sv[8];
-    float bmax = -__builtin_inff();
+      for (int t = 0; t < 2; ++t) {
+        st[u][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kb + 16 * t + 4 * g + r;
-        const float s = key <= qpos ? st[t][r] * p.scale_log2 : -__builtin_inff();
-        sv[4 * t + r] = s;
-        bmax = fmaxf(bmax, s);
+        for (int s4 = 0; s4 < 4; ++s4)
+          st[u][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[t][s4], qb[u][s4], st[u][t], 0, 0, 0);
       }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-    const float mn = fmaxf(m, bmax);
-    const float mref = mn == -__builtin_inff() ? 0.0f : mn;   // no key yet: every weight is 0
-    const float alpha = __builtin_amdgcn_exp2f(m - mref);
-    f16x8 pb;
-    float ps = 0.0f;
+    load(j + kFpWaves);
+    __builtin_amdgcn_sched_barrier(0);         // keep the next block's loads here
+    // online softmax of query (u, c) over keys kb + 16 t + 4 g + r
+    f16x8 pb[kQt];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      // the sum takes the rounded weights the product uses, so O / l stays a
-      // weighted mean of V rows
-      pb[e] = (_Float16)__builtin_amdgcn_exp2f(sv[e] - mref);
-      ps += (float)pb[e];
+    for (int u = 0; u < kQt; ++u) {
+      float sv[8];
+      float bmax = -__builtin_inff();
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = kb + 16 * t + 4 * g + r;
+          const float s = key <= qpos[u] ? st[u][t][r] * p.scale_log2 : -__builtin_inff();
+          sv[4 * t + r] = s;
+          bmax = fmaxf(bmax, s);
+        }
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
+      bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+      const float mn = fmaxf(m[u], bmax);
+      const float mref = mn == -__builtin_inff() ? 0.0f : mn;   // no key yet: every weight is 0
+      const float alpha = __builtin_amdgcn_exp2f(m[u] - mref);
+      float ps = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // the sum takes the rounded weights the product uses, so O / l stays
+        // a weighted mean of V rows
+        pb[u][e] = (_Float16)__builtin_amdgcn_exp2f(sv[e] - mref);
+        ps += (float)pb[u][e];
+      }
+      l[u] = l[u] * alpha + ps;
+      m[u] = mn;
+      if (__any(alpha != 1.0f)) {              // the running maximum moved for some query
+#pragma unroll
+        for (int n = 0; n < 8; ++n) o[u][n] *= alpha;
+      }
     }
-    l = l * alpha + ps;
-    m = mn;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) o[n] *= alpha;
-    wave_lds_fence();                            // V^T stores visible to the wave
+    wave_lds_fence();                          // V^T stores visible to the wave
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
       const _Float16* row = vt + (16 * n + c) * kVtLd + 4 * g;
       const f16x4 lo = *reinterpret_cast<const f16x4*>(row);
       const f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16);
       const f16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-      o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[n], 0, 0, 0);
-    }
-  };
-
-  // Wave-uniform loop over this wave's blocks, the next block's loads issued
-  // before the current block's arithmetic (two register sets, alternating).
-  int j = wave;
-  if (j < nblk) {
-    FpBlock b0, b1;
-    load(j, b0);
-    for (;;) {
-      load(j + kFpWaves, b1);
-      compute(j, b0);
-      j += kFpWaves;
-      if (j >= nblk) break;
-      load(j + kFpWaves, b0);
-      compute(j, b1);
-      j += kFpWaves;
-      if (j >= nblk) break;
+#pragma unroll
+      for (int u = 0; u < kQt; ++u) o[u][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[u], o[u][n], 0, 0, 0);
     }
   }
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
+#pragma unroll
+  for (int u = 0; u < kQt; ++u) {
+    l[u] += __shfl_xor(l[u], 16);
+    l[u] += __shfl_xor(l[u], 32);
+    if (g == 0) {
+      fml[0][wave][16 * u + c] = m[u];
+      fml[1][wave][16 * u + c] = l[u];
+    }
+  }
 
-  // Fold the four waves' states: O rows [wave][query][dim], then m and l.
-  __syncthreads();                               // every wave is done with its V^T
+  // Fold the four waves' states one query tile at a time: O rows
+  // [wave][query][dim] in the V^T buffers, then each thread 8 dims of a query.
   float* fo = reinterpret_cast<float*>(lds);
-  float* fm = fo + kFpWaves * kFpQueries * kOLd;
-  float* fl = fm + kFpWaves * kFpQueries;
+  const int q = tid >> 4;
+  const int d0 = (tid & 15) * 8;
 #pragma unroll
-  for (int n = 0; n < 8; ++n)
-    *reinterpret_cast<f32x4*>(fo + (wave * kFpQueries + c) * kOLd + 16 * n + 4 * g) = o[n];
-  if (g == 0) {
-    fm[wave * kFpQueries + c] = m;
-    fl[wave * kFpQueries + c] = l;
-  }
-  __syncthreads();
-  const int q = tid >> 4;                        // query of this thread
-  const int d0 = (tid & 15) * 8;                 // its 8 dims
-  if (q < nq) {
-    float mw[kFpWaves];
-    float M = -__builtin_inff();
+  for (int u = 0; u < kQt; ++u) {
+    __syncthreads();                           // V^T, or the previous tile's fold, is done
 #pragma unroll
-    for (int w = 0; w < kFpWaves; ++w) {
-      mw[w] = fm[w * kFpQueries + q];
-      M = fmaxf(M, mw[w]);
+    for (int n = 0; n < 8; ++n)
+      *reinterpret_cast<f32x4*>(fo + (wave * 16 + c) * kOLd + 16 * n + 4 * g) = o[u][n];
+    __syncthreads();
+    const int qq = 16 * u + q;
+    if (qq < nq) {
+      float mw[kFpWaves];
+      float M = -__builtin_inff();
+#pragma unroll
+      for (int w = 0; w < kFpWaves; ++w) {
+        mw[w] = fml[0][w][qq];
+        M = fmaxf(M, mw[w]);
+      }
+      float L = 0.0f;
+      float acc[8] = {};
+#pragma unroll
+      for (int w = 0; w < kFpWaves; ++w) {
+        const float sc = mw[w] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
+        L += sc * fml[1][w][qq];
+        const float* row = fo + (w * 16 + q) * kOLd + d0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += sc * row[e];
+      }
+      f16x8 outv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) outv[e] = (_Float16)(acc[e] / L);
+      *reinterpret_cast<f16x8*>(p.out + (long long)(q0 + qq) * p.out_stride + h * 128 + d0) = outv;
     }
-    float L = 0.0f;
-    float acc[8] = {};
-#pragma unroll
-    for (int w = 0; w < kFpWaves; ++w) {
-      const float sc = mw[w] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
-      L += sc * fl[w * kFpQueries + q];
-      const float* row = fo + (w * kFpQueries + q) * kOLd + d0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[e] += sc * row[e];
-    }
-    f16x8 outv;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) outv[e] = (_Float16)(acc[e] / L);
-    *reinterpret_cast<f16x8*>(p.out + (long long)(q0 + q) * p.out_stride + h * 128 + d0) = outv;
   }
 }
 
 }  // namespace
 
 hipError_t launch_flash_prefill(const FlashPrefillParams& p, hipStream_t stream) {
-  const dim3 grid(p.num_heads, (p.tokens + kFpQueries - 1) / kFpQueries);
+  const dim3 grid(p.num_heads * ((p.tokens + kFpQueries - 1) / kFpQueries));
   hipLaunchKernelGGL(flash_prefill_kernel, grid, dim3(kFpWaves * 64), 0, stream, p);
   return hipGetLastError();
 }

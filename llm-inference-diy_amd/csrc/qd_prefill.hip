@@ -333,6 +333,7 @@ constexpr int kMmLd = kMmK + 8;             // LDS row stride in halves
 constexpr int kMmStage = kMmTile * kMmK / 8 / 256;   // 16-byte chunks per thread per operand
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 
 template <int kEpi>
 __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) {
@@ -427,6 +428,128 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
     }
 }
 
+// Large-M form of the same product (M >= 512: the matrix-core prefill's 2048-
+// token passes): a 128 x 128 workgroup tile computed as Y^T = W X^T, so the
+// MFMA's A operand is W's rows and B the tokens' rows, and accumulator lane
+// (g = l / 16, c = l % 16) holds rows 4 g .. 4 g + 3 of W for token c: four
+// adjacent outputs of one token, stored as 8 bytes.  Four waves of 64 x 64
+// (4 x 4 MFMA blocks) per workgroup and K tiles of 64 through LDS, the next
+// tile's loads in flight in registers; per 32 of K a wave reads 8 fragments
+// for 16 MFMAs (a 64 x 64 tile does twice the work of a 32 x 32 one per byte
+// of LDS, and a 128 x 128 workgroup twice the work of a 64 x 64 one per byte
+// of L2).  The grid is one-dimensional and its index is remapped so that,
+// with workgroups dealt to the 8 XCDs in turn, XCD x computes a contiguous
+// eighth of W's row tiles for all tokens and its L2 holds only that eighth of
+// W.  Requires y and res 8-byte aligned and ldy a multiple of 4.
+constexpr int kBt = 128;                     // tokens per workgroup
+constexpr int kBn = 128;                     // rows of W per workgroup
+constexpr int kBk = 64;                      // K per LDS tile
+constexpr int kBLd = kBk + 8;                // LDS row stride in halves
+constexpr int kBStage = kBt * kBk / 8 / 256; // 16-byte chunks per thread per operand (4)
+constexpr int kGemmXcds = 8;                 // MI355X: workgroups are dealt to 8 XCDs in turn
+
+template <int kEpi>
+__global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvParams p) {
+  __shared__ __align__(16) uint16_t xs[kBt * kBLd];
+  __shared__ __align__(16) uint16_t ws[kBn * kBLd];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int ttiles = (p.t + kBt - 1) / kBt;
+  const int nwg = ttiles * ((p.n + kBn - 1) / kBn);
+  int pi = blockIdx.x;                         // XCD-major: XCD x takes pi in [x nwg/8, (x+1) nwg/8)
+  if (nwg % kGemmXcds == 0) pi = (pi % kGemmXcds) * (nwg / kGemmXcds) + pi / kGemmXcds;
+  const int n0 = (pi / ttiles) * kBn;
+  const int t0 = (pi % ttiles) * kBt;
+  // staging map: chunk i of this thread is row (tid + 256 i) / 8 of the tile,
+  // halves 8 ((tid + 256 i) % 8) .. +8 of its K tile (k is a multiple of 64,
+  // so every chunk lies inside k)
+  const uint16_t* xg[kBStage];
+  const uint16_t* wg[kBStage];
+  int so[kBStage];
+#pragma unroll
+  for (int i = 0; i < kBStage; ++i) {
+    const int c = tid + 256 * i;
+    const int r = c >> 3, col = (c & 7) * 8;
+    so[i] = r * kBLd + col;
+    xg[i] = p.x + (long long)min(t0 + r, p.t - 1) * p.ldx + col;
+    wg[i] = p.w + (long long)min(n0 + r, p.n - 1) * p.k + col;
+  }
+  f16x8 xr[kBStage], wr[kBStage];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < kBStage; ++i) {
+      xr[i] = *reinterpret_cast<const f16x8*>(xg[i] + k0);
+      wr[i] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(wg[i] + k0));
+    }
+  };
+  const int wn = (wave >> 1) * 64, wt = (wave & 1) * 64;
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const int ktiles = p.k / kBk;
+  fetch(0);
+  for (int kt = 0; kt < ktiles; ++kt) {
+    __syncthreads();                           // every wave is done with the previous tile
+#pragma unroll
+    for (int i = 0; i < kBStage; ++i) {
+      *reinterpret_cast<f16x8*>(&xs[so[i]]) = xr[i];
+      *reinterpret_cast<f16x8*>(&ws[so[i]]) = wr[i];
+    }
+    __syncthreads();
+    if (kt + 1 < ktiles) fetch((kt + 1) * kBk);
+#pragma unroll
+    for (int ks = 0; ks < kBk; ks += 32) {
+      f16x8 a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = *reinterpret_cast<const f16x8*>(&ws[(wn + 16 * i + fr) * kBLd + ks + fk]);
+        b[i] = *reinterpret_cast<const f16x8*>(&xs[(wt + 16 * i + fr) * kBLd + ks + fk]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+  }
+  // block (i, j): rows n0 + wn + 16 i + 4 (l / 16) + r of W, token t0 + wt + 16 j + l % 16
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = t0 + wt + 16 * j + fr;
+    if (t >= p.t) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = n0 + wn + 16 * i + (lane >> 4) * 4;
+      if (n >= p.n) continue;
+      _Float16* dst = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
+      const _Float16* res = reinterpret_cast<const _Float16*>(p.res) + (long long)t * p.ldy + n;
+      if (n + 4 <= p.n) {
+        f16x4_t v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = to_f16(acc[i][j][r]);
+        if constexpr (kEpi == 1) {
+          const f16x4_t rv = *reinterpret_cast<const f16x4_t*>(res);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = (_Float16)((float)rv[r] + (float)v[r]);
+        }
+        *reinterpret_cast<f16x4_t*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (n + r >= p.n) break;
+          _Float16 y = to_f16(acc[i][j][r]);
+          if constexpr (kEpi == 1) y = (_Float16)((float)res[r] + (float)y);
+          dst[r] = y;
+        }
+      }
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float eps, uint16_t* xn,
@@ -480,6 +603,16 @@ hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t*
 
 hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream) {
   if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
+  const bool vec8 = ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) == 0 &&
+                    p.ldy % 4 == 0;
+  if (p.t >= 512 && vec8) {
+    const dim3 grid(((p.n + kBn - 1) / kBn) * ((p.t + kBt - 1) / kBt));
+    if (epi == 0)
+      hipLaunchKernelGGL(gemm_nt_mfma128_kernel<0>, grid, dim3(256), 0, stream, p);
+    else
+      hipLaunchKernelGGL(gemm_nt_mfma128_kernel<1>, grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+  }
   const dim3 grid((p.n + kMmTile - 1) / kMmTile, (p.t + kMmTile - 1) / kMmTile);
   if (epi == 0)
     hipLaunchKernelGGL(gemm_nt_mfma_kernel<0>, grid, dim3(256), 0, stream, p);

@@ -59,7 +59,10 @@ def test_exact_mode_is_the_decode_gemv(qdiy, m, n, k, with_res):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (37, 100, 512), (127, 6144, 2048), (256, 2048, 5504),
-                                   (200, 5504, 2048)])
+                                   (200, 5504, 2048),
+                                   # m >= 512: the 128 x 128 tile (ragged m and n, a partial
+                                   # group of four outputs at n = 130)
+                                   (600, 130, 512), (1024, 2048, 5504), (2048, 6144, 2048)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_mfma_mode_within_fp32_summation_bound(qdiy, m, n, k, with_res):
     rng = np.random.default_rng(7 * m + n + k + with_res)
@@ -96,6 +99,31 @@ def test_gemm_nt_rejects_bad_arguments(qdiy):
         qdiy.gemm_nt(big[:4 * 64], w, big[128:128 + 4 * 16], 4, 16, 64)
     qdiy.gemm_nt(x, w, y, 4, 16, 64, mode=qdiy.GEMM_MFMA, ldx=96)     # strided x is fine
     torch.cuda.synchronize()
+
+
+def test_mfma_large_m_unaligned_output_and_in_place_residual(qdiy):
+    """m >= 512 with y rows an odd number of elements apart (the 64 x 64 tile
+    takes it) and with the residual added in place (the 128 x 128 tile): both
+    within the fp32 summation bound."""
+    m, n, k = 640, 96, 256
+    rng = np.random.default_rng(3)
+    x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
+    x64, W64 = x.astype(np.float64), W.astype(np.float64)
+    s = x64 @ W64.T
+    bound = k * 2.0 ** -23 * (np.abs(x64) @ np.abs(W64).T)
+    ldy = n + 1
+    y = torch.zeros(m * ldy, dtype=torch.float16, device="cuda")
+    qdiy.gemm_nt(_dev(x.reshape(-1)), _dev(W.reshape(-1)), y, m, n, k, mode=qdiy.GEMM_MFMA, ldy=ldy)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().reshape(m, ldy)[:, :n].astype(np.float64)
+    assert np.all(np.abs(got - s) <= ulp16(s) + bound)
+    yr = _dev(R.reshape(-1))
+    qdiy.gemm_nt(_dev(x.reshape(-1)), _dev(W.reshape(-1)), yr, m, n, k, residual=yr, mode=qdiy.GEMM_MFMA)
+    torch.cuda.synchronize()
+    got = yr.cpu().numpy().reshape(m, n).astype(np.float64)
+    h = s.astype(np.float16).astype(np.float64)
+    want = R.astype(np.float64) + h
+    assert np.all(np.abs(got - want) <= ulp16(want) + ulp16(h) + bound + ulp16(s))
 
 
 @pytest.mark.parametrize("hidden,inter", [(512, 1368), (2048, 5504)])

@@ -119,6 +119,7 @@ CASES = [  # H, pos0, T, layout, q_pad, out_pad
     (16, 777, 33, "head_major", 8, 8),
     (4, 1000, 256, "engine", 0, 0),
     (12, 31, 17, "head_major", 0, 0),
+    (12, 5, 40, "engine", 0, 0),         # 36 workgroups: not a multiple of the 8 XCDs
 ]
 
 
@@ -135,7 +136,8 @@ def test_exact_mode_is_decode_attention(qdiy, H, pos0, T, layout, q_pad, out_pad
         pr.close()
 
 
-@pytest.mark.parametrize("H,pos0,T,layout,q_pad,out_pad", CASES + [(16, 1792, 256, "engine", 4096, 0)])
+@pytest.mark.parametrize("H,pos0,T,layout,q_pad,out_pad",
+                         CASES + [(16, 1792, 256, "engine", 4096, 0), (4, 0, 2048, "engine", 1024, 0)])
 def test_mfma_mode_within_2e3(qdiy, H, pos0, T, layout, q_pad, out_pad):
     pr = Prompt(qdiy, H, pos0, T, seed=H * 11 + pos0 + T, layout=layout, q_pad=q_pad, out_pad=out_pad)
     try:
