@@ -46,7 +46,7 @@ for _p in (ROOT, PKG):
 H, D = 16, 128
 HID = H * D
 PEAK_GBPS = 8000.0
-KV_LENS = (512, 8192, 32768)
+KV_LENS = (512, 8192, 16384, 32768)
 HEADLINE_L = 8192
 METRIC = "decode-attention achieved HBM GB/s (% of peak) + µs/call at KV 512/8K/32K"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode_attention_L8192.json")
@@ -398,7 +398,7 @@ def main() -> int:
                                "decode_attention_scan_kernel + decode_attention_merge_kernel)",
                      "achieved": round(head["gbps"], 1), "peak": PEAK_GBPS,
                      "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": traffic,
-                     "per_kernel_trace": "profiles/decode_attention_kernel_trace_L512_L8192_L32768.md"},
+                     "per_kernel_trace": "profiles/decode_attention_kernel_trace_L512_to_L32768.md"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -461,16 +461,16 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvPara
   if (nwg % kGemmXcds == 0) pi = (pi % kGemmXcds) * (nwg / kGemmXcds) + pi / kGemmXcds;
   const int n0 = (pi / ttiles) * kBn;
   const int t0 = (pi % ttiles) * kBt;
-  // staging map: chunk i of this thread is row (tid + 256 i) / 8 of the tile,
-  // halves 8 ((tid + 256 i) % 8) .. +8 of its K tile (k is a multiple of 64,
-  // so every chunk lies inside k)
+  // staging map: chunk i of this thread is row (tid + 256 i) / (kBk / 8) of
+  // the tile, halves 8 ((tid + 256 i) % (kBk / 8)) .. +8 of its K tile (k is a
+  // multiple of kBk, so every chunk lies inside k)
   const uint16_t* xg[kBStage];
   const uint16_t* wg[kBStage];
   int so[kBStage];
 #pragma unroll
   for (int i = 0; i < kBStage; ++i) {
     const int c = tid + 256 * i;
-    const int r = c >> 3, col = (c & 7) * 8;
+    const int r = c / (kBk / 8), col = (c % (kBk / 8)) * 8;
     so[i] = r * kBLd + col;
     xg[i] = p.x + (long long)min(t0 + r, p.t - 1) * p.ldx + col;
     wg[i] = p.w + (long long)min(n0 + r, p.n - 1) * p.k + col;
@@ -605,7 +605,7 @@ hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t str
   if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
   const bool vec8 = ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) == 0 &&
                     p.ldy % 4 == 0;
-  if (p.t >= 512 && vec8) {
+  if (p.t >= 512 && vec8 && p.k % kBk == 0) {
     const dim3 grid(((p.n + kBn - 1) / kBn) * ((p.t + kBt - 1) / kBt));
     if (epi == 0)
       hipLaunchKernelGGL(gemm_nt_mfma128_kernel<0>, grid, dim3(256), 0, stream, p);

@@ -95,6 +95,9 @@ def test_calls_reject_null_context(qdiy):
     assert lib.qd_decode_attention_split(None, p, p, p, p, 1, 16, 128, 4, None) == qdiy.QD_EINVAL
     assert lib.qd_qkv_bias_rope_cache(None, p, None, p, p, 0, 8, 16, 128, None) == qdiy.QD_EINVAL
     assert b"ctx" in lib.qd_last_error()
+    assert lib.qd_prefill_attention(None, p, 2048, p, p, p, 2048, 0, 4, 16, 128, qdiy.GEMM_MFMA,
+                                    None) == qdiy.QD_EINVAL
+    assert b"ctx" in lib.qd_last_error()
     v, s = ctypes.c_int(), ctypes.c_int()
     assert lib.qd_decode_attention_plan(None, 1, ctypes.byref(v), ctypes.byref(s)) == qdiy.QD_EINVAL
     assert lib.qd_ctx_destroy(None) == qdiy.QD_OK
