@@ -152,3 +152,31 @@ def test_engine_mfma_prefill(qdiy, hidden, inter):
     d = np.abs(exact[0] - mfma[0])
     assert float(np.max(d)) <= 0.02 * float(np.max(np.abs(exact[0]))) + 0.01, float(np.max(d))
     assert float(np.corrcoef(exact[0], mfma[0])[0, 1]) > 0.999
+
+
+def test_engine_mfma_prefill_two_passes(qdiy):
+    """A 2300-token prompt: the MFMA mode runs it as passes of 2048 and 251 tokens (the
+    second pass's attention starts at position 2048, over the first pass's KV rows), the
+    exact mode as passes of 256. The next step's logits agree as above, and switching the
+    mode back and forth keeps both working."""
+    cfg = qdiy.model_cfg(vocab_size=512, hidden_size=512, num_layers=2, num_heads=4,
+                         intermediate_size=1408, max_seqlen=2400)
+    img = qdiy.random_model_image(cfg, 77, 0.03, nthreads=8)
+    prompt = [int(t) for t in np.random.default_rng(2300).integers(0, 512, 2300)]
+    logits = {}
+    with qdiy.Engine(image=img) as eng:
+        for mode in (qdiy.GEMM_MFMA, qdiy.GEMM_EXACT, qdiy.GEMM_MFMA):
+            eng.set_prefill_mode(mode)
+            eng.reset()
+            pos = eng.prefill(prompt[:-1])
+            assert pos == len(prompt) - 1
+            eng.step(prompt[-1], pos)
+            got = eng.logits().astype(np.float64)
+            if mode in logits:
+                assert _same(logits[mode], got), "the same mode must repeat bit for bit"
+            logits[mode] = got
+    exact, mfma = logits[qdiy.GEMM_EXACT], logits[qdiy.GEMM_MFMA]
+    assert np.all(np.isfinite(mfma))
+    d = np.abs(exact - mfma)
+    assert float(np.max(d)) <= 0.02 * float(np.max(np.abs(exact))) + 0.01, float(np.max(d))
+    assert float(np.corrcoef(exact, mfma)[0, 1]) > 0.999
