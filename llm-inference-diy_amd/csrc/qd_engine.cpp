@@ -148,6 +148,7 @@ struct qd_engine {
   int* p_tokens = nullptr;
   uint16_t *p_x = nullptr, *p_xn = nullptr, *p_qkv = nullptr, *p_att = nullptr;
   uint16_t *p_g = nullptr, *p_u = nullptr, *p_act = nullptr;
+  float* p_split = nullptr;             // split-K partials of the MFMA prefill GEMMs
 
   const uint16_t* w(long long off) const { return weights + off; }
   uint16_t* kc(int l) const { return k_cache + (long long)l * cfg.max_seqlen * cfg.hidden_size; }
@@ -171,6 +172,7 @@ void engine_free(qd_engine* e) {
   (void)hipFree(e->act);
   (void)hipFree(e->logits);
   (void)hipFree(e->lm_ws);
+  (void)hipFree(e->p_split);
   for (void* q : {(void*)e->p_tokens, (void*)e->p_x, (void*)e->p_xn, (void*)e->p_qkv, (void*)e->p_att,
                   (void*)e->p_g, (void*)e->p_u, (void*)e->p_act})
     (void)hipFree(q);
@@ -251,7 +253,8 @@ int prefill_batched(qd_engine* e, const int* tokens, int T, int pos0) {
   auto gemv = [&](const uint16_t* x, long long ldx, const uint16_t* w, int n, int k, uint16_t* y,
                   long long ldy, int epi) {
     qd::BatchedGemvParams p{x, ldx, w, n, k, T, y, ldy, y};
-    if (e->prefill_mode == QD_GEMM_MFMA && k % 64 == 0) return qd::launch_gemm_mfma(p, epi, e->stream);
+    if (e->prefill_mode == QD_GEMM_MFMA && k % 64 == 0)
+      return qd::launch_gemm_mfma_split(p, epi, e->p_split, qd::kGemmSplitWsBytes, e->stream);
     return qd::launch_gemv_batched(p, epi, e->stream);
   };
   for (uint32_t l = 0; l < c.num_layers && he == hipSuccess; ++l) {
@@ -491,7 +494,8 @@ int qd_engine_create_from_image(const void* image, long long bytes, qd_engine** 
   struct { void** p; long long n; } allocs[] = {
       {(void**)&e->weights, wbytes},  {(void**)&e->k_cache, e->kv_bytes}, {(void**)&e->v_cache, e->kv_bytes},
       {(void**)&e->x, H * 2},         {(void**)&e->qkv, 3 * H * 2},     {(void**)&e->attn_out, H * 2},
-      {(void**)&e->act, I * 2},       {(void**)&e->logits, V * 2},      {&e->lm_ws, (long long)e->lm_ws_bytes}};
+      {(void**)&e->act, I * 2},       {(void**)&e->logits, V * 2},      {&e->lm_ws, (long long)e->lm_ws_bytes},
+      {(void**)&e->p_split, (long long)qd::kGemmSplitWsBytes}};
   for (auto& a : allocs) {
     if ((he = hipMalloc(a.p, (size_t)a.n)) != hipSuccess) {
       engine_free(e);

@@ -157,6 +157,10 @@ struct BatchedGemvParams {
   uint16_t* y;
   long long ldy;
   const uint16_t* res;    // epilogue 1 only
+  // Split-K form of the MFMA product only: slice z of K (kslice wide) writes
+  // its fp32 sums to part + z * t * n ([t][n] rows); set by launch_gemm_mfma_split.
+  float* part;
+  int kslice;
 };
 
 // Causal prefill attention of `tokens` queries at positions pos0, pos0 + 1, ...
@@ -228,6 +232,13 @@ hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t 
 // The same product on the matrix cores (fp32 accumulation in the hardware's
 // order, not bit-reproducible on the host); p.k must be a multiple of 64.
 hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream);
+// The same, allowed to split K over up to 4 workgroups per tile when the tile
+// grid leaves CUs idle: fp32 partial sums in `workspace` (kGemmSplitWsBytes
+// suffice for every shape), then one launch folds them in slice order and
+// applies the epilogue.  Without a workspace it is launch_gemm_mfma.
+constexpr size_t kGemmSplitWsBytes = (size_t)4 << 20;
+hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* workspace,
+                                  size_t workspace_bytes, hipStream_t stream);
 hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_layer,
                                uint16_t* v_layer, const float2* rope_cs, long long row_stride,
                                long long head_stride, int pos0, int num_heads, int T,

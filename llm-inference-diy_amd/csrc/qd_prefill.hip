@@ -20,6 +20,8 @@
 //   rope_batched_kernel        bias + RoPE + KV append per token (qd_rope_cache)
 //   swiglu_batched_kernel      act = half(g * (u / (1 + exp(-u))))
 // Attention runs per token with qd_decode_attention's plan for that length.
+#include <algorithm>
+
 #include "qd_device.h"
 #include "qd_internal.h"
 
@@ -326,7 +328,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
 // not 32.  Two workgroups fit a CU (2 x 67.6 KB of its 160 KB LDS).  Tokens
 // past t and rows past n load clamped rows and are not stored; the K past the
 // end of a partial last tile is staged as zeros, which add nothing.  K must be
-// a multiple of 64.
+// a multiple of 64.  kEpi 2 is the split-K form: workgroup z = blockIdx.z sums
+// K slice [z kslice, (z + 1) kslice) and stores its fp32 tile to p.part.
 constexpr int kMmTile = 64;                 // tokens and rows per workgroup
 constexpr int kMmK = 256;                   // K per LDS tile
 constexpr int kMmLd = kMmK + 8;             // LDS row stride in halves
@@ -357,12 +360,17 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
     xg[i] = p.x + (long long)min(t0 + sr[i], p.t - 1) * p.ldx + sc[i];
     wg[i] = p.w + (long long)min(n0 + sr[i], p.n - 1) * p.k + sc[i];
   }
+  int kbeg = 0, kend = p.k;
+  if constexpr (kEpi == 2) {
+    kbeg = blockIdx.z * p.kslice;
+    kend = min(p.k, kbeg + p.kslice);
+  }
   f16x8 xr[kMmStage], wr[kMmStage];
   const f16x8 zero = {};
   auto fetch = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < kMmStage; ++i) {
-      if (k0 + sc[i] < p.k) {
+      if (k0 + sc[i] < kend) {
         xr[i] = *reinterpret_cast<const f16x8*>(xg[i] + k0);
         wr[i] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(wg[i] + k0));
       } else {
@@ -378,8 +386,8 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const int ktiles = (p.k + kMmK - 1) / kMmK;
-  fetch(0);
+  const int ktiles = kend > kbeg ? (kend - kbeg + kMmK - 1) / kMmK : 0;
+  if (ktiles > 0) fetch(kbeg);
   for (int kt = 0; kt < ktiles; ++kt) {
     __syncthreads();                           // every wave is done with the previous tile
 #pragma unroll
@@ -388,8 +396,8 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
       *reinterpret_cast<f16x8*>(&ws[sr[i] * kMmLd + sc[i]]) = wr[i];
     }
     __syncthreads();
-    if (kt + 1 < ktiles) fetch((kt + 1) * kMmK);
-    const int kn = min(kMmK, p.k - kt * kMmK);   // a multiple of 64
+    if (kt + 1 < ktiles) fetch(kbeg + (kt + 1) * kMmK);
+    const int kn = min(kMmK, kend - kbeg - kt * kMmK);   // a multiple of 64
     for (int ks = 0; ks < kn; ks += 32) {
       f16x8 a[2], b[2];
 #pragma unroll
@@ -416,6 +424,10 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
       for (int r = 0; r < 4; ++r) {
         const int t = t0 + wm + 16 * i + (lane >> 4) * 4 + r;
         if (t >= p.t) continue;
+        if constexpr (kEpi == 2) {
+          p.part[((long long)blockIdx.z * p.t + t) * p.n + n] = acc[i][j][r];
+          continue;
+        }
         const _Float16 y = to_f16(acc[i][j][r]);
         _Float16* dst = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
         if constexpr (kEpi == 0) {
@@ -426,6 +438,22 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
         }
       }
     }
+}
+
+// Folds the split-K partials of gemm_nt_mfma_kernel<2>: the slices' fp32 sums
+// added in slice order, then the epilogue of kEpi (0: half(sum); 1: half(R +
+// half(sum))).  One thread per output.
+template <int kEpi>
+__global__ __launch_bounds__(256) void splitk_fold_kernel(BatchedGemvParams p, int splits) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  const long long tn = (long long)p.t * p.n;
+  if (i >= tn) return;
+  float s = p.part[i];
+  for (int z = 1; z < splits; ++z) s += p.part[z * tn + i];
+  const long long t = i / p.n, n = i - t * p.n;
+  _Float16 y = to_f16(s);
+  if constexpr (kEpi == 1) y = (_Float16)((float)reinterpret_cast<const _Float16*>(p.res)[t * p.ldy + n] + (float)y);
+  reinterpret_cast<_Float16*>(p.y)[t * p.ldy + n] = y;
 }
 
 // Large-M form of the same product (M >= 512: the matrix-core prefill's 2048-
@@ -619,6 +647,36 @@ hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t str
   else
     hipLaunchKernelGGL(gemm_nt_mfma_kernel<1>, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+  if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
+  const long long tiles = (long long)((p.n + kMmTile - 1) / kMmTile) * ((p.t + kMmTile - 1) / kMmTile);
+  const bool small = p.t < 512 || ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) ||
+                     p.ldy % 4 || p.k % kBk;    // the conditions under which launch_gemm_mfma takes the 64 x 64 tile
+  int splits = small && workspace ? (int)std::min<long long>(4, 256 / tiles) : 1;
+  if (splits > 1) {
+    // slices of whole K tiles, none empty
+    const int kslice = ((p.k + splits - 1) / splits + kMmK - 1) / kMmK * kMmK;
+    splits = (p.k + kslice - 1) / kslice;
+    if (splits > 1 && (size_t)splits * p.t * p.n * sizeof(float) <= workspace_bytes) {
+      BatchedGemvParams q = p;
+      q.part = workspace;
+      q.kslice = kslice;
+      const dim3 grid((p.n + kMmTile - 1) / kMmTile, (p.t + kMmTile - 1) / kMmTile, splits);
+      hipLaunchKernelGGL(gemm_nt_mfma_kernel<2>, grid, dim3(256), 0, stream, q);
+      hipError_t e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const dim3 fgrid((unsigned)(((long long)p.t * p.n + 255) / 256));
+      if (epi == 0)
+        hipLaunchKernelGGL(splitk_fold_kernel<0>, fgrid, dim3(256), 0, stream, q, splits);
+      else
+        hipLaunchKernelGGL(splitk_fold_kernel<1>, fgrid, dim3(256), 0, stream, q, splits);
+      return hipGetLastError();
+    }
+  }
+  return launch_gemm_mfma(p, epi, stream);
 }
 
 hipError_t launch_embed(const uint16_t* wte, const int* tokens, uint16_t* x, int hidden, int T,
