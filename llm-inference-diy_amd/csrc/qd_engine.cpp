@@ -274,9 +274,18 @@ int prefill_batched(qd_engine* e, const int* tokens, int T, int pos0) {
     if (rc != QD_OK) return rc;
     he = gemv(e->p_att, H, e->w(f.proj_w), H, H, e->p_x, H, 1);
     if (he == hipSuccess) he = qd::launch_rmsnorm_batched(e->p_x, e->w(f.ln_2), kEps, e->p_xn, H, T, e->stream);
-    if (he == hipSuccess) he = gemv(e->p_xn, H, e->w(f.w1), I, H, e->p_g, I, 0);
-    if (he == hipSuccess) he = gemv(e->p_xn, H, e->w(f.w2), I, H, e->p_u, I, 0);
-    if (he == hipSuccess) he = qd::launch_swiglu_batched(e->p_g, e->p_u, e->p_act, (long long)T * I, e->stream);
+    bool joint = false;                          // gate/up GEMM with the SwiGLU in its epilogue
+    if (he == hipSuccess && e->prefill_mode == QD_GEMM_MFMA) {
+      qd::BatchedGemvParams q{e->p_xn, H, e->w(f.w1), I, H, T, e->p_act, I, nullptr};
+      q.w2 = e->w(f.w2);
+      const hipError_t je = qd::launch_gemm_mfma_swiglu(q, e->stream);
+      joint = je == hipSuccess;
+      if (je != hipSuccess && je != hipErrorNotSupported) he = je;
+    }
+    if (he == hipSuccess && !joint) he = gemv(e->p_xn, H, e->w(f.w1), I, H, e->p_g, I, 0);
+    if (he == hipSuccess && !joint) he = gemv(e->p_xn, H, e->w(f.w2), I, H, e->p_u, I, 0);
+    if (he == hipSuccess && !joint)
+      he = qd::launch_swiglu_batched(e->p_g, e->p_u, e->p_act, (long long)T * I, e->stream);
     if (he == hipSuccess) he = gemv(e->p_act, I, e->w(f.w_down), H, I, e->p_x, H, 1);
   }
   return he == hipSuccess ? QD_OK : hip_fail(he, "prefill launch");

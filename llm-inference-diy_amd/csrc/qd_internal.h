@@ -161,6 +161,9 @@ struct BatchedGemvParams {
   // its fp32 sums to part + z * t * n ([t][n] rows); set by launch_gemm_mfma_split.
   float* part;
   int kslice;
+  // Joint gate/up form only (launch_gemm_mfma_swiglu): W2, the up weight, with
+  // w as W1 and y = act.
+  const uint16_t* w2;
 };
 
 // Causal prefill attention of `tokens` queries at positions pos0, pos0 + 1, ...
@@ -239,6 +242,13 @@ hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t str
 constexpr size_t kGemmSplitWsBytes = (size_t)4 << 20;
 hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* workspace,
                                   size_t workspace_bytes, hipStream_t stream);
+// act[t][i] = half(g * (u / (1 + exp(-u)))) with g = half(X W1^T), u = half(X W2^T)
+// (p.w = W1, p.w2 = W2, p.n = inter, p.y = act) in one matrix-core launch, the
+// SwiGLU applied in the GEMM's epilogue.  hipErrorNotSupported (nothing
+// launched) unless t >= 512, act 8-byte aligned, ldy a multiple of 4 and k a
+// multiple of 64: the caller then runs the two projections and
+// launch_swiglu_batched.
+hipError_t launch_gemm_mfma_swiglu(const BatchedGemvParams& p, hipStream_t stream);
 hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_layer,
                                uint16_t* v_layer, const float2* rope_cs, long long row_stride,
                                long long head_stride, int pos0, int num_heads, int T,

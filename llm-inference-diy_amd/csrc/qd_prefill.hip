@@ -469,6 +469,12 @@ __global__ __launch_bounds__(256) void splitk_fold_kernel(BatchedGemvParams p, i
 // with workgroups dealt to the 8 XCDs in turn, XCD x computes a contiguous
 // eighth of W's row tiles for all tokens and its L2 holds only that eighth of
 // W.  Requires y and res 8-byte aligned and ldy a multiple of 4.
+// kEpi 3 is the joint gate/up form: a workgroup takes 64 intermediate rows,
+// its LDS W tile holding those rows of W1 (tile rows 0..63) and of W2 (64..127);
+// wave (wy = w / 2) multiplies gate rows 32 wy .. +32 as its A blocks 0-1 and
+// the same up rows as blocks 2-3, so one lane holds g and u of the same
+// outputs and the epilogue writes act = half(g * (u / (1 + exp(-u)))) on the
+// fp16-rounded g and u, as swiglu_batched_kernel does.
 constexpr int kBt = 128;                     // tokens per workgroup
 constexpr int kBn = 128;                     // rows of W per workgroup
 constexpr int kBk = 64;                      // K per LDS tile
@@ -483,11 +489,12 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvPara
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  constexpr int kRows = kEpi == 3 ? kBn / 2 : kBn;   // rows of the output per workgroup
   const int ttiles = (p.t + kBt - 1) / kBt;
-  const int nwg = ttiles * ((p.n + kBn - 1) / kBn);
+  const int nwg = ttiles * ((p.n + kRows - 1) / kRows);
   int pi = blockIdx.x;                         // XCD-major: XCD x takes pi in [x nwg/8, (x+1) nwg/8)
   if (nwg % kGemmXcds == 0) pi = (pi % kGemmXcds) * (nwg / kGemmXcds) + pi / kGemmXcds;
-  const int n0 = (pi / ttiles) * kBn;
+  const int n0 = (pi / ttiles) * kRows;
   const int t0 = (pi % ttiles) * kBt;
   // staging map: chunk i of this thread is row (tid + 256 i) / (kBk / 8) of
   // the tile, halves 8 ((tid + 256 i) % (kBk / 8)) .. +8 of its K tile (k is a
@@ -501,7 +508,10 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvPara
     const int r = c / (kBk / 8), col = (c % (kBk / 8)) * 8;
     so[i] = r * kBLd + col;
     xg[i] = p.x + (long long)min(t0 + r, p.t - 1) * p.ldx + col;
-    wg[i] = p.w + (long long)min(n0 + r, p.n - 1) * p.k + col;
+    if constexpr (kEpi == 3)
+      wg[i] = (r < 64 ? p.w : p.w2) + (long long)min(n0 + (r & 63), p.n - 1) * p.k + col;
+    else
+      wg[i] = p.w + (long long)min(n0 + r, p.n - 1) * p.k + col;
   }
   f16x8 xr[kBStage], wr[kBStage];
   auto fetch = [&](int k0) {
@@ -534,7 +544,8 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvPara
       f16x8 a[4], b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        a[i] = *reinterpret_cast<const f16x8*>(&ws[(wn + 16 * i + fr) * kBLd + ks + fk]);
+        const int ar = kEpi == 3 ? (i >> 1) * 64 + (wave >> 1) * 32 + 16 * (i & 1) : wn + 16 * i;
+        a[i] = *reinterpret_cast<const f16x8*>(&ws[(ar + fr) * kBLd + ks + fk]);
         b[i] = *reinterpret_cast<const f16x8*>(&xs[(wt + 16 * i + fr) * kBLd + ks + fk]);
       }
 #pragma unroll
@@ -543,6 +554,37 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvPara
         for (int j = 0; j < 4; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
+  }
+  if constexpr (kEpi == 3) {
+    // blocks (i, j) and (i + 2, j), i < 2: gate and up of intermediate rows
+    // n0 + 32 wy + 16 i + 4 (l / 16) + r, token t0 + wt + 16 j + l % 16
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int t = t0 + wt + 16 * j + fr;
+      if (t >= p.t) continue;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int n = n0 + (wave >> 1) * 32 + 16 * i + (lane >> 4) * 4;
+        if (n >= p.n) continue;
+        f16x4_t v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gh = (float)to_f16(acc[i][j][r]);
+          const float uh = (float)to_f16(acc[i + 2][j][r]);
+          const float e = exp2_rep(-uh * kLog2e);
+          v[r] = to_f16(gh * (uh / (1.0f + e)));
+        }
+        _Float16* dst = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
+        if (n + 4 <= p.n) {
+          *reinterpret_cast<f16x4_t*>(dst) = v;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.n) dst[r] = v[r];
+        }
+      }
+    }
+    return;
   }
   // block (i, j): rows n0 + wn + 16 i + 4 (l / 16) + r of W, token t0 + wt + 16 j + l % 16
 #pragma unroll
@@ -646,6 +688,15 @@ hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t str
     hipLaunchKernelGGL(gemm_nt_mfma_kernel<0>, grid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL(gemm_nt_mfma_kernel<1>, grid, dim3(256), 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_mfma_swiglu(const BatchedGemvParams& p, hipStream_t stream) {
+  if (p.t < 512 || p.k < 64 || p.k % kBk != 0 || p.n < 1 || !p.w2 ||
+      (reinterpret_cast<uintptr_t>(p.y) & 7u) || p.ldy % 4)
+    return hipErrorNotSupported;
+  const dim3 grid(((p.n + kBn / 2 - 1) / (kBn / 2)) * ((p.t + kBt - 1) / kBt));
+  hipLaunchKernelGGL(gemm_nt_mfma128_kernel<3>, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
