@@ -244,10 +244,10 @@ hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* wo
                                   size_t workspace_bytes, hipStream_t stream);
 // act[t][i] = half(g * (u / (1 + exp(-u)))) with g = half(X W1^T), u = half(X W2^T)
 // (p.w = W1, p.w2 = W2, p.n = inter, p.y = act) in one matrix-core launch, the
-// SwiGLU applied in the GEMM's epilogue.  hipErrorNotSupported (nothing
-// launched) unless t >= 512, act 8-byte aligned, ldy a multiple of 4 and k a
-// multiple of 64: the caller then runs the two projections and
-// launch_swiglu_batched.
+// SwiGLU applied in the GEMM's epilogue: the 128 x 128 tile from 512 tokens
+// (act 8-byte aligned, ldy a multiple of 4), else the 64 x 64 tile.
+// hipErrorNotSupported (nothing launched) unless k is a multiple of 64: the
+// caller then runs the two projections and launch_swiglu_batched.
 hipError_t launch_gemm_mfma_swiglu(const BatchedGemvParams& p, hipStream_t stream);
 hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_layer,
                                uint16_t* v_layer, const float2* rope_cs, long long row_stride,

@@ -330,6 +330,11 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
 // end of a partial last tile is staged as zeros, which add nothing.  K must be
 // a multiple of 64.  kEpi 2 is the split-K form: workgroup z = blockIdx.z sums
 // K slice [z kslice, (z + 1) kslice) and stores its fp32 tile to p.part.
+// kEpi 3 is the joint gate/up form: a workgroup takes 32 intermediate rows, its
+// W tile holding them from W1 (tile rows 0..31) and W2 (32..63); wave w's B
+// blocks are gate rows 16 (w % 2) .. +16 and the same up rows, so one lane
+// holds g and u of the same output and writes act = half(g * (u / (1 +
+// exp(-u)))) on the fp16-rounded g and u.
 constexpr int kMmTile = 64;                 // tokens and rows per workgroup
 constexpr int kMmK = 256;                   // K per LDS tile
 constexpr int kMmLd = kMmK + 8;             // LDS row stride in halves
@@ -345,7 +350,7 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int n0 = blockIdx.x * kMmTile;
+  const int n0 = blockIdx.x * (kEpi == 3 ? kMmTile / 2 : kMmTile);
   const int t0 = blockIdx.y * kMmTile;
   // staging map: chunk c = tid + 256 i is row c / 32 of the tile, halves
   // 8 (c % 32) .. +8 of its K tile
@@ -358,7 +363,10 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
     sr[i] = c >> 5;
     sc[i] = (c & 31) * 8;
     xg[i] = p.x + (long long)min(t0 + sr[i], p.t - 1) * p.ldx + sc[i];
-    wg[i] = p.w + (long long)min(n0 + sr[i], p.n - 1) * p.k + sc[i];
+    if constexpr (kEpi == 3)
+      wg[i] = (sr[i] < 32 ? p.w : p.w2) + (long long)min(n0 + (sr[i] & 31), p.n - 1) * p.k + sc[i];
+    else
+      wg[i] = p.w + (long long)min(n0 + sr[i], p.n - 1) * p.k + sc[i];
   }
   int kbeg = 0, kend = p.k;
   if constexpr (kEpi == 2) {
@@ -403,7 +411,8 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         a[i] = *reinterpret_cast<const f16x8*>(&xs[(wm + 16 * i + fr) * kMmLd + ks + fk]);
-        b[i] = *reinterpret_cast<const f16x8*>(&ws[(wn + 16 * i + fr) * kMmLd + ks + fk]);
+        const int br = kEpi == 3 ? 32 * i + 16 * (wave & 1) : wn + 16 * i;
+        b[i] = *reinterpret_cast<const f16x8*>(&ws[(br + fr) * kMmLd + ks + fk]);
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
@@ -411,6 +420,24 @@ __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) 
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
+  }
+  if constexpr (kEpi == 3) {
+    // blocks (i, 0) and (i, 1): gate and up of row n0 + 16 (w % 2) + l % 16 for
+    // token t0 + wm + 16 i + 4 (l / 16) + r
+    const int n = n0 + 16 * (wave & 1) + fr;
+    if (n >= p.n) return;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + wm + 16 * i + (lane >> 4) * 4 + r;
+        if (t >= p.t) continue;
+        const float gh = (float)to_f16(acc[i][0][r]);
+        const float uh = (float)to_f16(acc[i][1][r]);
+        const float e = exp2_rep(-uh * kLog2e);
+        reinterpret_cast<_Float16*>(p.y)[(long long)t * p.ldy + n] = to_f16(gh * (uh / (1.0f + e)));
+      }
+    return;
   }
   // D[4 (l / 16) + r][l % 16] of block (i, j): token t0 + wm + 16 i + 4 (l / 16) + r,
   // row n0 + wn + 16 j + l % 16
@@ -692,11 +719,14 @@ hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t str
 }
 
 hipError_t launch_gemm_mfma_swiglu(const BatchedGemvParams& p, hipStream_t stream) {
-  if (p.t < 512 || p.k < 64 || p.k % kBk != 0 || p.n < 1 || !p.w2 ||
-      (reinterpret_cast<uintptr_t>(p.y) & 7u) || p.ldy % 4)
-    return hipErrorNotSupported;
-  const dim3 grid(((p.n + kBn / 2 - 1) / (kBn / 2)) * ((p.t + kBt - 1) / kBt));
-  hipLaunchKernelGGL(gemm_nt_mfma128_kernel<3>, grid, dim3(256), 0, stream, p);
+  if (p.k < 64 || p.k % 64 != 0 || p.n < 1 || p.t < 1 || !p.w2) return hipErrorNotSupported;
+  if (p.t >= 512 && p.k % kBk == 0 && !(reinterpret_cast<uintptr_t>(p.y) & 7u) && p.ldy % 4 == 0) {
+    const dim3 grid(((p.n + kBn / 2 - 1) / (kBn / 2)) * ((p.t + kBt - 1) / kBt));
+    hipLaunchKernelGGL(gemm_nt_mfma128_kernel<3>, grid, dim3(256), 0, stream, p);
+  } else {
+    const dim3 grid((p.n + kMmTile / 2 - 1) / (kMmTile / 2), (p.t + kMmTile - 1) / kMmTile);
+    hipLaunchKernelGGL(gemm_nt_mfma_kernel<3>, grid, dim3(256), 0, stream, p);
+  }
   return hipGetLastError();
 }
 
