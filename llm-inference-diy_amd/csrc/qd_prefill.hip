@@ -239,15 +239,19 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_batched_kernel(BatchedGe
 
 // Bias, rotate-half RoPE and KV append for token t at position pos0 + t: one
 // thread per (head, rotation pair), as qkv_bias_rope_cache_kernel
-// (qd_rope_cache.hip) does for a single token.
-__global__ __launch_bounds__(64) void rope_batched_kernel(uint16_t* qkv, const uint16_t* bias,
+// (qd_rope_cache.hip) does for a single token; kRopeHeads heads (one wave
+// each) per workgroup.  (One head per workgroup measured the same: the
+// scattered 2-byte accesses, not the workgroup count, set its time.)
+constexpr int kRopeHeads = 4;
+__global__ __launch_bounds__(kRopeHeads * 64) void rope_batched_kernel(uint16_t* qkv, const uint16_t* bias,
                                                           uint16_t* k_layer, uint16_t* v_layer,
                                                           const float2* rope_cs, long long row_stride,
                                                           long long head_stride, int pos0,
                                                           int num_heads) {
   const int t = blockIdx.y;
-  const int h = blockIdx.x;
-  const int i = threadIdx.x;
+  const int h = blockIdx.x * kRopeHeads + (threadIdx.x >> 6);
+  if (h >= num_heads) return;                  // whole wave
+  const int i = threadIdx.x & 63;
   const int hid = num_heads * 128;
   const int pos = pos0 + t;
   _Float16* q = reinterpret_cast<_Float16*>(qkv) + (long long)t * 3 * hid;
@@ -686,7 +690,8 @@ hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_
                                uint16_t* v_layer, const float2* rope_cs, long long row_stride,
                                long long head_stride, int pos0, int num_heads, int T,
                                hipStream_t stream) {
-  hipLaunchKernelGGL(rope_batched_kernel, dim3(num_heads, T), dim3(64), 0, stream, qkv, bias, k_layer,
+  hipLaunchKernelGGL(rope_batched_kernel, dim3((num_heads + kRopeHeads - 1) / kRopeHeads, T),
+                     dim3(kRopeHeads * 64), 0, stream, qkv, bias, k_layer,
                      v_layer, rope_cs, row_stride, head_stride, pos0, num_heads);
   return hipGetLastError();
 }
