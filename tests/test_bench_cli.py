@@ -1,6 +1,7 @@
-"""bench.py's command-line contract that needs no GPU: the build measures one
+"""bench.py's contract that needs no GPU: the build measures one
 GPU only, so any --gpus above 1 exits with status 2 and says so, before any
-GPU work; a non-zero rank (a launcher's extra processes) prints nothing."""
+GPU work; a non-zero rank (a launcher's extra processes) prints nothing; and
+the profile summaries its JSON line cites are committed."""
 import os
 import subprocess
 import sys
@@ -26,3 +27,14 @@ def test_non_zero_rank_prints_nothing():
     res = _bench("--gpus", "1", env=env)
     assert res.returncode == 0
     assert res.stdout == ""
+
+
+def test_profiles_cited_by_bench_exist():
+    """Every profiles/ summary bench.py cites in its JSON line is committed."""
+    import re
+    text = open(os.path.join(ROOT, "bench.py")).read()
+    cited = set(re.findall(r"profiles/[\w.\-]+\.(?:md|json|txt)", text))
+    cited |= {"profiles/" + m for m in re.findall(r'"profiles",\s*"([\w.\-]+)"', text)}
+    assert cited
+    for path in sorted(cited):
+        assert os.path.exists(os.path.join(ROOT, path)), path
