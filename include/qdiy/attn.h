@@ -140,6 +140,26 @@ int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
                               int num_heads, int head_dim, int num_splits,
                               hipStream_t stream);
 
+/* Allocation-free qd_decode_attention.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc), since
+ * qd_ctx_create allocates.  Same outputs, bit for bit, as qd_decode_attention
+ * with a context of these strides on the current device (same plan and
+ * kernels); the KV strides are passed here instead of through a qd_cfg.
+ * The split partials live in a static device array (520 KiB per GPU, held
+ * until the process ends) instead of context scratch, so the call makes no
+ * hipMalloc/hipFree and no other allocating call.  Limit: the plan's
+ * num_heads * splits partial slots must fit its 1024 slots, which every
+ * automatic plan does on devices of up to 512 compute units at any head
+ * count up to 1024 (QD_EINVAL otherwise).  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (two streams, two threads) race;
+ * order them on one stream.  Requirements on the pointers and strides are
+ * qd_decode_attention's; seqlen * kv_row_stride * 2 must stay below 4 GiB. */
+int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer,
+                                const uint16_t* v_layer, uint16_t* out, int seqlen,
+                                int num_heads, int head_dim, long long kv_row_stride,
+                                long long kv_head_stride, hipStream_t stream);
+
 /* Launch plan qd_decode_attention would use for seqlen: *variant is 0 for
  * fused, 1 for split; *num_splits the split count (1 for fused). */
 int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* num_splits);

@@ -44,10 +44,54 @@
 //     workgroup on gfx950 (buffer_wbl2 sc1, measured ~1 us each and
 //     serialised per XCD), far more than a second launch.
 //   * No MFMA: at q=1 the work is a bandwidth-bound GEMV-like reduction.
+#include <atomic>
+#include <mutex>
+
 #include "qd_device.h"
 #include "qd_internal.h"
 
 namespace qd {
+
+// Split partials of qd_decode_attention_noalloc: a static device array, so
+// that entry point allocates nothing.  Every GPU the library runs on holds its
+// own copy until the process ends, and every call on a GPU shares it, so calls
+// that overlap on one GPU (e.g. on two streams) race.  Nothing in it must
+// start at zero: each scan workgroup writes its whole slot before the merge
+// kernel reads it.  In host code the name `scratch` is a host-side stand-in,
+// not a device address; host code uses only the per-device address that
+// static_scratch() looks up.
+static __device__ __align__(256) float scratch[kStaticScratchSlots * (128 + 2)];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+}  // namespace
+
+int static_scratch(float** part_o, float2** part_ml) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(QD_EINVAL, "device %d above the static scratch's %d devices", dev, kMaxDevices);
+  float* base = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!base) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    base = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!base) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));   // this device's copy
+      if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+      if (!addr) return fail(QD_EHIP, "hipGetSymbolAddress(scratch) returned NULL");
+      base = static_cast<float*>(addr);
+      g_scratch_addr[dev].store(base, std::memory_order_release);
+    }
+  }
+  *part_o = base;
+  *part_ml = reinterpret_cast<float2*>(base + (size_t)kStaticScratchSlots * 128);
+  return QD_OK;
+}
+
 namespace {
 
 constexpr int kD = 128;

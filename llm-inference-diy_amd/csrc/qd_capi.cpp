@@ -60,10 +60,10 @@ qd::AttnPlan plan_fused(int seqlen) {
   return plan;
 }
 
-qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
+qd::AttnPlan plan_split(int num_cus, int num_heads, int seqlen, int requested) {
   int splits, rows;
   if (requested <= 0) {
-    qd::auto_split(seqlen, ctx->num_cus, ctx->cfg.num_heads, &splits, &rows);
+    qd::auto_split(seqlen, num_cus, num_heads, &splits, &rows);
   } else {
     splits = std::min(requested, qd::kMaxSplits);
     rows = (seqlen + splits - 1) / splits;
@@ -79,8 +79,16 @@ qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
   return plan;
 }
 
+qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
+  return plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, requested);
+}
+
+qd::AttnPlan plan_auto(int num_cus, int num_heads, int seqlen) {
+  return seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(num_cus, num_heads, seqlen, 0);
+}
+
 qd::AttnPlan plan_auto(const qd_ctx* ctx, int seqlen) {
-  return seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(ctx, seqlen, 0);
+  return plan_auto(ctx->num_cus, ctx->cfg.num_heads, seqlen);
 }
 
 
@@ -448,6 +456,67 @@ int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
     return fail(QD_EINVAL, "num_splits %d above the maximum %d", num_splits, qd::kMaxSplits);
   return run_attention(ctx, q, k_layer, v_layer, out, seqlen,
                        plan_split(ctx, seqlen, num_splits), stream);
+}
+
+int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, const uint16_t* v_layer,
+                                uint16_t* out, int seqlen, int num_heads, int head_dim,
+                                long long kv_row_stride, long long kv_head_stride,
+                                hipStream_t stream) {
+  if (!q || !k_layer || !v_layer || !out)
+    return fail(QD_EINVAL, "q, k_layer, v_layer and out must be non-NULL");
+  if (!aligned16(q) || !aligned16(k_layer) || !aligned16(v_layer) || !aligned16(out))
+    return fail(QD_EINVAL, "q, k_layer, v_layer and out must be 16-byte aligned");
+  if (head_dim != QD_HEAD_DIM) return fail(QD_EINVAL, "head_dim %d unsupported (must be %d)", head_dim, QD_HEAD_DIM);
+  if (num_heads < 1 || num_heads > 4096) return fail(QD_EINVAL, "num_heads %d outside [1, 4096]", num_heads);
+  if (kv_row_stride < 1 || kv_head_stride < 1 || (kv_row_stride % 8) || (kv_head_stride % 8))
+    return fail(QD_EINVAL, "kv strides must be positive multiples of 8 elements");
+  if (seqlen < 1) return fail(QD_EINVAL, "seqlen %d must be >= 1", seqlen);
+  // the kernels address a row as (32-bit byte offset) from a per-head base
+  if ((long long)seqlen * kv_row_stride * 2 > 0xFFFFFF00LL)
+    return fail(QD_EINVAL, "seqlen * kv_row_stride * 2 bytes must stay below 4 GiB");
+  const size_t ob = (size_t)num_heads * QD_HEAD_DIM * 2;
+  const size_t kvb = ((size_t)(seqlen - 1) * kv_row_stride + (size_t)(num_heads - 1) * kv_head_stride +
+                      QD_HEAD_DIM) * 2;
+  if (qd::overlaps(out, ob, k_layer, kvb) || qd::overlaps(out, ob, v_layer, kvb))
+    return fail(QD_EINVAL, "out overlaps the k_layer or v_layer rows being read");
+  int dev = -1, num_cus = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  e = hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess || num_cus < 1) return hip_fail(e, "hipDeviceGetAttribute(multiProcessorCount)");
+  // the plan qd_decode_attention picks for a context of this device and head count
+  const qd::AttnPlan plan = plan_auto(num_cus, num_heads, seqlen);
+  const long long slots = (long long)num_heads * plan.splits;
+  if (plan.variant == 1 && slots > qd::kStaticScratchSlots)
+    return fail(QD_EINVAL,
+                "%d heads x %d splits = %lld partial slots exceed the static scratch's %d "
+                "(use qd_decode_attention with a context)",
+                num_heads, plan.splits, slots, qd::kStaticScratchSlots);
+  qd::AttnParams p;
+  p.q = q;
+  p.k = k_layer;
+  p.v = v_layer;
+  p.out = out;
+  p.part_o = nullptr;
+  p.part_ml = nullptr;
+  if (plan.variant == 1) {
+    const int rc = qd::static_scratch(&p.part_o, &p.part_ml);
+    if (rc != QD_OK) return rc;
+  }
+  p.row_stride = kv_row_stride;
+  p.head_stride = kv_head_stride;
+  p.seqlen = seqlen;
+  p.num_heads = num_heads;
+  p.splits = plan.splits;
+  p.rows_per_split = plan.rows_per_split;
+  p.scale_log2 = (float)(1.4426950408889634 / std::sqrt(128.0));  // log2(e)/sqrt(128)
+  p.q_batch_stride = 0;
+  p.out_batch_stride = 0;
+  p.num_cus = num_cus;
+  p.split_stride = plan.splits;
+  e = qd::launch_decode_attention(p, plan, stream);
+  if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+  return QD_OK;
 }
 
 int qd_prefill_attention(qd_ctx* ctx, const uint16_t* q, long long q_stride, const uint16_t* k_layer,

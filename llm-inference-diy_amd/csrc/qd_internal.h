@@ -13,6 +13,17 @@ namespace qd {
 // num_heads * kMaxSplits * (128 + 2) floats (2.1 MB at 16 heads).
 constexpr int kMaxSplits = 256;
 
+// Partial slots (num_heads * splits) of the allocation-free entry point's
+// static device scratch: 1024 * (128 + 2) floats = 520 KiB per GPU, enough for
+// every automatic split plan on devices of up to 512 compute units.
+constexpr int kStaticScratchSlots = 1024;
+
+// The calling thread's current device's copy of the static scratch, as device
+// addresses: O partials [kStaticScratchSlots][128], then the (m, l) pairs.
+// The address is looked up with hipGetSymbolAddress on the first call per
+// device and kept.  Returns a QD_* status (message via fail()).
+int static_scratch(float** part_o, float2** part_ml);
+
 // Split planner constants, from measured sweeps on MI355X (16 heads, cold KV):
 // one split workgroup per CU in total, two per CU between kTwoPerCuMin and
 // kTwoPerCuMax rows (8.1 vs 8.5 us at 2048), each split at least

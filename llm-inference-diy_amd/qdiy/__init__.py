@@ -29,7 +29,7 @@ EXPORTS = (
     "qd_ctx_create", "qd_ctx_destroy", "qd_qkv_bias_rope_cache", "qd_qkv_proj_rope_cache",
     "qd_decode_attention",
     "qd_decode_attention_fused", "qd_decode_attention_split", "qd_decode_attention_plan",
-    "qd_decode_attention_plan_detail",
+    "qd_decode_attention_plan_detail", "qd_decode_attention_noalloc",
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
@@ -100,6 +100,7 @@ def load() -> ctypes.CDLL:
     L.qd_decode_attention.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     L.qd_decode_attention_fused.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     L.qd_decode_attention_split.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
+    L.qd_decode_attention_noalloc.argtypes = [vp, vp, vp, vp, i, i, i, ll, ll, vp]
     L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
     L.qd_decode_attention_plan_detail.argtypes = [vp, i, i, i, ctypes.POINTER(AttnPlan)]
     u16p = ctypes.POINTER(ctypes.c_uint16)
@@ -301,6 +302,27 @@ class Context:
                                              _ptr(qkv, "qkv"), _ptr(k_layer, "k_layer", False),
                                              _ptr(v_layer, "v_layer", False), pos, max_seqlen, H,
                                              HEAD_DIM, _stream(stream)))
+
+
+def decode_attention_noalloc(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
+                             out: torch.Tensor, seqlen: int, num_heads: int,
+                             kv_row_stride: int | None = None, kv_head_stride: int = HEAD_DIM,
+                             stream=None) -> torch.Tensor:
+    """qd_decode_attention_noalloc: Context.decode_attention without a context; the
+    split partials live in the library's static per-GPU scratch (no allocation)."""
+    row = num_heads * HEAD_DIM if kv_row_stride is None else kv_row_stride
+    if q.numel() < num_heads * HEAD_DIM or out.numel() < num_heads * HEAD_DIM:
+        raise ValueError("q and out need num_heads*128 elements")
+    if seqlen >= 1:
+        last = (seqlen - 1) * row + (num_heads - 1) * kv_head_stride + HEAD_DIM
+        for t, name in ((k_layer, "k_layer"), (v_layer, "v_layer")):
+            if t.numel() < last:
+                raise ValueError(f"{name} holds {t.numel()} elements; {seqlen} rows need {last}")
+    _check(load().qd_decode_attention_noalloc(_ptr(q, "q"), _ptr(k_layer, "k_layer", False),
+                                              _ptr(v_layer, "v_layer", False), _ptr(out, "out"),
+                                              seqlen, num_heads, HEAD_DIM, row, kv_head_stride,
+                                              _stream(stream)))
+    return out
 
 
 # ---------------------------------------------------------------- decode.h
