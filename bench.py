@@ -15,6 +15,21 @@ ascending order; each length allocates its own buffers.  achieved GB/s =
 algorithmic bytes per call / us per call with B(L) = 8192 + 8192*L (Q in,
 O out, K and V rows read once).
 
+Warm-up: before the first timed region of each length, at least --warmup calls
+and WARMUP_FLOOR_S of wall time of calls run, and the last ~2 ms of them are
+queued without a host synchronisation, so the first timed call follows busy
+GPU work.  (From an idle GPU, the first 20 calls ran ~8% slower per call than
+the steady state, which a 20-step window would report.)  The warm-up that ran
+is reported in config.warmup_run.
+
+roofline: the dominant kernel of the call, the split scan kernel, timed live
+between two HIP events on the call's stream over `steps` scan-only launches
+(qd_decode_attention_stage) on the same rotated layers; achieved = its
+algorithmic bytes (K and V rows and Q: 8192*L + 4096) / its mean duration per
+launch.  The merge kernel is timed the same way (config.merge_kernel_us).
+config.read_ceiling_us is a load-only kernel over the same layers in the
+scan's launch shape: what one kernel streaming those bytes takes on this box.
+
 The CPU baseline is the repository's C restatement of the reference kernels
 (oracle/) on the host cores of the same box, on a bounded sample of the same
 workload.
@@ -49,11 +64,21 @@ PEAK_GBPS = 8000.0
 KV_LENS = (512, 8192, 16384, 32768)
 HEADLINE_L = 8192
 METRIC = "decode-attention achieved HBM GB/s (% of peak) + µs/call at KV 512/8K/32K"
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_decode_attention_L8192.json")
+WARMUP_FLOOR_S = 0.1     # wall time of calls before the first timed region of a length
+WARMUP_TAIL_S = 0.002    # GPU time of calls queued, unsynchronised, right before a region
+
+
+def traffic_file(L: int) -> str:
+    """rocprofv3 FETCH_SIZE / WRITE_SIZE summary of one call at L (profiles/)."""
+    return os.path.join(ROOT, "profiles", f"traffic_decode_attention_L{L}.json")
 
 
 def algo_bytes(L: int) -> int:
     return 2 * H * D * 2 + 2 * H * L * D * 2     # Q + O, K + V
+
+
+def scan_bytes(L: int) -> int:
+    return H * D * 2 + 2 * H * L * D * 2         # Q, K + V: what the scan kernel must read
 
 
 def log(msg: str) -> None:
@@ -70,11 +95,39 @@ def bench_lib():
     lib = ctypes.CDLL(path)
     vp, i, ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
     lib.qd_bench_decode_attention.argtypes = [vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
+    lib.qd_bench_read_ceiling.argtypes = [vp, vp, ll, ll, i, i, i, vp, vp]
     lib.qd_bench_attn_front.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
     return lib
 
 
-def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int = 0):
+def warm_up(run, warmup: int, floor_s: float = WARMUP_FLOOR_S):
+    """Runs max(warmup, 1) calls, then host-synchronised chunks of ~10 ms until
+    floor_s of wall time has passed, then queues ~WARMUP_TAIL_S of calls without
+    synchronising: the caller records its first event behind them, so the GPU is
+    busy right up to the timed region.  Returns (calls run, wall ms)."""
+    import torch
+
+    t0 = time.perf_counter()
+    n = max(1, warmup)
+    run(n)
+    torch.cuda.synchronize()
+    per_call = (time.perf_counter() - t0) / n
+    while time.perf_counter() - t0 < floor_s:
+        chunk = max(1, int(0.01 / max(per_call, 1e-6)))
+        t1 = time.perf_counter()
+        run(chunk)
+        torch.cuda.synchronize()
+        per_call = (time.perf_counter() - t1) / chunk
+        n += chunk
+    tail = max(20, int(WARMUP_TAIL_S / max(per_call, 1e-6)))
+    run(tail)
+    return n + tail, (time.perf_counter() - t0) * 1e3
+
+
+def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int = 0,
+            detail: bool = False):
+    """us per call at L, cold (layers rotated) and hot (one layer).  detail: also the
+    scan kernel's own duration (events around it) and the read ceiling."""
     import torch
 
     import qdiy
@@ -101,35 +154,75 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
         if rc != 0:
             raise RuntimeError(f"bench loop failed: {qdiy.load().qd_last_error().decode()}")
 
-    def timed(iters, layers):
+    def timed(iters, fn):
+        # no host synchronisation before e0: it is recorded behind the warm-up tail
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
         e0.record(stream)
-        run(iters, layers)
+        fn(iters)
         e1.record(stream)
         e1.synchronize()
         return e0.elapsed_time(e1) * 1e3 / iters          # us per call
 
-    run(warmup, n_layers)
-    us_cold = timed(steps, n_layers)
-    run(warmup, 1)
-    us_hot = timed(steps, 1)
+    cold = lambda n: run(n, n_layers)
+    warm_calls, warm_ms = warm_up(cold, warmup)
+    us_cold = timed(steps, cold)
+    scan_us = merge_us = ceiling_us = None
+    tail = max(20, int(WARMUP_TAIL_S / (us_cold * 1e-6)))
+    if detail:
+        # the call's kernels on their own, back to back over the same layers
+        # (qd_decode_attention_stage): scan only, then merge only
+        def stage(kind):
+            def fn(n):
+                rc = lib.qd_bench_decode_attention(ctx._h, q.data_ptr(), kc.data_ptr(),
+                                                   vc.data_ptr(), out.data_ptr(), HID, L * HID,
+                                                   n_layers, L, H, n, kind, 0, sh)
+                if rc != 0:
+                    raise RuntimeError(f"stage loop failed: {qdiy.load().qd_last_error().decode()}")
+            return fn
+
+        stage(3)(tail)
+        scan_us = timed(steps, stage(3))
+        if ctx.plan_detail(L).variant == qdiy.SPLIT:
+            stage(4)(tail)
+            merge_us = timed(steps, stage(4))
+        # load-only kernel over the same layers' K and V rows, same launch shape
+        sink = torch.empty(256 * 16, dtype=torch.uint8, device="cuda")
+
+        def read(n):
+            if lib.qd_bench_read_ceiling(kc.data_ptr(), vc.data_ptr(), L * HID * 2, L * HID * 2,
+                                         n_layers, 256, n, sink.data_ptr(), sh) != 0:
+                raise RuntimeError("read-ceiling launch failed")
+
+        read(tail)
+        ceiling_us = timed(steps, read)
+    hot = lambda n: run(n, 1)
+    warm_up(hot, warmup, floor_s=0.0)
+    us_hot = timed(steps, hot)
     if not torch.isfinite(out).all():
         raise RuntimeError("non-finite attention output")
-    if variant == 1:
-        plan = ("fused", 1)
-    else:
-        d = ctx.plan_detail(L, "split" if variant == 2 else "auto", splits)
-        plan = ("fused" if d.variant == qdiy.FUSED else "split", d.num_splits)
+    d = ctx.plan_detail(L, {0: "auto", 1: "fused", 2: "split"}[variant], splits)
+    plan = ("fused" if d.variant == qdiy.FUSED else "split", d.num_splits)
+    kernel = (f"decode_attention_scan_kernel<{d.waves}, {d.rows_per_tile}, "
+              f"{'false' if d.variant == qdiy.FUSED else 'true'}, false>")
     ctx.close()
     del kc, vc
     torch.cuda.empty_cache()
     gbps = algo_bytes(L) / (us_cold * 1e-6) / 1e9
     res = {"L": L, "us_cold": us_cold, "us_hot": us_hot, "gbps": gbps,
            "gbps_hot": algo_bytes(L) / (us_hot * 1e-6) / 1e9, "frac": gbps / PEAK_GBPS,
-           "layers": n_layers, "plan": f"{plan[0]}x{plan[1]}"}
+           "layers": n_layers, "plan": f"{plan[0]}x{plan[1]}", "kernel": kernel,
+           "warmup_calls": warm_calls, "warmup_ms": round(warm_ms, 1),
+           "scan_us": scan_us, "merge_us": merge_us, "read_ceiling_us": ceiling_us}
+    extra = ""
+    if detail:
+        res["scan_gbps"] = scan_bytes(L) / (scan_us * 1e-6) / 1e9
+        res["ceiling_gbps"] = 2 * L * HID * 2 / (ceiling_us * 1e-6) / 1e9
+        extra = (f"; alone: scan kernel {scan_us:.2f} us ({res['scan_gbps']:.0f} GB/s), merge "
+                 f"kernel {merge_us if merge_us is None else round(merge_us, 2)} us; read ceiling "
+                 f"{ceiling_us:.2f} us ({res['ceiling_gbps']:.0f} GB/s)")
     log(f"[bench] L={L}: {us_cold:.2f} us/call cold ({gbps:.0f} GB/s, {100 * gbps / PEAK_GBPS:.1f}% "
-        f"of 8 TB/s), {us_hot:.2f} us hot, plan {res['plan']}, {n_layers} layers rotated")
+        f"of 8 TB/s), {us_hot:.2f} us hot, plan {res['plan']}, {n_layers} layers rotated, "
+        f"warm-up {warm_calls} calls / {warm_ms:.0f} ms{extra}")
     return res
 
 
@@ -165,18 +258,17 @@ def measure_front(lib, steps: int, warmup: int):
         if rc != 0:
             raise RuntimeError(f"front-end bench failed: {qdiy.load().qd_last_error().decode()}")
 
-    def timed(iters, with_attn):
-        run(warmup, with_attn)
+    def timed(iters, with_attn, floor_s):
+        warm_up(lambda n: run(n, with_attn), warmup, floor_s)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
         e0.record(stream)
         run(iters, with_attn)
         e1.record(stream)
         e1.synchronize()
         return e0.elapsed_time(e1) * 1e3 / iters
 
-    us_front = timed(steps, 0)
-    us_all = timed(steps, 1)
+    us_front = timed(steps, 0, WARMUP_FLOOR_S)
+    us_all = timed(steps, 1, 0.0)
     ctx.close()
     del w, kc, vc
     torch.cuda.empty_cache()
@@ -351,18 +443,24 @@ def main() -> int:
     # an earlier phase freed its own can land on physical pages that run the same
     # calls up to ~3% slower (15.45 against 14.97-15.05 us per call at L=8192).
     order = [HEADLINE_L] + [L for L in kv if L != HEADLINE_L]
-    measured = {L: measure(lib, L, args.steps, args.warmup, variant, args.splits) for L in order}
+    detail = variant == 0
+    measured = {L: measure(lib, L, args.steps, args.warmup, variant, args.splits, detail)
+                for L in order}
     res = {L: measured[L] for L in kv}
     head = res[HEADLINE_L]
     # config 1 names the fused single-workgroup-per-head path at L=512
     fused512 = measure(lib, 512, args.steps, args.warmup, 1, 0) if 512 in kv and variant == 0 else None
     front = None if args.no_front else measure_front(lib, args.steps, args.warmup)
     e2e = None if args.no_e2e else measure_e2e(lib)
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("traffic_bytes_per_launch")
+    # counter evidence per length (profiles/traffic_decode_attention_L*.json)
+    traffic = {}
+    for L in kv:
+        if os.path.exists(traffic_file(L)):
+            with open(traffic_file(L)) as f:
+                traffic[L] = json.load(f)
     cpu = None if args.no_cpu else cpu_baseline(HEADLINE_L, args.cpu_seconds)
+    per_l = lambda key, nd=3: {str(L): (None if r.get(key) is None else round(r[key], nd))
+                               for L, r in res.items()}
     line = {
         "metric": METRIC,
         "value": round(head["gbps"], 1),
@@ -374,7 +472,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "fp16",
         "data": "synthetic",
         "config": {
             "workload": f"decode_attention_L{HEADLINE_L}",
@@ -383,22 +481,37 @@ def main() -> int:
             "cache_layout": "[pos][16*128] (reference engine layout)",
             "cache": "cold: each step reads a different layer; >= 1 GiB rotated; "
                      f"L={HEADLINE_L} measured first, in the process's first KV buffers",
+            "warmup_run": {"floor_ms": WARMUP_FLOOR_S * 1e3,
+                           "calls": {str(L): r["warmup_calls"] for L, r in res.items()},
+                           "ms": {str(L): r["warmup_ms"] for L, r in res.items()}},
             "plan": head["plan"],
-            "us_per_call": {str(L): round(r["us_cold"], 3) for L, r in res.items()},
-            "gbps": {str(L): round(r["gbps"], 1) for L, r in res.items()},
+            "us_per_call": per_l("us_cold"),
+            "gbps": per_l("gbps", 1),
             "pct_of_peak": {str(L): round(100 * r["frac"], 1) for L, r in res.items()},
-            "us_per_call_hot": {str(L): round(r["us_hot"], 3) for L, r in res.items()},
+            "us_per_call_hot": per_l("us_hot"),
             "plans": {str(L): r["plan"] for L, r in res.items()},
+            "scan_kernel_us": per_l("scan_us"),
+            "scan_kernel_gbps": per_l("scan_gbps", 1),
+            "merge_kernel_us": per_l("merge_us"),
+            "read_ceiling_us": per_l("read_ceiling_us"),
+            "read_ceiling_gbps": per_l("ceiling_gbps", 1),
+            "traffic_over_algorithmic": {str(L): t.get("traffic_over_algorithmic")
+                                         for L, t in traffic.items()},
             "fused_path_us_per_call_512": None if fused512 is None else round(fused512["us_cold"], 3),
             "config4_front_end": front,
             "config5_e2e": e2e,
         },
-        "roofline": {"bound": "hbm",
-                     "kernel": f"qd_decode_attention call ({head['plan']}: "
-                               "decode_attention_scan_kernel + decode_attention_merge_kernel)",
-                     "achieved": round(head["gbps"], 1), "peak": PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(head["frac"], 4), "traffic": traffic,
-                     "per_kernel_trace": "profiles/decode_attention_kernel_trace_L512_to_L32768.md"},
+        "roofline": None if not detail else {
+            "bound": "hbm",
+            "kernel": f"{head['kernel']} (the scan of qd_decode_attention at L={HEADLINE_L}, "
+                      f"{head['plan']})",
+            "achieved": round(head["scan_gbps"], 1), "peak": PEAK_GBPS, "unit": "GB/s",
+            "frac": round(head["scan_gbps"] / PEAK_GBPS, 4),
+            "traffic": traffic.get(HEADLINE_L, {}).get("scan_kernel_traffic_bytes"),
+            "algorithmic_bytes_per_launch": scan_bytes(HEADLINE_L),
+            "launch_us": round(head["scan_us"], 3),
+            "call_frac": round(head["frac"], 4),
+            "per_kernel_trace": "profiles/decode_attention_kernel_trace_L512_to_L32768.md"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -49,8 +49,8 @@ def _run(cmd, verbose):
 
 
 def build(verbose: bool = False) -> str:
-    """Builds libqdiy.so (kernels + C ABI), libqdiy_bench.so (bench loop) and the
-    qdiy_engine executable (stdin/stdout protocol)."""
+    """Builds libqdiy.so (kernels + C ABI), libqdiy_bench.so (bench loops and the
+    read-ceiling kernel) and the qdiy_engine executable (stdin/stdout protocol)."""
     os.makedirs(LIB_DIR, exist_ok=True)
     tmp = LIB + ".tmp"
     _run([hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
@@ -58,9 +58,10 @@ def build(verbose: bool = False) -> str:
           "-Wl,-soname,libqdiy.so", "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]], verbose)
     os.replace(tmp, LIB)
     tmp = BENCH_LIB + ".tmp"
-    _run([hipcc(), "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-I", INCLUDE,
-          "-o", tmp, os.path.join(CSRC, "qd_bench.cpp"), "-L", LIB_DIR, "-lqdiy",
-          "-Wl,-rpath,$ORIGIN"], verbose)
+    _run([hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+          *DEVICE_FLAGS, "-I", INCLUDE, "-o", tmp, os.path.join(CSRC, "qd_bench.cpp"),
+          os.path.join(CSRC, "qd_bench_read.hip"), "-L", LIB_DIR, "-lqdiy", "-Wl,-rpath,$ORIGIN"],
+         verbose)
     os.replace(tmp, BENCH_LIB)
     tmp = ENGINE_EXE + ".tmp"
     _run([hipcc(), "-O2", "-std=c++17", "-Wall", "-I", INCLUDE, "-o", tmp,

@@ -451,20 +451,24 @@ hipError_t launch_decode_attention_split_batch(const AttnParams& p, int rows_per
   return hipGetLastError();
 }
 
-hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream) {
+hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream,
+                                   int stages) {
   if (plan.variant == 0) {
-    launch_scan<16, false>(p, plan.rows_per_tile, dim3(p.num_heads), stream);
+    if (stages & kStageScan) launch_scan<16, false>(p, plan.rows_per_tile, dim3(p.num_heads), stream);
     return hipGetLastError();
   }
-  const dim3 grid(p.num_heads * p.splits);
-  switch (plan.waves) {
-    case 16: launch_scan<16, true>(p, plan.rows_per_tile, grid, stream); break;
-    case 8: launch_scan<8, true>(p, plan.rows_per_tile, grid, stream); break;
-    default: launch_scan<4, true>(p, plan.rows_per_tile, grid, stream); break;
+  if (stages & kStageScan) {
+    const dim3 grid(p.num_heads * p.splits);
+    switch (plan.waves) {
+      case 16: launch_scan<16, true>(p, plan.rows_per_tile, grid, stream); break;
+      case 8: launch_scan<8, true>(p, plan.rows_per_tile, grid, stream); break;
+      default: launch_scan<4, true>(p, plan.rows_per_tile, grid, stream); break;
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(decode_attention_merge_kernel<256>, dim3(p.num_heads), dim3(256), 0, stream, p);
+  if (stages & kStageMerge)
+    hipLaunchKernelGGL(decode_attention_merge_kernel<256>, dim3(p.num_heads), dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -8,11 +8,13 @@
 // on the same stream; this function never synchronises.
 #include <cstdint>
 
-#include "qdiy/attn.h"
+#include "qdiy/bench.h"
 
 extern "C" {
 
-// variant: 0 auto (qd_decode_attention), 1 fused, 2 split with num_splits.
+// variant: 0 auto (qd_decode_attention), 1 fused, 2 split with num_splits,
+// 3 the scan kernel of qd_decode_attention only, 4 its merge kernel only
+// (qd_decode_attention_stage).
 int qd_bench_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k,
                               const uint16_t* v, uint16_t* out, long long q_layer_stride,
                               long long kv_layer_stride, int n_layers, int seqlen, int num_heads,
@@ -30,6 +32,9 @@ int qd_bench_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k,
     else if (variant == 2)
       rc = qd_decode_attention_split(ctx, ql, kl, vl, ol, seqlen, num_heads, QD_HEAD_DIM,
                                      num_splits, stream);
+    else if (variant == 3 || variant == 4)
+      rc = qd_decode_attention_stage(ctx, ql, kl, vl, ol, seqlen, num_heads, QD_HEAD_DIM,
+                                     variant == 3 ? QD_STAGE_SCAN : QD_STAGE_MERGE, stream);
     else
       rc = qd_decode_attention(ctx, ql, kl, vl, ol, seqlen, num_heads, QD_HEAD_DIM, stream);
     if (rc != QD_OK) return rc;

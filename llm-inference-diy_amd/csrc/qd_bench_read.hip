@@ -1,0 +1,73 @@
+// Read ceiling of the decode-attention workload (libqdiy_bench.so): a kernel
+// that only reads what a qd_decode_attention call must read -- one layer's K
+// and V rows -- in the same launch shape as the split scan (256 workgroups of
+// 256 threads at 16 heads on 256 CUs), with the same 16-byte non-temporal
+// loads, rotating over the same layers.  It does no arithmetic beyond an XOR
+// fold, so its time per launch is what the box gives one kernel streaming
+// those bytes: the ceiling the attention call is measured against.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Workgroup w reads units [w * per_wg, (w + 1) * per_wg) of 16 bytes of K and
+// of V; each thread keeps U units of each in flight, all issued before any is
+// folded.  The fold feeds a store that never happens for real data (the
+// sentinel would need an exact 128-bit XOR match), so no load is dead code.
+template <int U>
+__global__ __launch_bounds__(256) void read_ceiling_kernel(const u32x4* __restrict__ k,
+                                                           const u32x4* __restrict__ v,
+                                                           unsigned per_wg, u32x4* sink) {
+  const size_t base = (size_t)blockIdx.x * per_wg;
+  const u32x4* kb = k + base;
+  const u32x4* vb = v + base;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (unsigned i = threadIdx.x; i < per_wg; i += 256u * U) {
+    u32x4 a[U], b[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const unsigned j = min(i + 256u * u, per_wg - 1u);
+      a[u] = __builtin_nontemporal_load(kb + j);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const unsigned j = min(i + 256u * u, per_wg - 1u);
+      b[u] = __builtin_nontemporal_load(vb + j);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
+  }
+  if (acc.x == 0x9E3779B9u && acc.y == 0x7F4A7C15u && acc.z == 0x85EBCA6Bu && acc.w == 0xC2B2AE35u)
+    sink[blockIdx.x] = acc;
+}
+
+}  // namespace
+
+extern "C" {
+
+// `iters` launches, launch i reading layer i % n_layers: `bytes` of K at
+// k + layer * layer_stride_bytes and the same of V.  bytes must be a multiple
+// of 16 * grid; sink holds grid 16-byte slots.  Asynchronous on `stream`.
+int qd_bench_read_ceiling(const void* k, const void* v, long long layer_stride_bytes,
+                          long long bytes, int n_layers, int grid, int iters, void* sink,
+                          hipStream_t stream) {
+  if (!k || !v || !sink || n_layers < 1 || grid < 1 || iters < 0 || bytes <= 0 ||
+      bytes % (16LL * grid) != 0 || bytes / 16 / grid > 0xFFFFFFFFLL)
+    return 1;
+  const unsigned per_wg = (unsigned)(bytes / 16 / grid);
+  for (int it = 0; it < iters; ++it) {
+    const long long off = (long long)(it % n_layers) * layer_stride_bytes;
+    hipLaunchKernelGGL(read_ceiling_kernel<4>, dim3(grid), dim3(256), 0, stream,
+                       reinterpret_cast<const u32x4*>(static_cast<const char*>(k) + off),
+                       reinterpret_cast<const u32x4*>(static_cast<const char*>(v) + off), per_wg,
+                       static_cast<u32x4*>(sink));
+    if (hipGetLastError() != hipSuccess) return 2;
+  }
+  return 0;
+}
+
+}  // extern "C"

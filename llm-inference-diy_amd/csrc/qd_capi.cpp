@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "qd_internal.h"
+#include "qdiy/bench.h"
 #include "qdiy/decode.h"
 
 namespace {
@@ -142,10 +143,10 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
 }
 
 int run_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                  uint16_t* out, int seqlen, const qd::AttnPlan& plan_in, hipStream_t stream) {
-  const qd::AttnPlan& plan = plan_in;
+                  uint16_t* out, int seqlen, const qd::AttnPlan& plan, hipStream_t stream,
+                  int stages = qd::kStageScan | qd::kStageMerge) {
   const qd::AttnParams p = make_params(ctx, q, k, v, out, seqlen, plan);
-  hipError_t e = qd::launch_decode_attention(p, plan, stream);
+  hipError_t e = qd::launch_decode_attention(p, plan, stream, stages);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return QD_OK;
 }
@@ -437,6 +438,17 @@ int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
   const qd::AttnPlan plan =
       plan_auto(ctx, seqlen);
   return run_attention(ctx, q, k_layer, v_layer, out, seqlen, plan, stream);
+}
+
+int qd_decode_attention_stage(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
+                              const uint16_t* v_layer, uint16_t* out, int seqlen, int num_heads,
+                              int head_dim, int stages, hipStream_t stream) {
+  int rc = check_attention_args(ctx, q, k_layer, v_layer, out, seqlen, num_heads, head_dim);
+  if (rc != QD_OK) return rc;
+  if (stages < 1 || stages > (QD_STAGE_SCAN | QD_STAGE_MERGE))
+    return fail(QD_EINVAL, "stages %d is not a non-empty set of QD_STAGE_SCAN, QD_STAGE_MERGE", stages);
+  return run_attention(ctx, q, k_layer, v_layer, out, seqlen, plan_auto(ctx, seqlen), stream,
+                       stages);
 }
 
 int qd_decode_attention_fused(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,

@@ -220,7 +220,12 @@ inline bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
   return x < y + nb && y < x + na;
 }
 
-hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream);
+// stages: kStageScan launches the scan kernel (the only kernel of a fused
+// plan), kStageMerge the merge kernel of a split plan; a call is both.
+constexpr int kStageScan = 1;
+constexpr int kStageMerge = 2;
+hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream,
+                                   int stages = kStageScan | kStageMerge);
 // Fused (one 16-wave workgroup per head, 4-row tiles) attention of `tokens`
 // queries at once, token b over p.seqlen + b rows: the arithmetic of the fused
 // plan of qd_decode_attention, query by query.

@@ -30,6 +30,8 @@ EXPORTS = (
     "qd_decode_attention",
     "qd_decode_attention_fused", "qd_decode_attention_split", "qd_decode_attention_plan",
     "qd_decode_attention_plan_detail", "qd_decode_attention_noalloc",
+    # qdiy/bench.h
+    "qd_decode_attention_stage",
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
@@ -101,6 +103,7 @@ def load() -> ctypes.CDLL:
     L.qd_decode_attention_fused.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     L.qd_decode_attention_split.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
     L.qd_decode_attention_noalloc.argtypes = [vp, vp, vp, vp, i, i, i, ll, ll, vp]
+    L.qd_decode_attention_stage.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
     L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
     L.qd_decode_attention_plan_detail.argtypes = [vp, i, i, i, ctypes.POINTER(AttnPlan)]
     u16p = ctypes.POINTER(ctypes.c_uint16)

@@ -8,7 +8,7 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = [os.path.join(ROOT, "include", "qdiy", h) for h in ("attn.h", "decode.h", "engine.h")]
+HEADERS = [os.path.join(ROOT, "include", "qdiy", h) for h in ("attn.h", "decode.h", "engine.h", "bench.h")]
 
 
 def _declared():
