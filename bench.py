@@ -182,7 +182,8 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
 
         stage(3)(tail)
         scan_us = timed(steps, stage(3))
-        if ctx.plan_detail(L).variant == qdiy.SPLIT:
+        pd = ctx.plan_detail(L)
+        if pd.variant == qdiy.SPLIT and not pd.merge_in_kernel:
             stage(4)(tail)
             merge_us = timed(steps, stage(4))
         # load-only kernel over the same layers' K and V rows, same launch shape
@@ -201,8 +202,10 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     if not torch.isfinite(out).all():
         raise RuntimeError("non-finite attention output")
     d = ctx.plan_detail(L, {0: "auto", 1: "fused", 2: "split"}[variant], splits)
-    plan = ("fused" if d.variant == qdiy.FUSED else "split", d.num_splits)
-    kernel = (f"decode_attention_scan_kernel<{d.waves}, {d.rows_per_tile}, "
+    plan = ("fused" if d.variant == qdiy.FUSED else
+            "split+merge-in-kernel" if d.merge_in_kernel else "split", d.num_splits)
+    kernel = (f"decode_attention_xmerge_kernel<{d.rows_per_tile}>" if d.merge_in_kernel else
+              f"decode_attention_scan_kernel<{d.waves}, {d.rows_per_tile}, "
               f"{'false' if d.variant == qdiy.FUSED else 'true'}, false>")
     ctx.close()
     del kc, vc
@@ -503,8 +506,8 @@ def main() -> int:
         },
         "roofline": None if not detail else {
             "bound": "hbm",
-            "kernel": f"{head['kernel']} (the scan of qd_decode_attention at L={HEADLINE_L}, "
-                      f"{head['plan']})",
+            "kernel": f"{head['kernel']} (the scan kernel of qd_decode_attention at "
+                      f"L={HEADLINE_L}, plan {head['plan']})",
             "achieved": round(head["scan_gbps"], 1), "peak": PEAK_GBPS, "unit": "GB/s",
             "frac": round(head["scan_gbps"] / PEAK_GBPS, 4),
             "traffic": traffic.get(HEADLINE_L, {}).get("scan_kernel_traffic_bytes"),

@@ -171,6 +171,9 @@ typedef struct qd_attn_plan {
   int rows_per_split; /* KV rows each workgroup scans (seqlen when fused) */
   int rows_per_tile;  /* rows each 16-lane group loads per tile */
   int waves;          /* wavefronts per scan workgroup */
+  int merge_in_kernel;/* split plans: 1 if the last split workgroup of each head
+                         merges inside the scan kernel (one launch), 0 if a
+                         merge kernel follows (two launches); same bits */
 } qd_attn_plan;
 
 /* Plan of the call selected by `entry` (0: qd_decode_attention,

@@ -28,6 +28,36 @@ int qd_decode_attention_stage(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
                               const uint16_t* v_layer, uint16_t* out, int seqlen,
                               int num_heads, int head_dim, int stages, hipStream_t stream);
 
+#define QD_MERGE_AUTO 0           /* in the scan kernel where it measured faster */
+#define QD_MERGE_TWO_LAUNCHES 1   /* always a separate merge kernel */
+#define QD_MERGE_IN_KERNEL 2      /* in the scan kernel wherever the context can */
+
+/* How the context's split plans merge their partials (QD_MERGE_*); every mode
+ * gives the same bits.  The scan kernel can fold them itself when the context
+ * found round-robin workgroup dispatch whose period divides num_heads
+ * (qd_ctx_xcd_period) and the grid is at most one workgroup per CU;
+ * QD_MERGE_AUTO (the default) does so up to 2048 rows, where it measured
+ * faster, and runs split plans with a merge kernel beyond.  A context that
+ * merges in the kernel also runs fused plans only up to 128 rows (224
+ * otherwise).  The other modes exist for A/B timing and tests. */
+int qd_ctx_set_merge(qd_ctx* ctx, int mode);
+
+/* Test hook of the in-kernel merge: the merging workgroup treats the partials
+ * of every split whose index mod 32 is set in `mask` as not visible to it and
+ * scans those splits again itself, as it does for partials written on another
+ * XCD.  0 (the default) turns it off.  Outputs are unchanged either way. */
+int qd_ctx_set_recompute_mask(qd_ctx* ctx, unsigned mask);
+
+/* Round-robin period of workgroup dispatch over XCDs found at context
+ * creation (8 on MI355X: workgroup i runs on XCD i mod 8), 1 if every
+ * workgroup ran on one XCD, 0 if the placement was not round-robin. */
+int qd_ctx_xcd_period(const qd_ctx* ctx, int* period);
+
+/* The XCD (HW_REG_XCC_ID) each workgroup of one `count`-workgroup launch on
+ * the current device ran on, into host array xcc[count].  Synchronous;
+ * allocates a count-word device buffer.  The probe qd_ctx_create runs. */
+int qd_xcd_placement(unsigned* xcc, int count);
+
 #ifdef __cplusplus
 }
 #endif

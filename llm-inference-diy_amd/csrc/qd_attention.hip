@@ -264,16 +264,65 @@ __device__ __forceinline__ void wave_merge(GroupState& st) {
 // workgroups past its split count exit, and its partials go to slots
 // (b * num_heads + h) * split_stride + c; every workgroup that runs does
 // exactly the work of the same workgroup of that query's single call.
-template <int NW, int U, bool kSplit, bool kBatch = false>
-__global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnParams p) {
-  __shared__ float so[NW][kD];
-  __shared__ float sm[NW];
-  __shared__ float sl[NW];
+// LDS of one workgroup's fold of its NW wave states.
+template <int NW>
+struct ScanLds {
+  float so[NW][kD];
+  float sm[NW];
+  float sl[NW];
+};
+
+// Scan rows [r0, r0 + nrows) of head h for query row q (the whole workgroup,
+// NW waves), fold each wave's four groups with lane shuffles and the NW wave
+// states in LDS, max-first: for tid < 128, (M, L, O) is the workgroup's
+// partial for dim tid (M and L the same in every thread).  Ends with the LDS
+// reads of the fold; a caller that reuses `lds` synchronises first.
+template <int NW, int U>
+__device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q, int h, int r0,
+                                          int nrows, ScanLds<NW>& lds, float& M, float& L,
+                                          float& O) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
   const int g = lane >> 4;
   const int t = lane & 15;
+  const f16x8 qv = *reinterpret_cast<const f16x8*>(q + h * kD + t * 8);
+  const long long off = h * p.head_stride + (long long)r0 * p.row_stride;
+  GroupState st;
+  init_state(st);
+  scan_rows<NW, U>(st, reinterpret_cast<const char*>(p.k + off),
+                   reinterpret_cast<const char*>(p.v + off), (unsigned)(p.row_stride * 2), nrows,
+                   wave, g, t, qv, p.scale_log2);
+  wave_merge(st);
+  if (lane < 16) {
+    *reinterpret_cast<f32x4*>(&lds.so[wave][t * 8]) = f32x4{st.o[0], st.o[1], st.o[2], st.o[3]};
+    *reinterpret_cast<f32x4*>(&lds.so[wave][t * 8 + 4]) = f32x4{st.o[4], st.o[5], st.o[6], st.o[7]};
+    if (t == 0) {
+      lds.sm[wave] = st.m;
+      lds.sl[wave] = st.l;
+    }
+  }
+  __syncthreads();
+  M = -__builtin_inff();
+  L = 0.0f;
+  O = 0.0f;
+  if (tid < kD) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, lds.sm[w]);
+    const float base = safe_base(M);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = exp2_rep_nonpos(lds.sm[w] - base);
+      L = __builtin_fmaf(wt, lds.sl[w], L);
+      O = __builtin_fmaf(wt, lds.so[w][tid], O);
+    }
+  }
+}
+
+template <int NW, int U, bool kSplit, bool kBatch = false>
+__global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnParams p) {
+  __shared__ ScanLds<NW> lds;
+  const int tid = threadIdx.x;
   const int h = blockIdx.x % p.num_heads;
   const int c = blockIdx.x / p.num_heads;
   const int b = blockIdx.y;                   // query of a batched call, else 0
@@ -286,36 +335,9 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
   }
   const int r0 = c * rows_per_split;
   const int nrows = min(seqlen - r0, rows_per_split);
-
-  const f16x8 qv = *reinterpret_cast<const f16x8*>(p.q + b * p.q_batch_stride + h * kD + t * 8);
-  const long long off = h * p.head_stride + (long long)r0 * p.row_stride;
-  GroupState st;
-  init_state(st);
-  scan_rows<NW, U>(st, reinterpret_cast<const char*>(p.k + off),
-                   reinterpret_cast<const char*>(p.v + off), (unsigned)(p.row_stride * 2), nrows,
-                   wave, g, t, qv, p.scale_log2);
-  wave_merge(st);
-  if (lane < 16) {
-    *reinterpret_cast<f32x4*>(&so[wave][t * 8]) = f32x4{st.o[0], st.o[1], st.o[2], st.o[3]};
-    *reinterpret_cast<f32x4*>(&so[wave][t * 8 + 4]) = f32x4{st.o[4], st.o[5], st.o[6], st.o[7]};
-    if (t == 0) {
-      sm[wave] = st.m;
-      sl[wave] = st.l;
-    }
-  }
-  __syncthreads();
+  float M, L, O;
+  scan_fold<NW, U>(p, p.q + b * p.q_batch_stride, h, r0, nrows, lds, M, L, O);
   if (tid < kD) {
-    float M = -__builtin_inff();
-#pragma unroll
-    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm[w]);
-    const float base = safe_base(M);
-    float L = 0.0f, O = 0.0f;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) {
-      const float wt = exp2_rep_nonpos(sm[w] - base);
-      L = __builtin_fmaf(wt, sl[w], L);
-      O = __builtin_fmaf(wt, so[w][tid], O);
-    }
     if constexpr (kSplit) {
       const long long slot = kBatch ? ((long long)b * p.num_heads + h) * p.split_stride + c
                                     : (long long)h * splits + c;
@@ -338,49 +360,54 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
 // ascending order with fmaf, issuing B splits' loads at a time, and the P
 // slice sums are added in LDS (slice order).  The kernel boundary after
 // stage 1 makes every partial visible on every XCD.
-template <int NT, bool kBatch = false>
-__global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p) {
-  constexpr int P = NT / 32;
-  constexpr int B = 8;
-  __shared__ float so[P][kD];
-  __shared__ float sm[P];
-  __shared__ float sl[P];
+constexpr int kMergeThreads = 256;
+constexpr int kMergeSlices = kMergeThreads / 32;   // P
+constexpr int kMergeBatch = 8;                     // B: splits per thread per round trip
+
+struct MergeLds {
+  float so[kMergeSlices][kD];
+  float sm[kMergeSlices];
+  float sl[kMergeSlices];
+};
+
+// Partials of one head as the merge reads them: (m, l) of split c, and dims
+// 4dq..4dq+3 of its O.
+struct PlainPartials {
+  const float* po;     // + dq * 4 already applied
+  const float2* pml;
+  __device__ float2 ml(int c) const { return pml[c]; }
+  __device__ f32x4 o4(int c) const { return *reinterpret_cast<const f32x4*>(po + (long long)c * kD); }
+};
+
+// Log-sum-exp fold of one head's `splits` partials by kMergeThreads threads,
+// max-first: thread (dq = tid % 32 -> dims 4dq..4dq+3, slice = tid / 32) takes
+// splits slice, slice + P, ...; the slices' maxima meet in LDS, so all threads
+// share the head's maximum M before any exponential.  Each thread then sums
+// w_c * l_c and w_c * O_c (w_c = exp2(m_c - M)) over its splits in ascending
+// order with fmaf, B splits' loads at a time, and the P slice sums are added
+// in LDS (slice order); out_head[d] = half(O_d / L).  ml / ov hold the
+// thread's first batch (splits slice + j * P, clamped to splits - 1), loaded
+// by the caller before the maximum is known so that one memory round trip
+// serves both; src loads the splits beyond the first batch.
+template <class Src>
+__device__ __forceinline__ void merge_fold(float2 (&ml)[kMergeBatch], f32x4 (&ov)[kMergeBatch],
+                                           int splits, const Src& src, MergeLds& lds,
+                                           _Float16* out_head) {
+  constexpr int P = kMergeSlices;
+  constexpr int B = kMergeBatch;
   const int tid = threadIdx.x;
-  const int h = blockIdx.x;
   const int dq = tid & 31;
   const int slice = tid >> 5;
-  int splits = p.splits;
-  long long first = (long long)h * p.splits;  // this head's first partial slot
-  _Float16* out = reinterpret_cast<_Float16*>(p.out);
-  if constexpr (kBatch) {
-    const int b = blockIdx.y;
-    int rows;
-    auto_split(p.seqlen + b, p.num_cus, p.num_heads, &splits, &rows);
-    first = ((long long)b * p.num_heads + h) * p.split_stride;
-    out += b * p.out_batch_stride;
-  }
-  const float* po = p.part_o + first * kD + dq * 4;
-  const float2* pml = p.part_ml + first;
-  // First batch of this thread's splits (slice, slice + P, ..., B of them),
-  // loaded before the maximum is known so one memory round trip serves both.
-  float2 ml[B];
-  f32x4 ov[B];
-#pragma unroll
-  for (int j = 0; j < B; ++j) {
-    const int cc = min(slice + j * P, splits - 1);
-    ml[j] = pml[cc];
-    ov[j] = *reinterpret_cast<const f32x4*>(po + (long long)cc * kD);
-  }
   float mm = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < B; ++j)
     if (slice + j * P < splits) mm = fmaxf(mm, ml[j].x);
-  for (int c = slice + B * P; c < splits; c += P) mm = fmaxf(mm, pml[c].x);
-  if (dq == 0) sm[slice] = mm;
+  for (int c = slice + B * P; c < splits; c += P) mm = fmaxf(mm, src.ml(c).x);
+  if (dq == 0) lds.sm[slice] = mm;
   __syncthreads();
-  float M = sm[0];
+  float M = lds.sm[0];
 #pragma unroll
-  for (int s = 1; s < P; ++s) M = fmaxf(M, sm[s]);
+  for (int s = 1; s < P; ++s) M = fmaxf(M, lds.sm[s]);
   const float base = safe_base(M);
   float ll = 0.0f;
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -399,21 +426,264 @@ __global__ __launch_bounds__(NT) void decode_attention_merge_kernel(AttnParams p
 #pragma unroll
     for (int j = 0; j < B; ++j) {
       const int cc = min(c0 + j * P, splits - 1);
-      ml[j] = pml[cc];
-      ov[j] = *reinterpret_cast<const f32x4*>(po + (long long)cc * kD);
+      ml[j] = src.ml(cc);
+      ov[j] = src.o4(cc);
     }
   }
-  *reinterpret_cast<f32x4*>(&so[slice][dq * 4]) = acc;
-  if (dq == 0) sl[slice] = ll;
+  *reinterpret_cast<f32x4*>(&lds.so[slice][dq * 4]) = acc;
+  if (dq == 0) lds.sl[slice] = ll;
   __syncthreads();
   if (tid < kD) {
-    float L = sl[0], O = so[0][tid];
+    float L = lds.sl[0], O = lds.so[0][tid];
 #pragma unroll
     for (int s = 1; s < P; ++s) {
-      L += sl[s];
-      O += so[s][tid];
+      L += lds.sl[s];
+      O += lds.so[s][tid];
     }
-    out[h * kD + tid] = to_f16(O / L);
+    out_head[tid] = to_f16(O / L);
+  }
+}
+
+template <bool kBatch = false>
+__global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(AttnParams p) {
+  __shared__ MergeLds lds;
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x;
+  const int dq = tid & 31;
+  const int slice = tid >> 5;
+  int splits = p.splits;
+  long long first = (long long)h * p.splits;  // this head's first partial slot
+  _Float16* out = reinterpret_cast<_Float16*>(p.out);
+  if constexpr (kBatch) {
+    const int b = blockIdx.y;
+    int rows;
+    auto_split(p.seqlen + b, p.num_cus, p.num_heads, &splits, &rows);
+    first = ((long long)b * p.num_heads + h) * p.split_stride;
+    out += b * p.out_batch_stride;
+  }
+  const PlainPartials src{p.part_o + first * kD + dq * 4, p.part_ml + first};
+  float2 ml[kMergeBatch];
+  f32x4 ov[kMergeBatch];
+#pragma unroll
+  for (int j = 0; j < kMergeBatch; ++j) {
+    const int cc = min(slice + j * kMergeSlices, splits - 1);
+    ml[j] = src.ml(cc);
+    ov[j] = src.o4(cc);
+  }
+  merge_fold(ml, ov, splits, src, lds, out + h * kD);
+}
+
+// ---------------------------------------------------------------------------
+// Split attention with the merge inside the scan kernel (one launch).
+//
+// Each split workgroup writes its partial as tagged words -- (value, tag)
+// pairs, the tag being the call's sequence number -- into its slot, waits for
+// its stores to be acknowledged (s_waitcnt vmcnt(0): the L2 of its XCD holds
+// them), then adds 1 to its head's arrival counter.  Atomics are performed at
+// a device-coherent point, so the counter sees every arrival whatever XCD it
+// came from; the workgroup that arrives last folds the head's partials.  (The
+// counters are never reset: the host passes the value they hold when the call
+// starts and adds the call's split count.)  The fold performs exactly
+// merge_fold's operations in merge_fold's order (below), one thread per dim,
+// so a call gives the two-launch path's bits.
+//
+// Every workgroup issues its loads of the head's slots right after its
+// arrival atomic, before the atomic returns: the merger's loads overlap the
+// atomic's round trip.  A slot of a split that arrives between those loads and
+// the merger's own arrival can be read before its stores land; its words are
+// then visibly stale (tags, below) and the slots are read again, a bounded
+// number of times.  Each wave reads whole slots, one 16-byte-per-lane load per
+// 1 KB slot, and the merger regroups them by dim in LDS.
+//
+// The merger reads the slots through its XCD's L2.  With the launch's
+// workgroup i on XCD (k + i) mod NX (round-robin dispatch, checked at context
+// creation) and num_heads a multiple of NX, every split of head h runs on one
+// XCD, so every slot the merger reads is in its own L2: no cache writeback or
+// invalidation stands between the splits and the merge.  Correctness does not
+// rest on that placement: every 8-byte word carries the tag and is written by
+// one store, so a word the merger can see is either this call's or visibly
+// stale.  A split whose words stay stale after the re-reads (written on
+// another XCD, still in that XCD's L2) is scanned again by the merger from the
+// KV cache -- the same arithmetic, so the same bits -- and the fold proceeds.
+// ---------------------------------------------------------------------------
+
+// Words of one tagged slot: O[128] as (O_d, tag), then (m, tag), (l, tag).
+constexpr int kXSlotWords = 144;   // 130 used; 1152 B, nine 128-B lines
+constexpr int kXPolls = 1 << 14;   // reads of the slots before the stale ones are scanned again
+static_assert(kXMaxSplits <= 64 && kXMaxSplits <= kMergeSlices * kMergeBatch,
+              "one wave holds a head's split weights; merge_fold reads them in one batch");
+
+__device__ __forceinline__ bool tag_ok(float word_tag, unsigned tag) { return __float_as_uint(word_tag) == tag; }
+
+// One read of a head's slots by the merging workgroup's layout: wave w takes
+// slots w, w + 4, ... (lane l: words 2l and 2l + 1, i.e. dims 2l, 2l + 1 of O),
+// and lanes c < SMAX of wave 0 also take slot c's (m, l) record.  The loads
+// are non-temporal: they do not return a line the CU's L1 kept from an
+// earlier read, which a later read of a slot must not see.  (In a dispatch
+// that does not split workgroups across CUs, buffer_inv sc0 leaves L1 lines
+// in place; measured on gfx950, a non-temporal load returned the line another
+// CU of the XCD had written since, in 80-120 ns.)
+template <int SMAX>
+__device__ __forceinline__ void read_slots(const char* __restrict__ head, int wave, int lane,
+                                           f32x4 (&v)[SMAX / 4], f32x4& rec) {
+#pragma unroll
+  for (int j = 0; j < SMAX / 4; ++j)
+    v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(
+        head + (unsigned)((wave + 4 * j) * kXSlotWords * 8 + lane * 16)));
+  if (wave == 0 && lane < SMAX)
+    rec = __builtin_nontemporal_load(
+        reinterpret_cast<const f32x4*>(head + (unsigned)(lane * kXSlotWords * 8 + kD * 8)));
+}
+
+// SMAX: a bound on p.splits (16, 32 or 64): the slots each wave reads, the
+// LDS the merger regroups them in.
+template <int U, int SMAX>
+__global__ __launch_bounds__(kMergeThreads) void decode_attention_xmerge_kernel(AttnParams p) {
+  static_assert(SMAX % 4 == 0 && SMAX <= kXMaxSplits, "SMAX: a multiple of 4, at most the slot count");
+  constexpr int NW = kMergeThreads / 64;
+  static_assert(NW == 4, "four waves read the slots");
+  __shared__ ScanLds<NW> slds;
+  __shared__ float s_o[SMAX][kD];      // O_c,d of the head's splits
+  __shared__ float s_w[SMAX];          // merge weight exp2(m_c - M) of split c
+  __shared__ float s_l[SMAX];          // l_c
+  __shared__ unsigned s_arrived[3];    // per read round, three rounds apart
+  __shared__ unsigned s_stale[3][2];   // one mask per read round, three rounds apart
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = blockIdx.x % p.num_heads;
+  const int c = blockIdx.x / p.num_heads;
+  const int splits = p.splits;
+  const float tagf = __uint_as_float(p.tag);
+  float2* head_slots = p.xpart + (long long)h * kXMaxSplits * kXSlotWords;
+  const char* head = reinterpret_cast<const char*>(head_slots);
+
+  // This split's partial, published as tagged words.
+  {
+    const int r0 = c * p.rows_per_split;
+    float M, L, O;
+    scan_fold<NW, U>(p, p.q, h, r0, min(p.seqlen - r0, p.rows_per_split), slds, M, L, O);
+    float2* slot = head_slots + (long long)c * kXSlotWords;
+    if (tid < kD) slot[tid] = float2{O, tagf};
+    if (tid == 0) *reinterpret_cast<f32x4*>(slot + kD) = f32x4{M, tagf, L, tagf};
+  }
+  // every wave's stores acknowledged (in its XCD's L2)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (tid < 6) (&s_stale[0][0])[tid] = 0u;
+  __syncthreads();
+  const int merger = splits - 1;                             // the last split, often the shortest
+  if (c != merger) {
+    // Arrival: a hint for the merger, which reads the slots themselves; no
+    // one waits for it here.
+    if (tid == 0)
+      __hip_atomic_fetch_add(p.xcnt + h * kXCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  // The merger: read the head's slots until every word carries this call's
+  // tag.  A slot still stale in a read that follows one in which every other
+  // split had arrived (each arrives after its stores are acknowledged) was
+  // written where this workgroup cannot see it: it is scanned again here, as
+  // is every slot still stale after kXPolls reads (and those the test hook
+  // names), so the loop always ends.
+  unsigned long long force = 0ull;
+  if (p.recompute_mask)
+    for (int cc = 0; cc < splits; ++cc)
+      if ((p.recompute_mask >> (cc & 31)) & 1u) force |= 1ull << cc;
+  f32x4 v[SMAX / 4];
+  f32x4 rec = {-__builtin_inff(), 0.0f, 0.0f, 0.0f};
+  bool all_arrived = false;                                  // seen in an earlier read
+  for (int round = 0;; ++round) {
+    read_slots<SMAX>(head, wave, lane, v, rec);
+    unsigned arrived = 0u;
+    if (tid == 0)
+      arrived = __hip_atomic_load(p.xcnt + h * kXCounterStride, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT) - p.cnt_base;
+    // Which splits have a word, among those read, that is not this call's.
+    unsigned long long stale_w = 0ull;                       // wave-uniform
+#pragma unroll
+    for (int j = 0; j < SMAX / 4; ++j) {
+      const int cc = wave + 4 * j;
+      if (__builtin_amdgcn_ballot_w64(!tag_ok(v[j][1], p.tag) || !tag_ok(v[j][3], p.tag)) &&
+          cc < splits)
+        stale_w |= 1ull << cc;
+    }
+    if (wave == 0)
+      stale_w |= __builtin_amdgcn_ballot_w64(lane < splits &&
+                                             (!tag_ok(rec[1], p.tag) || !tag_ok(rec[3], p.tag)));
+    unsigned* mask = s_stale[round % 3];
+    if (lane == 0 && stale_w) {
+      __hip_atomic_fetch_or(&mask[0], (unsigned)stale_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_fetch_or(&mask[1], (unsigned)(stale_w >> 32), __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    if (tid == 0) s_arrived[round % 3] = arrived;
+    if (tid < 2) s_stale[(round + 1) % 3][tid] = 0u;        // read two rounds ago, next written next round
+    __syncthreads();
+    const unsigned long long stale = (((unsigned long long)mask[1] << 32) | mask[0]) & ~force;
+    if ((stale | force) == 0ull || round > kXPolls) break;   // workgroup-uniform
+    const unsigned long long rescan = force | (all_arrived || round == kXPolls ? stale : 0ull);
+    all_arrived = s_arrived[round % 3] >= (unsigned)(splits - 1);
+    force = 0ull;
+    if (rescan) {
+      // Scan those splits again (same plan, same arithmetic, same bits) and
+      // publish them from this workgroup.
+      for (int cc = 0; cc < splits; ++cc) {
+        if (!((rescan >> cc) & 1ull)) continue;
+        const int r0 = cc * p.rows_per_split;
+        float M, L, O;
+        __syncthreads();                                     // slds reuse
+        scan_fold<NW, U>(p, p.q, h, r0, min(p.seqlen - r0, p.rows_per_split), slds, M, L, O);
+        float2* slot = head_slots + (long long)cc * kXSlotWords;
+        if (tid < kD) slot[tid] = float2{O, tagf};
+        if (tid == 0) *reinterpret_cast<f32x4*>(slot + kD) = f32x4{M, tagf, L, tagf};
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+    }
+  }
+
+  // Regroup by dim in LDS; wave 0 turns the records into merge_fold's weights:
+  // M = max_c m_c (fmaxf, exact in any order), w_c = exp2(m_c - safe_base(M)).
+#pragma unroll
+  for (int j = 0; j < SMAX / 4; ++j)
+    *reinterpret_cast<float2*>(&s_o[wave + 4 * j][2 * lane]) = float2{v[j][0], v[j][2]};
+  if (wave == 0) {
+    float m = -__builtin_inff();
+    if (lane < splits) m = fmaxf(m, rec[0]);
+    const float M = SMAX <= 16 ? row16_max(m) : wave64_max(m);   // splits in lanes 0..SMAX-1
+    if (lane < splits) {
+      s_w[lane] = exp2_rep_nonpos(m - safe_base(M));
+      s_l[lane] = rec[2];
+    }
+  }
+  __syncthreads();
+  // merge_fold's sums for dim d: slice s (of kMergeSlices) adds w_c * l_c and
+  // w_c * O_c over its splits c = s, s + P, ... in ascending order with fmaf
+  // from 0, then the slice sums are added in slice order (empty slices add
+  // 0.0f, as merge_fold's do).
+  if (tid < kD) {
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kMergeSlices; ++s) {
+      float acc = 0.0f, ll = 0.0f;
+#pragma unroll
+      for (int cc = s; cc < SMAX; cc += kMergeSlices) {
+        if (cc < splits) {
+          const float w = s_w[cc];
+          ll = __builtin_fmaf(w, s_l[cc], ll);
+          acc = __builtin_fmaf(w, s_o[cc][tid], acc);
+        }
+      }
+      if (s == 0) {
+        O = acc;
+        L = ll;
+      } else {
+        O += acc;
+        L += ll;
+      }
+    }
+    reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = to_f16(O / L);
   }
 }
 
@@ -446,8 +716,8 @@ hipError_t launch_decode_attention_split_batch(const AttnParams& p, int rows_per
     hipLaunchKernelGGL((decode_attention_scan_kernel<4, 2, true, true>), scan_grid, dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((decode_attention_merge_kernel<256, true>), dim3(p.num_heads, tokens), dim3(256), 0,
-                     stream, p);
+  hipLaunchKernelGGL((decode_attention_merge_kernel<true>), dim3(p.num_heads, tokens),
+                     dim3(kMergeThreads), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -455,6 +725,25 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
                                    int stages) {
   if (plan.variant == 0) {
     if (stages & kStageScan) launch_scan<16, false>(p, plan.rows_per_tile, dim3(p.num_heads), stream);
+    return hipGetLastError();
+  }
+  if (plan.xmerge) {
+    if (plan.waves != 4 || p.splits > kXMaxSplits || !p.xpart || !p.xcnt) return hipErrorInvalidValue;
+    if (stages & kStageScan) {
+      const dim3 grid(p.num_heads * p.splits);
+      const dim3 block(kMergeThreads);
+      const bool u4 = plan.rows_per_tile == 4;
+      if (p.splits <= 16) {
+        if (u4) hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, 16>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, 16>), grid, block, 0, stream, p);
+      } else if (p.splits <= 32) {
+        if (u4) hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, 32>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, 32>), grid, block, 0, stream, p);
+      } else {
+        if (u4) hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, 64>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, 64>), grid, block, 0, stream, p);
+      }
+    }
     return hipGetLastError();
   }
   if (stages & kStageScan) {
@@ -468,7 +757,21 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
     if (e != hipSuccess) return e;
   }
   if (stages & kStageMerge)
-    hipLaunchKernelGGL(decode_attention_merge_kernel<256>, dim3(p.num_heads), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(decode_attention_merge_kernel<false>, dim3(p.num_heads), dim3(kMergeThreads), 0,
+                       stream, p);
+  return hipGetLastError();
+}
+
+namespace {
+__global__ void xcd_probe_kernel(unsigned* out) {
+  unsigned id;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(id));
+  if (threadIdx.x == 0) out[blockIdx.x] = id;
+}
+}  // namespace
+
+hipError_t launch_xcd_probe(unsigned* out, int grid, hipStream_t stream) {
+  hipLaunchKernelGGL(xcd_probe_kernel, dim3(grid), dim3(64), 0, stream, out);
   return hipGetLastError();
 }
 

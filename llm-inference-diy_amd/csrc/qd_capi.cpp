@@ -6,6 +6,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -41,14 +42,20 @@ using qd::hip_fail;
 
 // Launch planner, from measured sweeps on MI355X (16 heads, cold KV, the
 // bit-reproducible kernels):
-//   * up to kFusedMaxRows rows: one 16-wave workgroup per head, no merge
-//     (4.8 us at 128 rows, 5.6 at 192; every split plan costs ~6 us there,
-//     the floor of two dependent launches);
+//   * short lengths: one 16-wave workgroup per head, no merge -- up to
+//     kFusedMaxRowsX rows when the context merges split plans inside the scan
+//     kernel (fused 4.7 us at 128 rows against 5.0 split, 5.3 against 5.1 at
+//     160), else up to kFusedMaxRows (split + merge kernel costs ~7 us there);
 //   * longer: one split workgroup per CU in total (16 splits at 16 heads), each
-//     looping over its rows (6.0 us at 256-512 rows, 15.3 at 8192, 42.2 at
-//     32768), except two per CU between 1025 and 2048 rows; other split counts
-//     or more waves per workgroup measured no better (qd::auto_split).
+//     looping over its rows (qd::auto_split); other split counts or more waves
+//     per workgroup measured no better.  Up to kXMergeMaxRows rows the last
+//     split of each head merges in the scan kernel (5.3-5.5 us at 256-512
+//     rows, 6.2 at 1024, against 7.2-7.6 with a merge kernel); beyond, a merge
+//     kernel follows (0.1-0.4 us faster there: 10.3 against 10.5 us at 4096,
+//     15.2 against 15.5 at 8192).
 constexpr int kFusedMaxRows = 224;
+constexpr int kFusedMaxRowsX = 128;
+constexpr int kXMergeMaxRows = 2048;
 constexpr int kPrefillBatch = 256;   // split-plan prefill queries per batched launch pair
 
 qd::AttnPlan plan_fused(int seqlen) {
@@ -58,6 +65,7 @@ qd::AttnPlan plan_fused(int seqlen) {
   plan.rows_per_split = seqlen;
   plan.rows_per_tile = 4;
   plan.waves = 16;
+  plan.xmerge = 0;
   return plan;
 }
 
@@ -77,6 +85,7 @@ qd::AttnPlan plan_split(int num_cus, int num_heads, int seqlen, int requested) {
   plan.splits = splits;
   plan.waves = 4;
   plan.rows_per_tile = rows >= 64 ? 4 : 2;
+  plan.xmerge = 0;
   return plan;
 }
 
@@ -88,8 +97,21 @@ qd::AttnPlan plan_auto(int num_cus, int num_heads, int seqlen) {
   return seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(num_cus, num_heads, seqlen, 0);
 }
 
+// Whether the context's split plans can merge in the scan kernel: it found
+// round-robin dispatch with num_heads a multiple of its period, and the
+// caller did not ask for two launches.
+bool xmerge_available(const qd_ctx* ctx) {
+  return ctx->xmerge_ok && ctx->merge_mode != QD_MERGE_TWO_LAUNCHES;
+}
+
+// Longest length the automatic plan runs fused.
+int fused_max_rows(const qd_ctx* ctx) {
+  return xmerge_available(ctx) ? kFusedMaxRowsX : kFusedMaxRows;
+}
+
 qd::AttnPlan plan_auto(const qd_ctx* ctx, int seqlen) {
-  return plan_auto(ctx->num_cus, ctx->cfg.num_heads, seqlen);
+  return seqlen <= fused_max_rows(ctx) ? plan_fused(seqlen)
+                                       : plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, 0);
 }
 
 
@@ -139,15 +161,52 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.out_batch_stride = 0;
   p.num_cus = ctx->num_cus;
   p.split_stride = plan.splits;
+  p.xpart = ctx->xpart;
+  p.xcnt = ctx->xcnt;
+  p.cnt_base = 0u;
+  p.tag = 0u;
+  p.recompute_mask = ctx->recompute_mask;
   return p;
 }
 
+// Whether a split plan of this context merges inside the scan kernel: the
+// merge is available, the length is at most kXMergeMaxRows (any length under
+// QD_MERGE_IN_KERNEL), and the grid is at most one workgroup per CU -- then
+// every split of a head runs on one XCD (measured: with two workgroups per
+// CU, about 13 of a head's 32 splits landed on other XCDs, and the merger had
+// to scan them again) -- and the merger reads the head's splits in one batch
+// of loads.
+bool use_xmerge(const qd_ctx* ctx, const qd::AttnPlan& plan, int seqlen) {
+  return plan.variant == 1 && xmerge_available(ctx) &&
+         (seqlen <= kXMergeMaxRows || ctx->merge_mode == QD_MERGE_IN_KERNEL) &&
+         plan.waves == 4 && plan.splits <= qd::kXMaxSplits &&
+         (long long)plan.splits * ctx->cfg.num_heads <= ctx->num_cus;
+}
+
 int run_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                  uint16_t* out, int seqlen, const qd::AttnPlan& plan, hipStream_t stream,
+                  uint16_t* out, int seqlen, const qd::AttnPlan& plan_in, hipStream_t stream,
                   int stages = qd::kStageScan | qd::kStageMerge) {
-  const qd::AttnParams p = make_params(ctx, q, k, v, out, seqlen, plan);
+  qd::AttnPlan plan = plan_in;
+  plan.xmerge = use_xmerge(ctx, plan, seqlen) ? 1 : 0;
+  qd::AttnParams p = make_params(ctx, q, k, v, out, seqlen, plan);
+  if (plan.xmerge && (stages & qd::kStageScan)) {
+    // A fresh tag per call; tag 0 is never used, and after 2^32 calls, once
+    // the tags wrap, the slots are cleared so that no stale word can carry the
+    // tag of the call that reads it.
+    if (++ctx->xtag == 0u) {
+      const hipError_t e = hipMemsetAsync(ctx->xpart, 0,
+                                          (size_t)ctx->cfg.num_heads * qd::kXMaxSplits * qd::kXSlotBytes,
+                                          stream);
+      if (e != hipSuccess) return hip_fail(e, "clearing the in-kernel merge slots");
+      ctx->xtag = 1u;
+    }
+    p.tag = ctx->xtag;
+    p.cnt_base = ctx->xcnt_sum;
+  }
   hipError_t e = qd::launch_decode_attention(p, plan, stream, stages);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
+  // every split of every head but its merger arrives once on its head's counter
+  if (plan.xmerge && (stages & qd::kStageScan)) ctx->xcnt_sum += (unsigned)(plan.splits - 1);
   return QD_OK;
 }
 
@@ -164,7 +223,7 @@ int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const 
   if (pos0 + tokens > ctx->cfg.max_seqlen)
     return fail(QD_EINVAL, "positions up to %d exceed max_seqlen %d", pos0 + tokens, ctx->cfg.max_seqlen);
   // queries whose length plan_auto makes fused: one launch for all of them
-  const int n_fused = std::max(0, std::min(tokens, kFusedMaxRows - pos0));
+  const int n_fused = std::max(0, std::min(tokens, fused_max_rows(ctx) - pos0));
   if (n_fused > 0) {
     qd::AttnParams p = make_params(ctx, q, k, v, out, pos0 + 1, plan_fused(pos0 + 1));
     p.q_batch_stride = q_stride;
@@ -178,7 +237,7 @@ int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const 
   if (n_fused >= tokens) return QD_OK;
   if (!ctx->pf_part_o) {
     // slots for kPrefillBatch queries x H heads x the largest automatic split count
-    const int stride = std::max(1, std::min(qd::kMaxSplits, 2 * ctx->num_cus / ctx->cfg.num_heads));
+    const int stride = std::max(1, std::min(qd::kMaxSplits, ctx->num_cus / ctx->cfg.num_heads));
     const size_t slots = (size_t)kPrefillBatch * ctx->cfg.num_heads * stride;
     hipError_t e = hipMalloc(&ctx->pf_part_o, slots * 128 * sizeof(float));
     if (e == hipSuccess) e = hipMalloc(&ctx->pf_part_ml, slots * sizeof(float2));
@@ -301,6 +360,60 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   if ((e = hipMemcpy(ctx->rope_cs, cs.data(), S * 64 * sizeof(float2), hipMemcpyHostToDevice)) !=
       hipSuccess)
     return cleanup(hip_fail(e, "hipMemcpy of the RoPE table"));
+
+  // In-kernel merge: tagged slots (all words tag 0, which no call uses) and
+  // zeroed arrival counters; then the dispatch placement it is fast under.
+  const size_t xpart_bytes = H * qd::kXMaxSplits * qd::kXSlotBytes;
+  const size_t xcnt_bytes = H * qd::kXCounterStride * sizeof(unsigned);
+  if ((e = hipMalloc(&ctx->xpart, xpart_bytes)) != hipSuccess ||
+      (e = hipMalloc(&ctx->xcnt, xcnt_bytes)) != hipSuccess) {
+    int code = hip_fail(e, "hipMalloc of the in-kernel merge scratch");
+    return cleanup(code == QD_EHIP ? QD_ENOMEM : code);
+  }
+  if ((e = hipMemset(ctx->xcnt, 0, xcnt_bytes)) != hipSuccess)
+    return cleanup(hip_fail(e, "hipMemset of the merge counters"));
+  // Probe which XCD each workgroup of a 256-workgroup launch runs on, into the
+  // slot area (cleared afterwards).  Round-robin with period n (workgroup i on
+  // XCD (k + i) mod n for some start k) puts every split of head h on one XCD
+  // when num_heads is a multiple of n; a single XCD for all is period 1.
+  // Anything else, in three tries, leaves the in-kernel merge off (it would
+  // still be correct, but would re-scan the splits it cannot see).  The
+  // device's first context probes; later ones reuse its answer, so every
+  // context of a process plans the same way on one device.
+  {
+    static std::mutex probe_mu;
+    static int probed_period[64];
+    static bool probed[64];
+    std::lock_guard<std::mutex> lock(probe_mu);
+    const int slot = ctx->device >= 0 && ctx->device < 64 ? ctx->device : -1;
+    int period = 0;
+    if (slot >= 0 && probed[slot]) {
+      period = probed_period[slot];
+    } else {
+      constexpr int kProbe = 256;
+      unsigned xcc[kProbe];
+      unsigned* dprobe = reinterpret_cast<unsigned*>(ctx->xpart);
+      for (int attempt = 0; attempt < 3 && period == 0; ++attempt) {
+        if ((e = qd::launch_xcd_probe(dprobe, kProbe, nullptr)) != hipSuccess ||
+            (e = hipMemcpy(xcc, dprobe, sizeof(xcc), hipMemcpyDeviceToHost)) != hipSuccess)
+          return cleanup(hip_fail(e, "XCD placement probe"));
+        period = qd::round_robin_period(xcc, kProbe);
+      }
+      if (slot >= 0) {
+        probed[slot] = true;
+        probed_period[slot] = period;
+      }
+    }
+    if ((e = hipMemset(ctx->xpart, 0, xpart_bytes)) != hipSuccess ||
+        (e = hipDeviceSynchronize()) != hipSuccess)
+      return cleanup(hip_fail(e, "clearing the in-kernel merge slots"));
+    ctx->num_xcd = period;
+    ctx->xmerge_ok = period > 0 && cfg->num_heads % period == 0;
+  }
+  ctx->xtag = 0u;
+  ctx->xcnt_sum = 0u;
+  ctx->merge_mode = QD_MERGE_AUTO;
+  ctx->recompute_mask = 0u;
   *out_ctx = ctx;
   return QD_OK;
 }
@@ -315,6 +428,8 @@ int qd_ctx_destroy(qd_ctx* ctx) {
   if (ctx->rope_cs) (void)hipFree(ctx->rope_cs);
   if (ctx->pf_part_o) (void)hipFree(ctx->pf_part_o);
   if (ctx->pf_part_ml) (void)hipFree(ctx->pf_part_ml);
+  if (ctx->xpart) (void)hipFree(ctx->xpart);
+  if (ctx->xcnt) (void)hipFree(ctx->xcnt);
   if (switch_dev) (void)hipSetDevice(dev);
   delete ctx;
   return QD_OK;
@@ -427,7 +542,39 @@ int qd_decode_attention_plan_detail(const qd_ctx* ctx, int seqlen, int entry, in
   plan->rows_per_split = p.rows_per_split;
   plan->rows_per_tile = p.rows_per_tile;
   plan->waves = p.waves;
+  plan->merge_in_kernel = use_xmerge(ctx, p, seqlen) ? 1 : 0;
   return QD_OK;
+}
+
+int qd_ctx_set_merge(qd_ctx* ctx, int mode) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  if (mode != QD_MERGE_AUTO && mode != QD_MERGE_TWO_LAUNCHES && mode != QD_MERGE_IN_KERNEL)
+    return fail(QD_EINVAL, "unknown merge mode %d", mode);
+  ctx->merge_mode = mode;
+  return QD_OK;
+}
+
+int qd_ctx_set_recompute_mask(qd_ctx* ctx, unsigned mask) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  ctx->recompute_mask = mask;
+  return QD_OK;
+}
+
+int qd_ctx_xcd_period(const qd_ctx* ctx, int* period) {
+  if (!ctx || !period) return fail(QD_EINVAL, "NULL argument");
+  *period = ctx->num_xcd;
+  return QD_OK;
+}
+
+int qd_xcd_placement(unsigned* xcc, int count) {
+  if (!xcc || count < 1 || count > 65536) return fail(QD_EINVAL, "xcc must hold 1..65536 entries");
+  unsigned* d = nullptr;
+  hipError_t e = hipMalloc(&d, (size_t)count * sizeof(unsigned));
+  if (e != hipSuccess) return hip_fail(e, "hipMalloc of the probe buffer");
+  if ((e = qd::launch_xcd_probe(d, count, nullptr)) == hipSuccess)
+    e = hipMemcpy(xcc, d, (size_t)count * sizeof(unsigned), hipMemcpyDeviceToHost);
+  (void)hipFree(d);
+  return e == hipSuccess ? QD_OK : hip_fail(e, "XCD placement probe");
 }
 
 int qd_decode_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
@@ -526,6 +673,11 @@ int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, cons
   p.out_batch_stride = 0;
   p.num_cus = num_cus;
   p.split_stride = plan.splits;
+  p.xpart = nullptr;      // two launches: the static scratch holds plain partials
+  p.xcnt = nullptr;
+  p.cnt_base = 0u;
+  p.tag = 0u;
+  p.recompute_mask = 0u;
   e = qd::launch_decode_attention(p, plan, stream);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return QD_OK;

@@ -43,6 +43,24 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 
+// Maximum over the 16 lanes of a DPP row (fmaxf: exact in any order, NaN only
+// if every lane is NaN).  All 16 lanes receive it.
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_mov<kDppQuadSwap1>(x));
+  x = fmaxf(x, dpp_mov<kDppQuadSwap2>(x));
+  x = fmaxf(x, dpp_mov<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp_mov<kDppMirror>(x));
+  return x;
+}
+
+// Maximum over all 64 lanes; every lane receives it.
+__device__ __forceinline__ float wave64_max(float x) {
+  x = row16_max(x);
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
 // Sum over all 64 lanes: row sums, then (row0 + row1) + (row2 + row3).  Every
 // lane receives the same value.
 __device__ __forceinline__ float wave64_sum(float x) {

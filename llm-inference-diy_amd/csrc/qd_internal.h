@@ -25,21 +25,19 @@ constexpr int kStaticScratchSlots = 1024;
 int static_scratch(float** part_o, float2** part_ml);
 
 // Split planner constants, from measured sweeps on MI355X (16 heads, cold KV):
-// one split workgroup per CU in total, two per CU between kTwoPerCuMin and
-// kTwoPerCuMax rows (8.1 vs 8.5 us at 2048), each split at least
-// kMinRowsPerSplit rows.
+// one split workgroup per CU in total, each split at least kMinRowsPerSplit
+// rows.  (Two workgroups per CU between 1025 and 2048 rows measured within
+// 0.1 us of one; one per CU keeps every split of a head on one XCD.)
 constexpr int kMinRowsPerSplit = 16;
-constexpr int kTwoPerCuMin = 1024;   // (1024, 2048] rows: two split workgroups per CU
-constexpr int kTwoPerCuMax = 2048;
 
 // The split plan of a query over `seqlen` rows when the caller names no split
-// count: num_cus / num_heads workgroups per head ((2 * num_cus) / num_heads in
-// (kTwoPerCuMin, kTwoPerCuMax]), at most one per kMinRowsPerSplit rows, rows
-// per split rounded up to a multiple of 4 (one load instruction covers 4 rows)
-// and no empty workgroups.  The host planner and the batched prefill kernels,
-// which plan every query for itself, both evaluate this one function.
+// count: num_cus / num_heads workgroups per head, at most one per
+// kMinRowsPerSplit rows, rows per split rounded up to a multiple of 4 (one
+// load instruction covers 4 rows) and no empty workgroups.  The host planner
+// and the batched prefill kernels, which plan every query for itself, both
+// evaluate this one function.
 __host__ __device__ inline void auto_split(int seqlen, int num_cus, int num_heads, int* splits, int* rows) {
-  int s = (seqlen > kTwoPerCuMin && seqlen <= kTwoPerCuMax ? 2 : 1) * num_cus / num_heads;
+  int s = num_cus / num_heads;
   const int by_rows = (seqlen + kMinRowsPerSplit - 1) / kMinRowsPerSplit;
   if (s > by_rows) s = by_rows;
   if (s < 1) s = 1;
@@ -76,7 +74,23 @@ struct AttnParams {
   // split_stride + c.
   int num_cus;
   int split_stride;
+  // In-kernel merge (decode_attention_xmerge_kernel) only: tagged slots
+  // [H][kXMaxSplits][kXSlotWords] (value, tag) words, per-head arrival
+  // counters (kXCounterStride apart; every head's counter holds cnt_base when
+  // the call starts and only grows), this call's tag, and a test hook: splits
+  // whose index mod 32 is set are treated as not visible.
+  float2* xpart;
+  unsigned* xcnt;
+  unsigned cnt_base;
+  unsigned tag;
+  unsigned recompute_mask;
 };
+
+// In-kernel merge limits: at most kXMaxSplits splits per head (the merge
+// reads them in one batch of loads); counters 128 bytes apart.
+constexpr int kXMaxSplits = 64;
+constexpr int kXCounterStride = 32;
+constexpr int kXSlotBytes = 1152;
 
 struct RopeParams {
   uint16_t* qkv;          // [3][H][128]
@@ -202,6 +216,7 @@ struct AttnPlan {
   int rows_per_split;     // rows each workgroup scans
   int rows_per_tile;      // rows per group per tile (template U)
   int waves;              // waves per split workgroup (4, 8 or 16)
+  int xmerge;             // split plans: merge inside the scan kernel (one launch)
 };
 
 // Error reporting of the C ABI: records a printf-style message for
@@ -224,8 +239,30 @@ inline bool overlaps(const void* a, size_t na, const void* b, size_t nb) {
 // plan), kStageMerge the merge kernel of a split plan; a call is both.
 constexpr int kStageScan = 1;
 constexpr int kStageMerge = 2;
+// A split plan with plan.xmerge is one launch (scan and merge in one kernel;
+// kStageScan launches it, kStageMerge alone launches nothing).
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream,
                                    int stages = kStageScan | kStageMerge);
+// Writes the XCD index (HW_REG_XCC_ID) of each of `grid` one-wave workgroups
+// to out[0..grid): the dispatch placement the in-kernel merge relies on for
+// speed (every split of a head on one XCD).
+hipError_t launch_xcd_probe(unsigned* out, int grid, hipStream_t stream);
+
+// Period n of a round-robin placement xcc[i] = (xcc[0] + i) mod n over XCDs
+// 0..n-1 (1 if all are equal), or 0 if the placement is not of that form.
+inline int round_robin_period(const unsigned* xcc, int count) {
+  unsigned hi = 0;
+  bool same = true;
+  for (int i = 0; i < count; ++i) {
+    hi = xcc[i] > hi ? xcc[i] : hi;
+    same = same && xcc[i] == xcc[0];
+  }
+  if (same) return 1;
+  const unsigned n = hi + 1;
+  for (int i = 1; i < count; ++i)
+    if (xcc[i] != (xcc[i - 1] + 1) % n) return 0;
+  return count >= (int)n ? (int)n : 0;
+}
 // Fused (one 16-wave workgroup per head, 4-row tiles) attention of `tokens`
 // queries at once, token b over p.seqlen + b rows: the arithmetic of the fused
 // plan of qd_decode_attention, query by query.
@@ -309,4 +346,17 @@ struct qd_ctx {
   float2* pf_part_ml;
   int pf_tokens;
   int pf_stride;
+  // In-kernel merge of split plans: tagged slots, arrival counters, the last
+  // call's tag; num_xcd is the round-robin period of workgroup dispatch found
+  // at creation (0 if dispatch was not round-robin), xmerge_ok whether
+  // num_heads is a multiple of it; merge_mode QD_MERGE_*; recompute_mask the
+  // test hook of AttnParams.
+  float2* xpart;
+  unsigned* xcnt;
+  unsigned xtag;
+  unsigned xcnt_sum;      // value of every head's arrival counter between calls
+  int num_xcd;
+  int xmerge_ok;
+  int merge_mode;
+  unsigned recompute_mask;
 };

@@ -31,7 +31,8 @@ EXPORTS = (
     "qd_decode_attention_fused", "qd_decode_attention_split", "qd_decode_attention_plan",
     "qd_decode_attention_plan_detail", "qd_decode_attention_noalloc",
     # qdiy/bench.h
-    "qd_decode_attention_stage",
+    "qd_decode_attention_stage", "qd_ctx_set_merge", "qd_ctx_set_recompute_mask",
+    "qd_ctx_xcd_period", "qd_xcd_placement",
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
@@ -44,6 +45,7 @@ EXPORTS = (
 )
 
 GEMM_EXACT, GEMM_MFMA = 0, 1      # qd_gemm_nt / qd_prefill_attention / qd_engine_set_prefill_mode modes
+MERGE_AUTO, MERGE_TWO_LAUNCHES, MERGE_IN_KERNEL = 0, 1, 2   # qd_ctx_set_merge modes (qdiy/bench.h)
 
 
 class QdError(RuntimeError):
@@ -76,9 +78,10 @@ class AttnPlan(ctypes.Structure):
     """qd_attn_plan: the complete launch plan of one decode-attention call."""
     _fields_ = [("variant", ctypes.c_int), ("num_splits", ctypes.c_int),
                 ("rows_per_split", ctypes.c_int), ("rows_per_tile", ctypes.c_int),
-                ("waves", ctypes.c_int)]
+                ("waves", ctypes.c_int), ("merge_in_kernel", ctypes.c_int)]
 
     def as_tuple(self):
+        """The plan fields that fix the output bits (merge_in_kernel does not)."""
         return (self.variant, self.num_splits, self.rows_per_split, self.rows_per_tile, self.waves)
 
 
@@ -104,6 +107,10 @@ def load() -> ctypes.CDLL:
     L.qd_decode_attention_split.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
     L.qd_decode_attention_noalloc.argtypes = [vp, vp, vp, vp, i, i, i, ll, ll, vp]
     L.qd_decode_attention_stage.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
+    L.qd_ctx_set_merge.argtypes = [vp, i]
+    L.qd_ctx_set_recompute_mask.argtypes = [vp, ctypes.c_uint]
+    L.qd_ctx_xcd_period.argtypes = [vp, ctypes.POINTER(i)]
+    L.qd_xcd_placement.argtypes = [ctypes.POINTER(ctypes.c_uint), i]
     L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
     L.qd_decode_attention_plan_detail.argtypes = [vp, i, i, i, ctypes.POINTER(AttnPlan)]
     u16p = ctypes.POINTER(ctypes.c_uint16)
@@ -200,6 +207,20 @@ class Context:
         last = (rows - 1) * self.kv_row_stride + (self.num_heads - 1) * self.kv_head_stride + HEAD_DIM
         if t.storage_offset() + last > t.untyped_storage().nbytes() // 2 or t.numel() < last:
             raise ValueError(f"{name} holds {t.numel()} elements; {rows} rows need {last}")
+
+    def set_merge(self, mode: int) -> None:
+        """qd_ctx_set_merge: MERGE_AUTO (in-kernel where possible) or MERGE_TWO_LAUNCHES."""
+        _check(load().qd_ctx_set_merge(self._h, mode))
+
+    def set_recompute_mask(self, mask: int) -> None:
+        """qd_ctx_set_recompute_mask (test hook of the in-kernel merge)."""
+        _check(load().qd_ctx_set_recompute_mask(self._h, mask & 0xFFFFFFFF))
+
+    def xcd_period(self) -> int:
+        """qd_ctx_xcd_period: round-robin period of workgroup dispatch (0: not round-robin)."""
+        v = ctypes.c_int()
+        _check(load().qd_ctx_xcd_period(self._h, ctypes.byref(v)))
+        return v.value
 
     def plan(self, seqlen: int):
         v, s = ctypes.c_int(), ctypes.c_int()
@@ -305,6 +326,13 @@ class Context:
                                              _ptr(qkv, "qkv"), _ptr(k_layer, "k_layer", False),
                                              _ptr(v_layer, "v_layer", False), pos, max_seqlen, H,
                                              HEAD_DIM, _stream(stream)))
+
+
+def xcd_placement(count: int = 256) -> list:
+    """qd_xcd_placement: the XCD each workgroup of one count-workgroup launch ran on."""
+    buf = (ctypes.c_uint * count)()
+    _check(load().qd_xcd_placement(buf, count))
+    return list(buf)
 
 
 def decode_attention_noalloc(q: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,

@@ -256,19 +256,21 @@ def test_invalid_arguments_raise(qdiy):
     g.close()
 
 
-def _planner_rules(L, H, cus, variant="auto", requested=0):
+def _planner_rules(L, H, cus, variant="auto", requested=0, period=0):
     """The launch planner as its measured rules state it: fused (one 16-wave
-    workgroup per head, 4-row tiles) up to 224 rows; above, one split workgroup
-    per CU in total ((2 * CUs) // H per head in 1025-2048 rows), at most one per
-    16 rows, at most 256, rows per split rounded up to a multiple of 4, no
-    empty workgroups, 4 waves, 4-row tiles from 64 rows per split."""
-    if variant == "fused" or (variant == "auto" and L <= 224):
+    workgroup per head, 4-row tiles) up to 128 rows where the context merges
+    split plans in the scan kernel (dispatch round-robin with a period that
+    divides H), else up to 224; above, one split workgroup per CU in total,
+    at most one per 16 rows, at most 256, rows per split rounded up to a
+    multiple of 4, no empty workgroups, 4 waves, 4-row tiles from 64 rows per
+    split."""
+    fused_max = 128 if period >= 1 and H % period == 0 else 224
+    if variant == "fused" or (variant == "auto" and L <= fused_max):
         return (0, 1, L, 4, 16)
     if requested > 0:
         s = min(requested, 256)
     else:
-        s = ((2 if 1024 < L <= 2048 else 1) * cus) // H
-        s = max(1, min(s, (L + 15) // 16, 256))
+        s = max(1, min(cus // H, (L + 15) // 16, 256))
     rows = -(-L // s)
     rows = (rows + 3) & ~3
     return (1, -(-L // rows), rows, 4 if rows >= 64 else 2, 4)
@@ -282,8 +284,13 @@ def test_planner_follows_its_rules(qdiy, H):
     lengths = sorted(set(list(range(1, 300)) + list(range(1000, 1100)) + list(range(2000, 2100)) +
                          [4095, 4096, 4097, 8191, 8192, 8193, 16384, 32767, 32768]))
     with qdiy.Context(num_heads=H, max_seqlen=32768) as ctx:
+        period = ctx.xcd_period()
         for L in lengths:
-            assert ctx.plan_detail(L).as_tuple() == _planner_rules(L, H, cus), (H, L)
+            assert ctx.plan_detail(L).as_tuple() == _planner_rules(L, H, cus, period=period), (H, L)
+            plan = ctx.plan_detail(L)
+            want_in_kernel = int(plan.variant == qdiy.SPLIT and period >= 1 and H % period == 0
+                                 and L <= 2048 and plan.num_splits <= 64 and plan.num_splits * H <= cus)
+            assert plan.merge_in_kernel == want_in_kernel, (H, L)
         for L in (1, 300, 8192):
             assert ctx.plan_detail(L, "fused").as_tuple() == _planner_rules(L, H, cus, "fused"), L
             for req in (1, 5, 16, 64, 300):

@@ -213,11 +213,12 @@ def test_prefill_gemm_widths(qdiy, hidden, inter):
 @pytest.mark.timeout(600)
 def test_long_prompt_batched_split_attention(qdiy):
     """A 1100-token prompt on 16 heads: the prefill's attention runs fused up to
-    224 rows, then in batched split launches (one pair per run of queries with
-    one tile depth) across the planner's regimes -- 4-row tiles at 1009-1024
-    rows and two workgroups per CU from 1025 -- every query under its own
-    plan.  Greedy tokens and the last logits equal the oracle's, which
-    attends query by query."""
+    the planner's fused length (128 rows on MI355X, 224 where split plans merge
+    in a second kernel), then in batched split launches (one pair per run of
+    queries with one tile depth) across the planner's regimes -- fewer splits
+    below 256 rows, 2-row tiles, 4-row tiles from 1009 rows -- every query
+    under its own plan.  Greedy tokens and the last logits equal the oracle's,
+    which attends query by query."""
     cfg = qdiy.model_cfg(vocab_size=300, hidden_size=2048, num_layers=1, num_heads=16,
                          intermediate_size=512, max_seqlen=1112)
     img = qdiy.random_model_image(cfg, 77, 0.03, nthreads=8)

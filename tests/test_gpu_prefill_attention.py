@@ -115,7 +115,8 @@ CASES = [  # H, pos0, T, layout, q_pad, out_pad
     (16, 0, 1, "engine", 0, 0),
     (16, 0, 127, "engine", 4096, 0),     # the engine's Q rows: q_stride = 3 * H * 128
     (16, 0, 256, "engine", 0, 8),
-    (16, 200, 40, "engine", 0, 0),       # crosses the fused / split plan boundary (224 rows)
+    (16, 200, 40, "engine", 0, 0),       # crosses the fused / split plan boundary of 224 rows
+    (16, 100, 60, "engine", 0, 0),       # crosses the fused / split plan boundary of 128 rows
     (16, 777, 33, "head_major", 8, 8),
     (4, 1000, 256, "engine", 0, 0),
     (12, 31, 17, "head_major", 0, 0),
@@ -128,7 +129,8 @@ def test_exact_mode_is_decode_attention(qdiy, H, pos0, T, layout, q_pad, out_pad
     pr = Prompt(qdiy, H, pos0, T, seed=H * 7 + pos0 + T, layout=layout, q_pad=q_pad, out_pad=out_pad)
     try:
         got = pr.run(qdiy, qdiy.GEMM_EXACT)
-        ts = sorted({0, T // 3, T // 2, T - 1, max(0, 224 - pos0 - 1), max(0, 224 - pos0)} & set(range(T)))
+        edges = {max(0, b - pos0 - d) for b in (128, 224) for d in (0, 1)}
+        ts = sorted(({0, T // 3, T // 2, T - 1} | edges) & set(range(T)))
         want = pr.decode_rows(qdiy, ts)
         for t in ts:
             assert _same(got[t], want[t]), f"query {t} (position {pos0 + t})"
