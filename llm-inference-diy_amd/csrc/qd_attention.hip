@@ -515,6 +515,53 @@ static_assert(kXMaxSplits <= 64 && kXMaxSplits <= kMergeSlices * kMergeBatch,
 
 __device__ __forceinline__ bool tag_ok(float word_tag, unsigned tag) { return __float_as_uint(word_tag) == tag; }
 
+// merge_fold's weights, one lane per split (lanes c < splits of one wave hold
+// split c's m and l): M = max_c m_c (fmaxf, exact in any order), then
+// s_w[c] = exp2(m_c - safe_base(M)) and s_l[c] = l_c.
+template <int SMAX>
+__device__ __forceinline__ void merge_weights(float m_c, float l_c, int lane, int splits,
+                                              float* s_w, float* s_l) {
+  float m = -__builtin_inff();
+  if (lane < splits) m = fmaxf(m, m_c);
+  const float M = SMAX <= 16 ? row16_max(m) : wave64_max(m);   // splits in lanes 0..SMAX-1
+  if (lane < splits) {
+    s_w[lane] = exp2_rep_nonpos(m - safe_base(M));
+    s_l[lane] = l_c;
+  }
+}
+
+// merge_fold's sums and output, one thread per dim d < 128: slice s (of
+// kMergeSlices) adds w_c * l_c and w_c * O_c over its splits c = s, s + P, ...
+// in ascending order with fmaf from 0, then the slice sums are added in slice
+// order (empty slices add 0.0f, as merge_fold's do); out[d] = half(O / L).
+template <int SMAX>
+__device__ __forceinline__ void fold_per_dim(const float* s_w, const float* s_l,
+                                             const float (*s_o)[kD], int splits, _Float16* out) {
+  const int tid = threadIdx.x;
+  if (tid >= kD) return;
+  float O = 0.0f, L = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMergeSlices; ++s) {
+    float acc = 0.0f, ll = 0.0f;
+#pragma unroll
+    for (int cc = s; cc < SMAX; cc += kMergeSlices) {
+      if (cc < splits) {
+        const float w = s_w[cc];
+        ll = __builtin_fmaf(w, s_l[cc], ll);
+        acc = __builtin_fmaf(w, s_o[cc][tid], acc);
+      }
+    }
+    if (s == 0) {
+      O = acc;
+      L = ll;
+    } else {
+      O += acc;
+      L += ll;
+    }
+  }
+  out[tid] = to_f16(O / L);
+}
+
 // One read of a head's slots by the merging workgroup's layout: wave w takes
 // slots w, w + 4, ... (lane l: words 2l and 2l + 1, i.e. dims 2l, 2l + 1 of O),
 // and lanes c < SMAX of wave 0 also take slot c's (m, l) record.  The loads
@@ -643,48 +690,45 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_xmerge_kernel(
     }
   }
 
-  // Regroup by dim in LDS; wave 0 turns the records into merge_fold's weights:
-  // M = max_c m_c (fmaxf, exact in any order), w_c = exp2(m_c - safe_base(M)).
+  // Regroup by dim in LDS, then the weights and the fold.
 #pragma unroll
   for (int j = 0; j < SMAX / 4; ++j)
     *reinterpret_cast<float2*>(&s_o[wave + 4 * j][2 * lane]) = float2{v[j][0], v[j][2]};
-  if (wave == 0) {
-    float m = -__builtin_inff();
-    if (lane < splits) m = fmaxf(m, rec[0]);
-    const float M = SMAX <= 16 ? row16_max(m) : wave64_max(m);   // splits in lanes 0..SMAX-1
-    if (lane < splits) {
-      s_w[lane] = exp2_rep_nonpos(m - safe_base(M));
-      s_l[lane] = rec[2];
-    }
-  }
+  if (wave == 0) merge_weights<SMAX>(rec[0], rec[2], lane, splits, s_w, s_l);
   __syncthreads();
-  // merge_fold's sums for dim d: slice s (of kMergeSlices) adds w_c * l_c and
-  // w_c * O_c over its splits c = s, s + P, ... in ascending order with fmaf
-  // from 0, then the slice sums are added in slice order (empty slices add
-  // 0.0f, as merge_fold's do).
-  if (tid < kD) {
-    float O = 0.0f, L = 0.0f;
+  fold_per_dim<SMAX>(s_w, s_l, s_o, splits, reinterpret_cast<_Float16*>(p.out) + h * kD);
+}
+
+// Stage 2 of the two-launch path for at most SMAX splits per head: merge_fold's
+// arithmetic, mapped as the in-kernel merge maps it (fewer memory round trips
+// and LDS steps than merge_fold's slices, the same bits).  One workgroup per
+// head: wave w loads splits w, w + 4, ... (lane l: dims 2l, 2l + 1), wave 0's
+// lane c split c's (m, l).
+template <int SMAX>
+__global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_dim_kernel(AttnParams p) {
+  static_assert(SMAX % 4 == 0 && SMAX <= 64, "one wave holds a head's split weights");
+  __shared__ float s_o[SMAX][kD];
+  __shared__ float s_w[SMAX];
+  __shared__ float s_l[SMAX];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = blockIdx.x;
+  const int splits = p.splits;
+  const float* po = p.part_o + (long long)h * splits * kD;
+  const float2* pml = p.part_ml + (long long)h * splits;
+  float2 v[SMAX / 4];
 #pragma unroll
-    for (int s = 0; s < kMergeSlices; ++s) {
-      float acc = 0.0f, ll = 0.0f;
+  for (int j = 0; j < SMAX / 4; ++j)
+    v[j] = *reinterpret_cast<const float2*>(po + (long long)min(wave + 4 * j, splits - 1) * kD + 2 * lane);
+  float2 ml = {-__builtin_inff(), 0.0f};
+  if (wave == 0) ml = pml[min(lane, splits - 1)];
 #pragma unroll
-      for (int cc = s; cc < SMAX; cc += kMergeSlices) {
-        if (cc < splits) {
-          const float w = s_w[cc];
-          ll = __builtin_fmaf(w, s_l[cc], ll);
-          acc = __builtin_fmaf(w, s_o[cc][tid], acc);
-        }
-      }
-      if (s == 0) {
-        O = acc;
-        L = ll;
-      } else {
-        O += acc;
-        L += ll;
-      }
-    }
-    reinterpret_cast<_Float16*>(p.out)[h * kD + tid] = to_f16(O / L);
-  }
+  for (int j = 0; j < SMAX / 4; ++j)
+    if (wave + 4 * j < splits) *reinterpret_cast<float2*>(&s_o[wave + 4 * j][2 * lane]) = v[j];
+  if (wave == 0) merge_weights<SMAX>(ml.x, ml.y, lane, splits, s_w, s_l);
+  __syncthreads();
+  fold_per_dim<SMAX>(s_w, s_l, s_o, splits, reinterpret_cast<_Float16*>(p.out) + h * kD);
 }
 
 }  // namespace
@@ -756,9 +800,17 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (stages & kStageMerge)
-    hipLaunchKernelGGL(decode_attention_merge_kernel<false>, dim3(p.num_heads), dim3(kMergeThreads), 0,
-                       stream, p);
+  if (stages & kStageMerge) {
+    const dim3 grid(p.num_heads), block(kMergeThreads);
+    if (p.splits <= 16)
+      hipLaunchKernelGGL(decode_attention_merge_dim_kernel<16>, grid, block, 0, stream, p);
+    else if (p.splits <= 32)
+      hipLaunchKernelGGL(decode_attention_merge_dim_kernel<32>, grid, block, 0, stream, p);
+    else if (p.splits <= 64)
+      hipLaunchKernelGGL(decode_attention_merge_dim_kernel<64>, grid, block, 0, stream, p);
+    else
+      hipLaunchKernelGGL(decode_attention_merge_kernel<false>, grid, block, 0, stream, p);
+  }
   return hipGetLastError();
 }
 
