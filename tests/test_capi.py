@@ -65,6 +65,24 @@ def test_product_sources_do_not_reach_the_oracle():
     assert hits == []
 
 
+def test_engine_cli_rejects_bad_options_before_any_gpu_work(qdiy):
+    """qdiy_engine exits with status 2 and a message on an unknown option or
+    prefill mode, before it loads a model or touches a GPU."""
+    import subprocess
+    for args, env_mode, msg in ((["--bogus"], None, "unknown option"),
+                                (["--prefill", "fast"], None, "exact or mfma"),
+                                (["--prefill=tensor"], None, "exact or mfma"),
+                                ([], "fp8", "exact or mfma")):
+        env = dict(os.environ)
+        env.pop("QDIY_PREFILL", None)
+        if env_mode:
+            env["QDIY_PREFILL"] = env_mode
+        res = subprocess.run([qdiy.ENGINE_EXE, *args, "no_such_model.bin"], input="exit\n",
+                             capture_output=True, text=True, timeout=120, env=env)
+        assert res.returncode == 2, (args, res.stderr)
+        assert msg in res.stderr
+
+
 def test_version_and_limits(qdiy):
     assert re.match(r"^\d+\.\d+\.\d+$", qdiy.version())
     assert qdiy.max_splits() >= 64

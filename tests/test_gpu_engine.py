@@ -252,20 +252,34 @@ def test_engine_rejects_bad_input(qdiy, tmp_path):
             eng.step(1, 600)                                  # pos == max_seqlen
 
 
-def test_engine_cli_protocol(qdiy, tmp_path):
+@pytest.mark.parametrize("how", ["default", "flag", "env"])
+def test_engine_cli_protocol(qdiy, tmp_path, how):
     """qdiy_engine speaks web_chat/app.py's protocol: [ENGINE_READY], reset ->
     [RESET_DONE], a prompt line -> [GENERATION_START], token lines,
-    [GENERATION_END]; at most 512 tokens; exit ends the process."""
+    [GENERATION_END]; at most 512 tokens; exit ends the process.  Prompts are
+    prefilled exactly by default and on the matrix cores with --prefill mfma
+    or QDIY_PREFILL=mfma; each run's tokens equal the library engine's in the
+    same prefill mode."""
     cfg = qdiy.model_cfg(**TINY)
     path = str(tmp_path / "tiny.bin")
     qdiy.write_random_model(path, cfg, 24, 0.05)
+    long_prompt = [int(t) for t in np.random.default_rng(3).integers(0, cfg.vocab_size, 70)]
+    mfma = how != "default"
     with qdiy.Engine(path=path) as eng:
-        want_a = eng.generate([5, 6, 7], 512)
-        want_b = eng.generate([9], 512)
+        if mfma:
+            eng.set_prefill_mode(qdiy.GEMM_MFMA)
+        want = [eng.generate(p, 512) for p in ([5, 6, 7], long_prompt, [9])]
     env = dict(os.environ)
-    proc = subprocess.run([qdiy.ENGINE_EXE, path], input="reset\n5 6 7\n9\nexit\n",
-                          capture_output=True, text=True, timeout=240, env=env)
+    env.pop("QDIY_PREFILL", None)
+    args = [qdiy.ENGINE_EXE, path]
+    if how == "flag":
+        args = [qdiy.ENGINE_EXE, "--prefill", "mfma", path]
+    elif how == "env":
+        env["QDIY_PREFILL"] = "mfma"
+    feed = "reset\n5 6 7\n" + " ".join(map(str, long_prompt)) + "\n9\nexit\n"
+    proc = subprocess.run(args, input=feed, capture_output=True, text=True, timeout=240, env=env)
     assert proc.returncode == 0, proc.stderr[-2000:]
+    assert f"Prefill:           {'mfma' if mfma else 'exact'}" in proc.stdout
     lines = [ln.strip() for ln in proc.stdout.splitlines() if ln.strip()]
     i = next(k for k, ln in enumerate(lines) if "[ENGINE_READY]" in ln)
     rest = lines[i + 1:]
@@ -279,8 +293,8 @@ def test_engine_cli_protocol(qdiy, tmp_path):
             cur = None
         else:
             cur.append(int(ln))
-    assert blocks == [want_a, want_b]
-    assert len(want_a) == 512
+    assert blocks == want
+    assert len(want[0]) == 512
 
 
 @pytest.mark.timeout(900)
