@@ -29,6 +29,8 @@ algorithmic bytes (K and V rows and Q: 8192*L + 4096) / its mean duration per
 launch.  The merge kernel is timed the same way (config.merge_kernel_us).
 config.read_ceiling_us is a load-only kernel over the same layers in the
 scan's launch shape: what one kernel streaming those bytes takes on this box.
+config.empty_kernel_us is an empty kernel of the merge's grid launched back to
+back: the dispatch floor any dependent launch pays.
 
 The CPU baseline is the repository's C restatement of the reference kernels
 (oracle/) on the host cores of the same box, on a bounded sample of the same
@@ -41,6 +43,7 @@ attention share of a decode step, and the prefill time of the 127-token prompt
 and of a 2048-token one, exact and with the projections on the matrix cores).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
+       python bench.py --only call|scan|merge|read|empty --kv L [--steps K]   (for rocprofv3)
 """
 from __future__ import annotations
 
@@ -96,6 +99,7 @@ def bench_lib():
     vp, i, ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
     lib.qd_bench_decode_attention.argtypes = [vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
     lib.qd_bench_read_ceiling.argtypes = [vp, vp, ll, ll, i, i, i, vp, vp]
+    lib.qd_bench_empty.argtypes = [i, i, vp]
     lib.qd_bench_attn_front.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
     return lib
 
@@ -124,13 +128,10 @@ def warm_up(run, warmup: int, floor_s: float = WARMUP_FLOOR_S):
     return n + tail, (time.perf_counter() - t0) * 1e3
 
 
-def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int = 0,
-            detail: bool = False):
-    """us per call at L, cold (layers rotated) and hot (one layer).  detail: also the
-    scan kernel's own duration (events around it) and the read ceiling."""
+def kv_layers(L: int):
+    """Synthetic config-2/3 inputs at L: (n_layers, K, V, Q, O), with enough layers
+    (>= 1 GiB of K+V) that a call reading layer i % n_layers streams from HBM."""
     import torch
-
-    import qdiy
 
     layer_bytes = 2 * L * HID * 2
     n_layers = max(3, math.ceil((1 << 30) / layer_bytes))
@@ -142,17 +143,85 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     kc.normal_(0.0, kscale, generator=gen)
     vc.normal_(0.0, 1.0, generator=gen)
     q = torch.empty(n_layers * HID, dtype=torch.float16, device="cuda").normal_(generator=gen)
-    out = torch.empty_like(q)
+    return n_layers, kc, vc, q, torch.empty_like(q)
+
+
+def attention_loop(lib, ctx, L, n_layers, kc, vc, q, out, sh, kind, splits=0):
+    """fn(iters, layers=n_layers): back-to-back calls from the native loop; kind is the
+    loop's variant (0 auto, 1 fused, 2 split, 3 scan kernel only, 4 merge kernel only)."""
+    import qdiy
+
+    def fn(iters, layers=n_layers):
+        rc = lib.qd_bench_decode_attention(ctx._h, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                           out.data_ptr(), HID, L * HID, layers, L, H, iters,
+                                           kind, splits, sh)
+        if rc != 0:
+            raise RuntimeError(f"bench loop failed: {qdiy.load().qd_last_error().decode()}")
+    return fn
+
+
+def read_loop(lib, L, n_layers, kc, vc, sh):
+    """fn(iters): the read-ceiling kernel over the same layers' K and V rows, in the
+    split scan's launch shape (256 workgroups of 256 threads)."""
+    import torch
+
+    sink = torch.empty(256 * 16, dtype=torch.uint8, device="cuda")
+
+    def fn(iters):
+        if lib.qd_bench_read_ceiling(kc.data_ptr(), vc.data_ptr(), L * HID * 2, L * HID * 2,
+                                     n_layers, 256, iters, sink.data_ptr(), sh) != 0:
+            raise RuntimeError("read-ceiling launch failed")
+    return fn
+
+
+def empty_loop(lib, sh, grid=H):
+    """fn(iters): empty kernels of `grid` workgroups, back to back (the dispatch floor)."""
+    def fn(iters):
+        if lib.qd_bench_empty(grid, iters, sh) != 0:
+            raise RuntimeError("empty-kernel launch failed")
+    return fn
+
+
+def profile_loop(lib, L: int, only: str, steps: int, warmup: int, variant: int, splits: int):
+    """For a profiler: warmup + steps launches of one loop at L, nothing else timed or
+    launched (so every dispatch in the trace belongs to that loop)."""
+    import torch
+
+    import qdiy
+
+    n_layers, kc, vc, q, out = kv_layers(L)
+    ctx = qdiy.Context(num_heads=H, max_seqlen=L)
+    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    kind = {"call": variant, "scan": 3, "merge": 4}.get(only)
+    fn = (read_loop(lib, L, n_layers, kc, vc, sh) if only == "read" else
+          empty_loop(lib, sh) if only == "empty" else
+          attention_loop(lib, ctx, L, n_layers, kc, vc, q, out, sh, kind, splits))
+    torch.cuda.synchronize()
+    fn(warmup + steps)
+    torch.cuda.synchronize()
+    d = ctx.plan_detail(L, {0: "auto", 1: "fused", 2: "split"}[variant], splits)
+    log(f"[bench] profile loop '{only}' at L={L}: {warmup + steps} launches, {n_layers} layers "
+        f"rotated, plan {'fused' if d.variant == qdiy.FUSED else 'split'}x{d.num_splits}"
+        f"{' merge in kernel' if d.merge_in_kernel else ''}")
+    ctx.close()
+
+
+def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int = 0,
+            detail: bool = False):
+    """us per call at L, cold (layers rotated) and hot (one layer).  detail: also the
+    call's kernels alone (scan, merge), the read ceiling and the dispatch floor."""
+    import torch
+
+    import qdiy
+
+    n_layers, kc, vc, q, out = kv_layers(L)
     ctx = qdiy.Context(num_heads=H, max_seqlen=L)
     stream = torch.cuda.current_stream()
     sh = ctypes.c_void_p(stream.cuda_stream)
+    loop = attention_loop(lib, ctx, L, n_layers, kc, vc, q, out, sh, variant, splits)
 
     def run(iters, layers):
-        rc = lib.qd_bench_decode_attention(ctx._h, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                                           out.data_ptr(), HID, L * HID, layers, L, H, iters,
-                                           variant, splits, sh)
-        if rc != 0:
-            raise RuntimeError(f"bench loop failed: {qdiy.load().qd_last_error().decode()}")
+        loop(iters, layers)
 
     def timed(iters, fn):
         # no host synchronisation before e0: it is recorded behind the warm-up tail
@@ -166,20 +235,12 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     cold = lambda n: run(n, n_layers)
     warm_calls, warm_ms = warm_up(cold, warmup)
     us_cold = timed(steps, cold)
-    scan_us = merge_us = ceiling_us = None
+    scan_us = merge_us = ceiling_us = floor_us = None
     tail = max(20, int(WARMUP_TAIL_S / (us_cold * 1e-6)))
     if detail:
         # the call's kernels on their own, back to back over the same layers
         # (qd_decode_attention_stage): scan only, then merge only
-        def stage(kind):
-            def fn(n):
-                rc = lib.qd_bench_decode_attention(ctx._h, q.data_ptr(), kc.data_ptr(),
-                                                   vc.data_ptr(), out.data_ptr(), HID, L * HID,
-                                                   n_layers, L, H, n, kind, 0, sh)
-                if rc != 0:
-                    raise RuntimeError(f"stage loop failed: {qdiy.load().qd_last_error().decode()}")
-            return fn
-
+        stage = lambda kind: attention_loop(lib, ctx, L, n_layers, kc, vc, q, out, sh, kind)
         stage(3)(tail)
         scan_us = timed(steps, stage(3))
         pd = ctx.plan_detail(L)
@@ -187,15 +248,13 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
             stage(4)(tail)
             merge_us = timed(steps, stage(4))
         # load-only kernel over the same layers' K and V rows, same launch shape
-        sink = torch.empty(256 * 16, dtype=torch.uint8, device="cuda")
-
-        def read(n):
-            if lib.qd_bench_read_ceiling(kc.data_ptr(), vc.data_ptr(), L * HID * 2, L * HID * 2,
-                                         n_layers, 256, n, sink.data_ptr(), sh) != 0:
-                raise RuntimeError("read-ceiling launch failed")
-
+        read = read_loop(lib, L, n_layers, kc, vc, sh)
         read(tail)
         ceiling_us = timed(steps, read)
+        # empty kernels of the merge's grid: what any dependent launch costs
+        empty = empty_loop(lib, sh)
+        empty(tail)
+        floor_us = timed(steps, empty)
     hot = lambda n: run(n, 1)
     warm_up(hot, warmup, floor_s=0.0)
     us_hot = timed(steps, hot)
@@ -215,14 +274,15 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
            "gbps_hot": algo_bytes(L) / (us_hot * 1e-6) / 1e9, "frac": gbps / PEAK_GBPS,
            "layers": n_layers, "plan": f"{plan[0]}x{plan[1]}", "kernel": kernel,
            "warmup_calls": warm_calls, "warmup_ms": round(warm_ms, 1),
-           "scan_us": scan_us, "merge_us": merge_us, "read_ceiling_us": ceiling_us}
+           "scan_us": scan_us, "merge_us": merge_us, "read_ceiling_us": ceiling_us,
+           "launch_floor_us": floor_us}
     extra = ""
     if detail:
         res["scan_gbps"] = scan_bytes(L) / (scan_us * 1e-6) / 1e9
         res["ceiling_gbps"] = 2 * L * HID * 2 / (ceiling_us * 1e-6) / 1e9
         extra = (f"; alone: scan kernel {scan_us:.2f} us ({res['scan_gbps']:.0f} GB/s), merge "
                  f"kernel {merge_us if merge_us is None else round(merge_us, 2)} us; read ceiling "
-                 f"{ceiling_us:.2f} us ({res['ceiling_gbps']:.0f} GB/s)")
+                 f"{ceiling_us:.2f} us ({res['ceiling_gbps']:.0f} GB/s); empty kernel {floor_us:.2f} us")
     log(f"[bench] L={L}: {us_cold:.2f} us/call cold ({gbps:.0f} GB/s, {100 * gbps / PEAK_GBPS:.1f}% "
         f"of 8 TB/s), {us_hot:.2f} us hot, plan {res['plan']}, {n_layers} layers rotated, "
         f"warm-up {warm_calls} calls / {warm_ms:.0f} ms{extra}")
@@ -414,6 +474,10 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one 256 MiB device copy (known FETCH_SIZE/WRITE_SIZE) and exit")
+    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty"],
+                    help="for a profiler: run warmup + steps launches of this loop per --kv length "
+                         "(call: qd_decode_attention; scan / merge: that kernel alone; read: the "
+                         "read-ceiling kernel; empty: empty kernels), print no JSON, and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -440,6 +504,10 @@ def main() -> int:
         return 0
     lib = bench_lib()
     variant = {"auto": 0, "fused": 1, "split": 2}[args.variant]
+    if args.only:
+        for L in args.kv:
+            profile_loop(lib, L, args.only, args.steps, args.warmup, variant, args.splits)
+        return 0
     kv = sorted(set(args.kv) | {HEADLINE_L})
     # The headline length is measured first, in the process's first KV buffers, as
     # an engine allocates its cache once at start-up.  Buffers allocated again after
@@ -498,6 +566,7 @@ def main() -> int:
             "merge_kernel_us": per_l("merge_us"),
             "read_ceiling_us": per_l("read_ceiling_us"),
             "read_ceiling_gbps": per_l("ceiling_gbps", 1),
+            "empty_kernel_us": per_l("launch_floor_us"),
             "traffic_over_algorithmic": {str(L): t.get("traffic_over_algorithmic")
                                          for L, t in traffic.items()},
             "fused_path_us_per_call_512": None if fused512 is None else round(fused512["us_cold"], 3),

@@ -45,6 +45,10 @@ __global__ __launch_bounds__(256) void read_ceiling_kernel(const u32x4* __restri
     sink[blockIdx.x] = acc;
 }
 
+// Does nothing: back-to-back launches of it time the dispatch floor, the cost
+// any dependent kernel (such as a separate merge launch) pays before its work.
+__global__ __launch_bounds__(256) void empty_kernel() {}
+
 }  // namespace
 
 extern "C" {
@@ -65,6 +69,16 @@ int qd_bench_read_ceiling(const void* k, const void* v, long long layer_stride_b
                        reinterpret_cast<const u32x4*>(static_cast<const char*>(k) + off),
                        reinterpret_cast<const u32x4*>(static_cast<const char*>(v) + off), per_wg,
                        static_cast<u32x4*>(sink));
+    if (hipGetLastError() != hipSuccess) return 2;
+  }
+  return 0;
+}
+
+// `iters` launches of an empty kernel of `grid` workgroups of 256 threads.
+int qd_bench_empty(int grid, int iters, hipStream_t stream) {
+  if (grid < 1 || iters < 0) return 1;
+  for (int it = 0; it < iters; ++it) {
+    hipLaunchKernelGGL(empty_kernel, dim3(grid), dim3(256), 0, stream);
     if (hipGetLastError() != hipSuccess) return 2;
   }
   return 0;
