@@ -263,9 +263,11 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     d = ctx.plan_detail(L, {0: "auto", 1: "fused", 2: "split"}[variant], splits)
     plan = ("fused" if d.variant == qdiy.FUSED else
             "split+merge-in-kernel" if d.merge_in_kernel else "split", d.num_splits)
-    kernel = (f"decode_attention_xmerge_kernel<{d.rows_per_tile}>" if d.merge_in_kernel else
+    smax = 16 if d.num_splits <= 16 else 32 if d.num_splits <= 32 else 64
+    kernel = (f"decode_attention_xmerge_kernel<{d.rows_per_tile}, {smax}, {d.loads_per_round}>"
+              if d.merge_in_kernel else
               f"decode_attention_scan_kernel<{d.waves}, {d.rows_per_tile}, "
-              f"{'false' if d.variant == qdiy.FUSED else 'true'}, false>")
+              f"{'false' if d.variant == qdiy.FUSED else 'true'}, false, {d.loads_per_round}>")
     ctx.close()
     del kc, vc
     torch.cuda.empty_cache()

@@ -174,6 +174,8 @@ typedef struct qd_attn_plan {
   int merge_in_kernel;/* split plans: 1 if the last split workgroup of each head
                          merges inside the scan kernel (one launch), 0 if a
                          merge kernel follows (two launches); same bits */
+  int loads_per_round;/* tiles whose loads a wave issues before consuming them
+                         in order (1 or 2; same bits) */
 } qd_attn_plan;
 
 /* Plan of the call selected by `entry` (0: qd_decode_attention,

@@ -48,6 +48,26 @@ int qd_ctx_set_merge(qd_ctx* ctx, int mode);
  * XCD.  0 (the default) turns it off.  Outputs are unchanged either way. */
 int qd_ctx_set_recompute_mask(qd_ctx* ctx, unsigned mask);
 
+/* Tiles whose loads a wave of a split plan issues before it consumes them
+ * (1, 2 or 4; consumed in the same order, so every depth gives the same
+ * bits); 0 (the default) lets the planner choose.  For sweeps and tests. */
+int qd_ctx_set_scan_depth(qd_ctx* ctx, int depth);
+
+/* Turns counting of in-kernel merges and their slot reads on (nonzero) or
+ * off (the default: the counts are atomics issued after the output, and a
+ * kernel ends only when they have completed, so they lengthen a call). */
+int qd_ctx_count_xmerges(qd_ctx* ctx, int on);
+
+/* Totals over the context's in-kernel merges (summed over heads; each total
+ * wraps at 2^32): *merges heads merged and *reads reads of a head's slots by
+ * its first merging wave (1 per merge when every partial was visible at the
+ * first read), over the calls made while counting was on; *rescans splits a
+ * merging workgroup scanned again because their partials stayed invisible to
+ * it, over every call.  Synchronous (a device-to-host copy on the null
+ * stream); any pointer may be null. */
+int qd_ctx_xmerge_stats(const qd_ctx* ctx, unsigned long long* merges, unsigned long long* reads,
+                        unsigned long long* rescans);
+
 /* Round-robin period of workgroup dispatch over XCDs found at context
  * creation (8 on MI355X: workgroup i runs on XCD i mod 8), 1 if every
  * workgroup ran on one XCD, 0 if the placement was not round-robin. */

@@ -38,11 +38,14 @@
 //     groups of a wave merge with lane shuffles, the waves of a workgroup in
 //     LDS.  A split workgroup writes one fp32 partial (m, l, O[128]); the
 //     reference keeps fp16 partials.
-//   * Partials are folded by a second, one-workgroup-per-head kernel.
-//     Cross-workgroup hand-off goes through the kernel boundary: an
-//     agent-scope release inside the kernel lowers to a whole-L2 writeback per
-//     workgroup on gfx950 (buffer_wbl2 sc1, measured ~1 us each and
-//     serialised per XCD), far more than a second launch.
+//   * Split partials are folded either by a second, one-workgroup-per-head
+//     kernel or, where every split of a head runs on one XCD, by the head's
+//     last split workgroup inside the scan kernel (one launch), which reads
+//     the other splits' tagged partials through its XCD's L2 with no fence:
+//     an agent-scope release inside the kernel lowers to a whole-L2 writeback
+//     per workgroup on gfx950 (buffer_wbl2 sc1, measured ~1 us each and
+//     serialised per XCD), more than a second launch.  Both folds perform the
+//     same operations in the same order.
 //   * No MFMA: at q=1 the work is a bandwidth-bound GEMV-like reduction.
 #include <atomic>
 #include <mutex>
@@ -209,21 +212,28 @@ __device__ __forceinline__ void consume_tile(GroupState& st, const KvTile<U>& tl
 
 // Scan rows [0, nrows) of one head.  Wave `wave` of NW takes the tiles of 4U
 // consecutive rows starting at wave*4U, (wave+NW)*4U, ...; row blk + 4u + g of
-// a tile goes to group g.  All 2U loads of a tile are issued before any of
-// them is consumed.  (Double-buffering the tiles was measured: it was slower
-// at L = 8192-32768, where the launch already streams at the box's read
-// ceiling, by 4-8%.)
-template <int NW, int U>
+// a tile goes to group g.  The loads of D consecutive tiles of the wave (all
+// 2U loads of each) are issued before any of them is consumed, then the tiles
+// are consumed in order: D changes how many memory round trips a wave waits
+// for, not the arithmetic.  (Prefetching tile i+1 while consuming tile i was
+// measured: it was slower at L = 8192-32768, where the launch already streams
+// at the box's read ceiling, by 4-8%.)
+template <int NW, int U, int D = 1>
 __device__ __forceinline__ void scan_rows(GroupState& st, const char* __restrict__ kbase,
                                           const char* __restrict__ vbase, unsigned row_bytes,
                                           int nrows, int wave, int g, int t, const f16x8 qv,
                                           float scale_log2) {
-  for (int blk = wave * 4 * U; blk < nrows; blk += NW * 4 * U) {
-    KvTile<U> tl;
-    load_tile<U>(tl, kbase, vbase, row_bytes, blk, nrows, g, t);
+  constexpr int kStep = NW * 4 * U;   // rows from one of a wave's tiles to its next
+  for (int blk = wave * 4 * U; blk < nrows; blk += kStep * D) {
+    KvTile<U> tl[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d == 0 || blk + d * kStep < nrows) load_tile<U>(tl[d], kbase, vbase, row_bytes, blk + d * kStep, nrows, g, t);
     // keep the scheduler from sinking loads next to their uses
     __builtin_amdgcn_sched_barrier(0);
-    consume_tile<U>(st, tl, blk, nrows, g, qv, scale_log2);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d == 0 || blk + d * kStep < nrows) consume_tile<U>(st, tl[d], blk + d * kStep, nrows, g, qv, scale_log2);
   }
 }
 
@@ -277,7 +287,7 @@ struct ScanLds {
 // states in LDS, max-first: for tid < 128, (M, L, O) is the workgroup's
 // partial for dim tid (M and L the same in every thread).  Ends with the LDS
 // reads of the fold; a caller that reuses `lds` synchronises first.
-template <int NW, int U>
+template <int NW, int U, int D = 1>
 __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q, int h, int r0,
                                           int nrows, ScanLds<NW>& lds, float& M, float& L,
                                           float& O) {
@@ -290,7 +300,7 @@ __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q
   const long long off = h * p.head_stride + (long long)r0 * p.row_stride;
   GroupState st;
   init_state(st);
-  scan_rows<NW, U>(st, reinterpret_cast<const char*>(p.k + off),
+  scan_rows<NW, U, D>(st, reinterpret_cast<const char*>(p.k + off),
                    reinterpret_cast<const char*>(p.v + off), (unsigned)(p.row_stride * 2), nrows,
                    wave, g, t, qv, p.scale_log2);
   wave_merge(st);
@@ -319,7 +329,7 @@ __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q
   }
 }
 
-template <int NW, int U, bool kSplit, bool kBatch = false>
+template <int NW, int U, bool kSplit, bool kBatch = false, int D = 1>
 __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnParams p) {
   __shared__ ScanLds<NW> lds;
   const int tid = threadIdx.x;
@@ -336,7 +346,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
   const int r0 = c * rows_per_split;
   const int nrows = min(seqlen - r0, rows_per_split);
   float M, L, O;
-  scan_fold<NW, U>(p, p.q + b * p.q_batch_stride, h, r0, nrows, lds, M, L, O);
+  scan_fold<NW, U, D>(p, p.q + b * p.q_batch_stride, h, r0, nrows, lds, M, L, O);
   if (tid < kD) {
     if constexpr (kSplit) {
       const long long slot = kBatch ? ((long long)b * p.num_heads + h) * p.split_stride + c
@@ -476,24 +486,28 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(A
 // ---------------------------------------------------------------------------
 // Split attention with the merge inside the scan kernel (one launch).
 //
-// Each split workgroup writes its partial as tagged words -- (value, tag)
-// pairs, the tag being the call's sequence number -- into its slot, waits for
-// its stores to be acknowledged (s_waitcnt vmcnt(0): the L2 of its XCD holds
-// them), then adds 1 to its head's arrival counter.  Atomics are performed at
-// a device-coherent point, so the counter sees every arrival whatever XCD it
-// came from; the workgroup that arrives last folds the head's partials.  (The
-// counters are never reset: the host passes the value they hold when the call
-// starts and adds the call's split count.)  The fold performs exactly
-// merge_fold's operations in merge_fold's order (below), one thread per dim,
-// so a call gives the two-launch path's bits.
+// Every split workgroup but the head's last writes its partial as tagged
+// words -- (value, tag) pairs, the tag being the call's sequence number --
+// into its slot, waits for its stores to be acknowledged (s_waitcnt vmcnt(0):
+// the L2 of its XCD holds them), then adds 1 to its head's arrival counter
+// and ends.  The head's last split is its merger: it keeps its own partial in
+// registers and reads the other splits' slots until every word it reads
+// carries this call's tag, then folds.  (The counters are never reset: the
+// host passes the value they hold when the call starts and adds the call's
+// split count minus one.)  The fold performs exactly merge_fold's operations
+// in merge_fold's order (below), one lane per dim, so a call gives the
+// two-launch path's bits.
 //
-// Every workgroup issues its loads of the head's slots right after its
-// arrival atomic, before the atomic returns: the merger's loads overlap the
-// atomic's round trip.  A slot of a split that arrives between those loads and
-// the merger's own arrival can be read before its stores land; its words are
-// then visibly stale (tags, below) and the slots are read again, a bounded
-// number of times.  Each wave reads whole slots, one 16-byte-per-lane load per
-// 1 KB slot, and the merger regroups them by dim in LDS.
+// Waves 0 and 1 of the merger each own 64 dims and poll on their own: a read
+// is one 8-byte load per lane per slot (the lane's dim: value and tag) plus
+// one slot record per lane (lane c: split c's m, l), the staleness test is a
+// ballot per slot, the merge weights are computed in the lanes that hold the
+// records and broadcast with readlane.  No LDS and no barrier stand between
+// the last slot becoming visible and the output store.  The counter is read
+// only to decide when a slot that stays stale may be scanned again (a slot
+// still stale in a read issued after the counter showed every other split
+// arrived was written where this workgroup cannot see it); that read is
+// consumed a round later, so it adds nothing to a read that finds every slot.
 //
 // The merger reads the slots through its XCD's L2.  With the launch's
 // workgroup i on XCD (k + i) mod NX (round-robin dispatch, checked at context
@@ -502,9 +516,14 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(A
 // invalidation stands between the splits and the merge.  Correctness does not
 // rest on that placement: every 8-byte word carries the tag and is written by
 // one store, so a word the merger can see is either this call's or visibly
-// stale.  A split whose words stay stale after the re-reads (written on
-// another XCD, still in that XCD's L2) is scanned again by the merger from the
-// KV cache -- the same arithmetic, so the same bits -- and the fold proceeds.
+// stale.  A split whose words stay stale (written on another XCD, still in
+// that XCD's L2) is scanned again by the whole merging workgroup from the KV
+// cache -- the same arithmetic, so the same bits -- and the reads resume.
+// The loads are non-temporal: they do not return a line the CU's L1 kept from
+// an earlier read, which a later read of a slot must not see.  (In a dispatch
+// that does not split workgroups across CUs, buffer_inv sc0 leaves L1 lines
+// in place; measured on gfx950, a non-temporal load returned the line another
+// CU of the XCD had written since, in 80-120 ns.)
 // ---------------------------------------------------------------------------
 
 // Words of one tagged slot: O[128] as (O_d, tag), then (m, tag), (l, tag).
@@ -534,22 +553,31 @@ __device__ __forceinline__ void merge_weights(float m_c, float l_c, int lane, in
 // kMergeSlices) adds w_c * l_c and w_c * O_c over its splits c = s, s + P, ...
 // in ascending order with fmaf from 0, then the slice sums are added in slice
 // order (empty slices add 0.0f, as merge_fold's do); out[d] = half(O / L).
+// The LDS reads do not depend on splits, so they are all issued up front; the
+// terms of absent splits are dropped by selects.
 template <int SMAX>
 __device__ __forceinline__ void fold_per_dim(const float* s_w, const float* s_l,
                                              const float (*s_o)[kD], int splits, _Float16* out) {
   const int tid = threadIdx.x;
   if (tid >= kD) return;
+  float o[SMAX], w[SMAX], l[SMAX];
+#pragma unroll
+  for (int cc = 0; cc < SMAX; ++cc) {
+    o[cc] = s_o[cc][tid];
+    w[cc] = s_w[cc];
+    l[cc] = s_l[cc];
+  }
   float O = 0.0f, L = 0.0f;
 #pragma unroll
   for (int s = 0; s < kMergeSlices; ++s) {
     float acc = 0.0f, ll = 0.0f;
 #pragma unroll
     for (int cc = s; cc < SMAX; cc += kMergeSlices) {
-      if (cc < splits) {
-        const float w = s_w[cc];
-        ll = __builtin_fmaf(w, s_l[cc], ll);
-        acc = __builtin_fmaf(w, s_o[cc][tid], acc);
-      }
+      const bool on = cc < splits;
+      const float nl = __builtin_fmaf(w[cc], l[cc], ll);
+      const float na = __builtin_fmaf(w[cc], o[cc], acc);
+      ll = on ? nl : ll;
+      acc = on ? na : acc;
     }
     if (s == 0) {
       O = acc;
@@ -562,141 +590,200 @@ __device__ __forceinline__ void fold_per_dim(const float* s_w, const float* s_l,
   out[tid] = to_f16(O / L);
 }
 
-// One read of a head's slots by the merging workgroup's layout: wave w takes
-// slots w, w + 4, ... (lane l: words 2l and 2l + 1, i.e. dims 2l, 2l + 1 of O),
-// and lanes c < SMAX of wave 0 also take slot c's (m, l) record.  The loads
-// are non-temporal: they do not return a line the CU's L1 kept from an
-// earlier read, which a later read of a slot must not see.  (In a dispatch
-// that does not split workgroups across CUs, buffer_inv sc0 leaves L1 lines
-// in place; measured on gfx950, a non-temporal load returned the line another
-// CU of the XCD had written since, in 80-120 ns.)
+// One read of the other splits' slots by a merging wave: lane l's dim
+// (value, tag) of every slot, lane c's slot record (lanes c < others), and,
+// issued last, the head's arrival counter (lane 0).
 template <int SMAX>
-__device__ __forceinline__ void read_slots(const char* __restrict__ head, int wave, int lane,
-                                           f32x4 (&v)[SMAX / 4], f32x4& rec) {
+struct SlotRead {
+  f32x2 o[SMAX];
+  f32x4 rec;
+  unsigned cnt;
+};
+
+template <int SMAX>
+__device__ __forceinline__ void issue_read(SlotRead<SMAX>& r, const char* head, unsigned dim_off,
+                                           int last_slot, int lane, int others, float m_own,
+                                           float l_own, const unsigned* counter) {
 #pragma unroll
-  for (int j = 0; j < SMAX / 4; ++j)
-    v[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(
-        head + (unsigned)((wave + 4 * j) * kXSlotWords * 8 + lane * 16)));
-  if (wave == 0 && lane < SMAX)
-    rec = __builtin_nontemporal_load(
+  for (int cc = 0; cc < SMAX; ++cc)
+    r.o[cc] = __builtin_nontemporal_load(
+        reinterpret_cast<const f32x2*>(head + (unsigned)(min(cc, last_slot) * kXSlotWords * 8) + dim_off));
+  r.rec = f32x4{m_own, 0.0f, l_own, 0.0f};   // lane others (the merger's own split) keeps these
+  if (lane < others)
+    r.rec = __builtin_nontemporal_load(
         reinterpret_cast<const f32x4*>(head + (unsigned)(lane * kXSlotWords * 8 + kD * 8)));
+  r.cnt = 0u;
+  if (lane == 0) r.cnt = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// SMAX: a bound on p.splits (16, 32 or 64): the slots each wave reads, the
-// LDS the merger regroups them in.
-template <int U, int SMAX>
+// Splits (< others) with a word in the read that is not this call's.
+template <int SMAX>
+__device__ __forceinline__ unsigned long long stale_splits(const SlotRead<SMAX>& r, int lane, int others,
+                                                           unsigned tag) {
+  unsigned long long stale =
+      __builtin_amdgcn_ballot_w64(lane < others && (!tag_ok(r.rec[1], tag) || !tag_ok(r.rec[3], tag)));
+#pragma unroll
+  for (int cc = 0; cc < SMAX; ++cc)
+    if (cc < others && __builtin_amdgcn_ballot_w64(!tag_ok(r.o[cc].y, tag))) stale |= 1ull << cc;
+  return stale;
+}
+
+// merge_fold's weights in the record lanes (M = max_c m_c, w_c = exp2(m_c -
+// safe_base(M))), broadcast with readlane, then its sums in its order: slice
+// s (of kMergeSlices) adds w_c * l_c and w_c * O_c over c = s, s + P, ...
+// ascending with fmaf from 0, the slice sums are added in slice order;
+// out = half(O / L) for this lane's dim.  Split `others` is the merger's own
+// (o_own).  Terms of absent splits are dropped by selects.
+template <int SMAX>
+__device__ __forceinline__ void fold_store(const SlotRead<SMAX>& r, int lane, int splits, float o_own,
+                                           _Float16* dst) {
+  const int others = splits - 1;
+  const float m = lane < splits ? r.rec[0] : -__builtin_inff();
+  const float M = SMAX <= 16 ? row16_max(m) : wave64_max(m);   // splits in lanes 0..SMAX-1
+  const float wl = exp2_rep_nonpos(m - safe_base(M));
+  const float lc_l = r.rec[2];
+  float O = 0.0f, L = 0.0f;
+#pragma unroll
+  for (int s = 0; s < kMergeSlices; ++s) {
+    float acc = 0.0f, ll = 0.0f;
+#pragma unroll
+    for (int cc = s; cc < SMAX; cc += kMergeSlices) {
+      const bool on = cc < splits;
+      const float w = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wl), cc));
+      const float lc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lc_l), cc));
+      const float oc = cc == others ? o_own : r.o[cc].x;
+      const float nl = __builtin_fmaf(w, lc, ll);
+      const float na = __builtin_fmaf(w, oc, acc);
+      ll = on ? nl : ll;
+      acc = on ? na : acc;
+    }
+    if (s == 0) {
+      O = acc;
+      L = ll;
+    } else {
+      O += acc;
+      L += ll;
+    }
+  }
+  *dst = to_f16(O / L);
+}
+
+// One wave of the merger (wave 0 or 1: dims 64 * wave + lane): reads the
+// other splits' slots until every word it needs is this call's, then folds
+// and stores its 64 dims of the head's output and returns 0.  Returns the
+// splits to scan again instead: those in `force`, or those still stale in a
+// read issued after a completed counter read saw every other split arrived,
+// or after kXPolls reads.  (m_own, l_own, o_own): the merger's own partial
+// (o_own: this lane's dim).  One read is in flight at a time: a kernel ends
+// only when its loads have returned, and a second read in flight when the
+// first finds every slot measured 0.6 us slower per call at L=8192.
+template <int SMAX>
+__device__ __forceinline__ unsigned long long merge_wave(const AttnParams& p, const char* head, int wave,
+                                                        int lane, int splits, float m_own, float l_own,
+                                                        float o_own, unsigned long long force,
+                                                        _Float16* out_head, unsigned& reads) {
+  const int others = splits - 1;                               // slots 0 .. splits - 2
+  const int last_slot = max(others - 1, 0);
+  const unsigned dim_off = (unsigned)((wave * 64 + lane) * 8);
+  const unsigned* counter = p.xcnt + (blockIdx.x % p.num_heads) * kXCounterStride;
+  bool arrived = false;   // a completed counter read, before this read was issued, saw all arrived
+  SlotRead<SMAX> r;
+  for (int round = 0;; ++round) {
+    issue_read<SMAX>(r, head, dim_off, last_slot, lane, others, m_own, l_own, counter);
+    ++reads;
+    const unsigned long long stale = stale_splits<SMAX>(r, lane, others, p.tag);
+    if ((stale | force) == 0ull) {
+      fold_store<SMAX>(r, lane, splits, o_own, out_head + wave * 64 + lane);
+      return 0ull;
+    }
+    const unsigned long long rescan = force | (arrived || round >= kXPolls ? stale : 0ull);
+    if (rescan) return rescan;
+    // This read's counter value: complete now, so it covers the next read.
+    arrived = (unsigned)__builtin_amdgcn_readfirstlane(r.cnt) - p.cnt_base >= (unsigned)others;
+  }
+}
+
+// SMAX: a bound on p.splits (16, 32 or 64): the slots each merging wave reads.
+template <int U, int SMAX, int D = 1>
 __global__ __launch_bounds__(kMergeThreads) void decode_attention_xmerge_kernel(AttnParams p) {
   static_assert(SMAX % 4 == 0 && SMAX <= kXMaxSplits, "SMAX: a multiple of 4, at most the slot count");
   constexpr int NW = kMergeThreads / 64;
-  static_assert(NW == 4, "four waves read the slots");
+  static_assert(NW == 4, "four waves scan; waves 0 and 1 hold the 128 dims");
   __shared__ ScanLds<NW> slds;
-  __shared__ float s_o[SMAX][kD];      // O_c,d of the head's splits
-  __shared__ float s_w[SMAX];          // merge weight exp2(m_c - M) of split c
-  __shared__ float s_l[SMAX];          // l_c
-  __shared__ unsigned s_arrived[3];    // per read round, three rounds apart
-  __shared__ unsigned s_stale[3][2];   // one mask per read round, three rounds apart
+  __shared__ unsigned long long s_need[2];   // splits to scan again, per merging wave
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = blockIdx.x % p.num_heads;
   const int c = blockIdx.x / p.num_heads;
   const int splits = p.splits;
+  const int merger = splits - 1;                             // the last split, often the shortest
   const float tagf = __uint_as_float(p.tag);
   float2* head_slots = p.xpart + (long long)h * kXMaxSplits * kXSlotWords;
   const char* head = reinterpret_cast<const char*>(head_slots);
 
-  // This split's partial, published as tagged words.
-  {
-    const int r0 = c * p.rows_per_split;
-    float M, L, O;
-    scan_fold<NW, U>(p, p.q, h, r0, min(p.seqlen - r0, p.rows_per_split), slds, M, L, O);
+  const int r0 = c * p.rows_per_split;
+  float M, L, O;   // valid in threads tid < kD
+  scan_fold<NW, U, D>(p, p.q, h, r0, min(p.seqlen - r0, p.rows_per_split), slds, M, L, O);
+  if (c != merger) {
+    // This split's partial, published as tagged words.
     float2* slot = head_slots + (long long)c * kXSlotWords;
     if (tid < kD) slot[tid] = float2{O, tagf};
     if (tid == 0) *reinterpret_cast<f32x4*>(slot + kD) = f32x4{M, tagf, L, tagf};
-  }
-  // every wave's stores acknowledged (in its XCD's L2)
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (tid < 6) (&s_stale[0][0])[tid] = 0u;
-  __syncthreads();
-  const int merger = splits - 1;                             // the last split, often the shortest
-  if (c != merger) {
-    // Arrival: a hint for the merger, which reads the slots themselves; no
-    // one waits for it here.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // acknowledged: in its XCD's L2
+    __syncthreads();
+    // Arrival: read by the merger only to decide on scanning a split again;
+    // no one waits for it here.
     if (tid == 0)
       __hip_atomic_fetch_add(p.xcnt + h * kXCounterStride, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
 
-  // The merger: read the head's slots until every word carries this call's
-  // tag.  A slot still stale in a read that follows one in which every other
-  // split had arrived (each arrives after its stores are acknowledged) was
-  // written where this workgroup cannot see it: it is scanned again here, as
-  // is every slot still stale after kXPolls reads (and those the test hook
-  // names), so the loop always ends.
-  unsigned long long force = 0ull;
+  // The merger.  Waves 2 and 3 wait at the barrier below; they take part only
+  // in scanning splits again.
+  unsigned long long force = 0ull;   // test hook: splits treated as never visible
   if (p.recompute_mask)
-    for (int cc = 0; cc < splits; ++cc)
+    for (int cc = 0; cc < merger; ++cc)
       if ((p.recompute_mask >> (cc & 31)) & 1u) force |= 1ull << cc;
-  f32x4 v[SMAX / 4];
-  f32x4 rec = {-__builtin_inff(), 0.0f, 0.0f, 0.0f};
-  bool all_arrived = false;                                  // seen in an earlier read
-  for (int round = 0;; ++round) {
-    read_slots<SMAX>(head, wave, lane, v, rec);
-    unsigned arrived = 0u;
-    if (tid == 0)
-      arrived = __hip_atomic_load(p.xcnt + h * kXCounterStride, __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT) - p.cnt_base;
-    // Which splits have a word, among those read, that is not this call's.
-    unsigned long long stale_w = 0ull;                       // wave-uniform
-#pragma unroll
-    for (int j = 0; j < SMAX / 4; ++j) {
-      const int cc = wave + 4 * j;
-      if (__builtin_amdgcn_ballot_w64(!tag_ok(v[j][1], p.tag) || !tag_ok(v[j][3], p.tag)) &&
-          cc < splits)
-        stale_w |= 1ull << cc;
+  bool done = wave >= 2;
+  unsigned reads = 0u, rescanned = 0u;
+  _Float16* out_head = reinterpret_cast<_Float16*>(p.out) + h * kD;
+  for (;;) {
+    unsigned long long need = 0ull;
+    if (!done) {
+      need = merge_wave<SMAX>(p, head, wave, lane, splits, M, L, O, force, out_head, reads);
+      done = need == 0ull;
     }
-    if (wave == 0)
-      stale_w |= __builtin_amdgcn_ballot_w64(lane < splits &&
-                                             (!tag_ok(rec[1], p.tag) || !tag_ok(rec[3], p.tag)));
-    unsigned* mask = s_stale[round % 3];
-    if (lane == 0 && stale_w) {
-      __hip_atomic_fetch_or(&mask[0], (unsigned)stale_w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      __hip_atomic_fetch_or(&mask[1], (unsigned)(stale_w >> 32), __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
-    if (tid == 0) s_arrived[round % 3] = arrived;
-    if (tid < 2) s_stale[(round + 1) % 3][tid] = 0u;        // read two rounds ago, next written next round
+    if (wave < 2 && lane == 0) s_need[wave] = need;
     __syncthreads();
-    const unsigned long long stale = (((unsigned long long)mask[1] << 32) | mask[0]) & ~force;
-    if ((stale | force) == 0ull || round > kXPolls) break;   // workgroup-uniform
-    const unsigned long long rescan = force | (all_arrived || round == kXPolls ? stale : 0ull);
-    all_arrived = s_arrived[round % 3] >= (unsigned)(splits - 1);
-    force = 0ull;
-    if (rescan) {
-      // Scan those splits again (same plan, same arithmetic, same bits) and
-      // publish them from this workgroup.
-      for (int cc = 0; cc < splits; ++cc) {
-        if (!((rescan >> cc) & 1ull)) continue;
-        const int r0 = cc * p.rows_per_split;
-        float M, L, O;
-        __syncthreads();                                     // slds reuse
-        scan_fold<NW, U>(p, p.q, h, r0, min(p.seqlen - r0, p.rows_per_split), slds, M, L, O);
-        float2* slot = head_slots + (long long)cc * kXSlotWords;
-        if (tid < kD) slot[tid] = float2{O, tagf};
-        if (tid == 0) *reinterpret_cast<f32x4*>(slot + kD) = f32x4{M, tagf, L, tagf};
-      }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
+    const unsigned long long all = s_need[0] | s_need[1];
+    if (all == 0ull) break;
+    // Scan those splits again (same plan, same arithmetic, same bits) and
+    // publish them from this workgroup; the merging waves then read again.
+    rescanned += (unsigned)__builtin_popcountll(all);
+    for (int cc = 0; cc < merger; ++cc) {
+      if (!((all >> cc) & 1ull)) continue;
+      const int rr = cc * p.rows_per_split;
+      float Mc, Lc, Oc;
+      scan_fold<NW, U, D>(p, p.q, h, rr, min(p.seqlen - rr, p.rows_per_split), slds, Mc, Lc, Oc);
+      float2* slot = head_slots + (long long)cc * kXSlotWords;
+      if (tid < kD) slot[tid] = float2{Oc, tagf};
+      if (tid == 0) *reinterpret_cast<f32x4*>(slot + kD) = f32x4{Mc, tagf, Lc, tagf};
+      __syncthreads();                                       // slds reuse
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    force = 0ull;
   }
-
-  // Regroup by dim in LDS, then the weights and the fold.
-#pragma unroll
-  for (int j = 0; j < SMAX / 4; ++j)
-    *reinterpret_cast<float2*>(&s_o[wave + 4 * j][2 * lane]) = float2{v[j][0], v[j][2]};
-  if (wave == 0) merge_weights<SMAX>(rec[0], rec[2], lane, splits, s_w, s_l);
-  __syncthreads();
-  fold_per_dim<SMAX>(s_w, s_l, s_o, splits, reinterpret_cast<_Float16*>(p.out) + h * kD);
+  if (tid == 0) {   // statistics, after the output; not waited for
+    unsigned* st = p.xcnt + h * kXCounterStride;
+    if (p.count_merges) {
+      __hip_atomic_fetch_add(st + kXStatMerges, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(st + kXStatReads, reads, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (rescanned)
+      __hip_atomic_fetch_add(st + kXStatRescans, rescanned, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // Stage 2 of the two-launch path for at most SMAX splits per head: merge_fold's
@@ -734,7 +821,23 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_dim_kern
 }  // namespace
 
 template <int NW, bool kSplit>
-static void launch_scan(const AttnParams& p, int rows_per_tile, dim3 grid, hipStream_t stream) {
+static void launch_scan(const AttnParams& p, int rows_per_tile, int depth, dim3 grid, hipStream_t stream) {
+  if constexpr (NW == 4 && kSplit) {   // deeper load rounds: split plans of 4-wave workgroups
+    if (depth == 4) {
+      if (rows_per_tile == 4)
+        hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, false, 4>), grid, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL((decode_attention_scan_kernel<4, 2, true, false, 4>), grid, dim3(256), 0, stream, p);
+      return;
+    }
+    if (depth == 2) {
+      if (rows_per_tile == 4)
+        hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, false, 2>), grid, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL((decode_attention_scan_kernel<4, 2, true, false, 2>), grid, dim3(256), 0, stream, p);
+      return;
+    }
+  }
   switch (rows_per_tile) {
     case 4:
       hipLaunchKernelGGL((decode_attention_scan_kernel<NW, 4, kSplit>), grid, dim3(NW * 64), 0, stream, p);
@@ -743,6 +846,24 @@ static void launch_scan(const AttnParams& p, int rows_per_tile, dim3 grid, hipSt
       hipLaunchKernelGGL((decode_attention_scan_kernel<NW, 2, kSplit>), grid, dim3(NW * 64), 0, stream, p);
       break;
   }
+}
+
+template <int SMAX, int D>
+static void launch_xmerge_d(const AttnParams& p, int rows_per_tile, dim3 grid, hipStream_t stream) {
+  if (rows_per_tile == 4)
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, D>), grid, dim3(kMergeThreads), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, SMAX, D>), grid, dim3(kMergeThreads), 0, stream, p);
+}
+
+template <int SMAX>
+static void launch_xmerge(const AttnParams& p, int rows_per_tile, int depth, dim3 grid, hipStream_t stream) {
+  if (depth == 4)
+    launch_xmerge_d<SMAX, 4>(p, rows_per_tile, grid, stream);
+  else if (depth == 2)
+    launch_xmerge_d<SMAX, 2>(p, rows_per_tile, grid, stream);
+  else
+    launch_xmerge_d<SMAX, 1>(p, rows_per_tile, grid, stream);
 }
 
 hipError_t launch_decode_attention_fused_batch(const AttnParams& p, int tokens, hipStream_t stream) {
@@ -768,34 +889,28 @@ hipError_t launch_decode_attention_split_batch(const AttnParams& p, int rows_per
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream,
                                    int stages) {
   if (plan.variant == 0) {
-    if (stages & kStageScan) launch_scan<16, false>(p, plan.rows_per_tile, dim3(p.num_heads), stream);
+    if (stages & kStageScan) launch_scan<16, false>(p, plan.rows_per_tile, 1, dim3(p.num_heads), stream);
     return hipGetLastError();
   }
   if (plan.xmerge) {
     if (plan.waves != 4 || p.splits > kXMaxSplits || !p.xpart || !p.xcnt) return hipErrorInvalidValue;
     if (stages & kStageScan) {
       const dim3 grid(p.num_heads * p.splits);
-      const dim3 block(kMergeThreads);
-      const bool u4 = plan.rows_per_tile == 4;
-      if (p.splits <= 16) {
-        if (u4) hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, 16>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, 16>), grid, block, 0, stream, p);
-      } else if (p.splits <= 32) {
-        if (u4) hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, 32>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, 32>), grid, block, 0, stream, p);
-      } else {
-        if (u4) hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, 64>), grid, block, 0, stream, p);
-        else hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, 64>), grid, block, 0, stream, p);
-      }
+      if (p.splits <= 16)
+        launch_xmerge<16>(p, plan.rows_per_tile, plan.depth, grid, stream);
+      else if (p.splits <= 32)
+        launch_xmerge<32>(p, plan.rows_per_tile, plan.depth, grid, stream);
+      else
+        launch_xmerge<64>(p, plan.rows_per_tile, plan.depth, grid, stream);
     }
     return hipGetLastError();
   }
   if (stages & kStageScan) {
     const dim3 grid(p.num_heads * p.splits);
     switch (plan.waves) {
-      case 16: launch_scan<16, true>(p, plan.rows_per_tile, grid, stream); break;
-      case 8: launch_scan<8, true>(p, plan.rows_per_tile, grid, stream); break;
-      default: launch_scan<4, true>(p, plan.rows_per_tile, grid, stream); break;
+      case 16: launch_scan<16, true>(p, plan.rows_per_tile, 1, grid, stream); break;
+      case 8: launch_scan<8, true>(p, plan.rows_per_tile, 1, grid, stream); break;
+      default: launch_scan<4, true>(p, plan.rows_per_tile, plan.depth, grid, stream); break;
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

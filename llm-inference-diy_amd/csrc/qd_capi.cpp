@@ -48,11 +48,12 @@ using qd::hip_fail;
 //     160), else up to kFusedMaxRows (split + merge kernel costs ~7 us there);
 //   * longer: one split workgroup per CU in total (16 splits at 16 heads), each
 //     looping over its rows (qd::auto_split); other split counts or more waves
-//     per workgroup measured no better.  Up to kXMergeMaxRows rows the last
-//     split of each head merges in the scan kernel (5.3-5.5 us at 256-512
-//     rows, 6.2 at 1024, against 7.2-7.6 with a merge kernel); beyond, a merge
-//     kernel follows (0.1-0.4 us faster there: 10.3 against 10.5 us at 4096,
-//     15.2 against 15.5 at 8192).
+//     per workgroup measured no better (L=8192: 14.7 us at 16 splits, 15.6 at
+//     32, 16.7 at 64, 17.1 at 24).  Up to kXMergeMaxRows rows the last split
+//     of each head merges in the scan kernel (5.1-5.4 us at 256-512 rows, 5.8
+//     at 768, 6.5-6.8 at 1280-1536, against 6.7-7.2 with a merge kernel; 7.37
+//     against 7.33 at 2048); beyond, a merge kernel follows (0.3-0.5 us faster
+//     there: 9.75 against 10.2 us at 4096, 14.7 against 15.05 at 8192).
 constexpr int kFusedMaxRows = 224;
 constexpr int kFusedMaxRowsX = 128;
 constexpr int kXMergeMaxRows = 2048;
@@ -66,6 +67,7 @@ qd::AttnPlan plan_fused(int seqlen) {
   plan.rows_per_tile = 4;
   plan.waves = 16;
   plan.xmerge = 0;
+  plan.depth = 1;
   return plan;
 }
 
@@ -86,6 +88,7 @@ qd::AttnPlan plan_split(int num_cus, int num_heads, int seqlen, int requested) {
   plan.waves = 4;
   plan.rows_per_tile = rows >= 64 ? 4 : 2;
   plan.xmerge = 0;
+  plan.depth = 1;
   return plan;
 }
 
@@ -110,8 +113,7 @@ int fused_max_rows(const qd_ctx* ctx) {
 }
 
 qd::AttnPlan plan_auto(const qd_ctx* ctx, int seqlen) {
-  return seqlen <= fused_max_rows(ctx) ? plan_fused(seqlen)
-                                       : plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, 0);
+  return seqlen <= fused_max_rows(ctx) ? plan_fused(seqlen) : plan_split(ctx, seqlen, 0);
 }
 
 
@@ -166,6 +168,7 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.cnt_base = 0u;
   p.tag = 0u;
   p.recompute_mask = ctx->recompute_mask;
+  p.count_merges = ctx->count_merges;
   return p;
 }
 
@@ -183,11 +186,29 @@ bool use_xmerge(const qd_ctx* ctx, const qd::AttnPlan& plan, int seqlen) {
          (long long)plan.splits * ctx->cfg.num_heads <= ctx->num_cus;
 }
 
+// The launch details that do not change the bits: whether the merge runs in
+// the scan kernel, and how many tiles a wave loads per round.  Measured (16
+// heads, cold): with the merge in the kernel, two tiles per round where a
+// wave has two or more (768 rows: 5.80 against 6.25 us, 1280: 6.53 against
+// 7.15, 1536: 6.81 against 7.25); one otherwise, and always with a merge
+// kernel (two per round was 0.1-0.7 us slower from 2048 rows up; four per
+// round slower everywhere).
+qd::AttnPlan finish_plan(const qd_ctx* ctx, const qd::AttnPlan& plan_in, int seqlen) {
+  qd::AttnPlan plan = plan_in;
+  plan.xmerge = use_xmerge(ctx, plan, seqlen) ? 1 : 0;
+  if (plan.variant == 1 && plan.waves == 4) {
+    const int tiles = (plan.rows_per_split + 16 * plan.rows_per_tile - 1) / (16 * plan.rows_per_tile);
+    plan.depth = ctx->scan_depth ? ctx->scan_depth : (plan.xmerge && tiles >= 2 ? 2 : 1);
+  } else {
+    plan.depth = 1;
+  }
+  return plan;
+}
+
 int run_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                   uint16_t* out, int seqlen, const qd::AttnPlan& plan_in, hipStream_t stream,
                   int stages = qd::kStageScan | qd::kStageMerge) {
-  qd::AttnPlan plan = plan_in;
-  plan.xmerge = use_xmerge(ctx, plan, seqlen) ? 1 : 0;
+  const qd::AttnPlan plan = finish_plan(ctx, plan_in, seqlen);
   qd::AttnParams p = make_params(ctx, q, k, v, out, seqlen, plan);
   if (plan.xmerge && (stages & qd::kStageScan)) {
     // A fresh tag per call; tag 0 is never used, and after 2^32 calls, once
@@ -414,6 +435,8 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   ctx->xcnt_sum = 0u;
   ctx->merge_mode = QD_MERGE_AUTO;
   ctx->recompute_mask = 0u;
+  ctx->count_merges = 0;
+  ctx->scan_depth = 0;
   *out_ctx = ctx;
   return QD_OK;
 }
@@ -534,15 +557,18 @@ int qd_decode_attention_plan_detail(const qd_ctx* ctx, int seqlen, int entry, in
   if (entry < 0 || entry > 2) return fail(QD_EINVAL, "entry %d is not 0, 1 or 2", entry);
   if (entry == 2 && num_splits > qd::kMaxSplits)
     return fail(QD_EINVAL, "num_splits %d above the maximum %d", num_splits, qd::kMaxSplits);
-  const qd::AttnPlan p = entry == 0   ? plan_auto(ctx, seqlen)
-                         : entry == 1 ? plan_fused(seqlen)
-                                      : plan_split(ctx, seqlen, num_splits);
+  const qd::AttnPlan p = finish_plan(ctx,
+                                     entry == 0   ? plan_auto(ctx, seqlen)
+                                     : entry == 1 ? plan_fused(seqlen)
+                                                  : plan_split(ctx, seqlen, num_splits),
+                                     seqlen);
   plan->variant = p.variant;
   plan->num_splits = p.splits;
   plan->rows_per_split = p.rows_per_split;
   plan->rows_per_tile = p.rows_per_tile;
   plan->waves = p.waves;
-  plan->merge_in_kernel = use_xmerge(ctx, p, seqlen) ? 1 : 0;
+  plan->merge_in_kernel = p.xmerge;
+  plan->loads_per_round = p.depth;
   return QD_OK;
 }
 
@@ -557,6 +583,36 @@ int qd_ctx_set_merge(qd_ctx* ctx, int mode) {
 int qd_ctx_set_recompute_mask(qd_ctx* ctx, unsigned mask) {
   if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
   ctx->recompute_mask = mask;
+  return QD_OK;
+}
+
+int qd_ctx_set_scan_depth(qd_ctx* ctx, int depth) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  if (depth != 0 && depth != 1 && depth != 2 && depth != 4)
+    return fail(QD_EINVAL, "scan depth must be 0, 1, 2 or 4, got %d", depth);
+  ctx->scan_depth = depth;
+  return QD_OK;
+}
+
+int qd_ctx_count_xmerges(qd_ctx* ctx, int on) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  ctx->count_merges = on != 0;
+  return QD_OK;
+}
+
+int qd_ctx_xmerge_stats(const qd_ctx* ctx, unsigned long long* merges, unsigned long long* reads,
+                        unsigned long long* rescans) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  const int H = ctx->cfg.num_heads;
+  std::vector<unsigned> c((size_t)H * qd::kXCounterStride);
+  const hipError_t e = hipMemcpy(c.data(), ctx->xcnt, c.size() * sizeof(unsigned), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpy of the merge counters");
+  unsigned long long t[3] = {0ull, 0ull, 0ull};
+  for (int h = 0; h < H; ++h)
+    for (int i = 0; i < 3; ++i) t[i] += c[(size_t)h * qd::kXCounterStride + qd::kXStatMerges + i];
+  if (merges) *merges = t[0];
+  if (reads) *reads = t[1];
+  if (rescans) *rescans = t[2];
   return QD_OK;
 }
 
@@ -678,6 +734,7 @@ int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, cons
   p.cnt_base = 0u;
   p.tag = 0u;
   p.recompute_mask = 0u;
+  p.count_merges = 0;
   e = qd::launch_decode_attention(p, plan, stream);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return QD_OK;

@@ -84,13 +84,20 @@ struct AttnParams {
   unsigned cnt_base;
   unsigned tag;
   unsigned recompute_mask;
+  int count_merges;       // nonzero: add to the merge and read totals (rescans always)
 };
 
 // In-kernel merge limits: at most kXMaxSplits splits per head (the merge
-// reads them in one batch of loads); counters 128 bytes apart.
+// reads them in one batch of loads); counters 128 bytes apart.  Word 0 of a
+// head's counter block is its arrival counter; words kXStatMerges,
+// kXStatReads and kXStatRescans total its merges, reads of its slots and
+// splits scanned again (qd_ctx_xmerge_stats).
 constexpr int kXMaxSplits = 64;
 constexpr int kXCounterStride = 32;
 constexpr int kXSlotBytes = 1152;
+constexpr int kXStatMerges = 1;
+constexpr int kXStatReads = 2;
+constexpr int kXStatRescans = 3;
 
 struct RopeParams {
   uint16_t* qkv;          // [3][H][128]
@@ -217,6 +224,7 @@ struct AttnPlan {
   int rows_per_tile;      // rows per group per tile (template U)
   int waves;              // waves per split workgroup (4, 8 or 16)
   int xmerge;             // split plans: merge inside the scan kernel (one launch)
+  int depth;              // 4-wave split plans: tiles per load round (1, 2 or 4; same bits)
 };
 
 // Error reporting of the C ABI: records a printf-style message for
@@ -359,4 +367,6 @@ struct qd_ctx {
   int xmerge_ok;
   int merge_mode;
   unsigned recompute_mask;
+  int count_merges;
+  int scan_depth;         // 0: the planner's tiles per load round; else forced for split plans
 };

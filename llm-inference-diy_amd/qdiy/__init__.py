@@ -32,7 +32,7 @@ EXPORTS = (
     "qd_decode_attention_plan_detail", "qd_decode_attention_noalloc",
     # qdiy/bench.h
     "qd_decode_attention_stage", "qd_ctx_set_merge", "qd_ctx_set_recompute_mask",
-    "qd_ctx_xcd_period", "qd_xcd_placement",
+    "qd_ctx_xcd_period", "qd_xcd_placement", "qd_ctx_xmerge_stats", "qd_ctx_count_xmerges", "qd_ctx_set_scan_depth",
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
@@ -78,10 +78,12 @@ class AttnPlan(ctypes.Structure):
     """qd_attn_plan: the complete launch plan of one decode-attention call."""
     _fields_ = [("variant", ctypes.c_int), ("num_splits", ctypes.c_int),
                 ("rows_per_split", ctypes.c_int), ("rows_per_tile", ctypes.c_int),
-                ("waves", ctypes.c_int), ("merge_in_kernel", ctypes.c_int)]
+                ("waves", ctypes.c_int), ("merge_in_kernel", ctypes.c_int),
+                ("loads_per_round", ctypes.c_int)]
 
     def as_tuple(self):
-        """The plan fields that fix the output bits (merge_in_kernel does not)."""
+        """The plan fields that fix the output bits (merge_in_kernel and
+        loads_per_round do not)."""
         return (self.variant, self.num_splits, self.rows_per_split, self.rows_per_tile, self.waves)
 
 
@@ -110,6 +112,10 @@ def load() -> ctypes.CDLL:
     L.qd_ctx_set_merge.argtypes = [vp, i]
     L.qd_ctx_set_recompute_mask.argtypes = [vp, ctypes.c_uint]
     L.qd_ctx_xcd_period.argtypes = [vp, ctypes.POINTER(i)]
+    ull_p = ctypes.POINTER(ctypes.c_ulonglong)
+    L.qd_ctx_xmerge_stats.argtypes = [vp, ull_p, ull_p, ull_p]
+    L.qd_ctx_count_xmerges.argtypes = [vp, i]
+    L.qd_ctx_set_scan_depth.argtypes = [vp, i]
     L.qd_xcd_placement.argtypes = [ctypes.POINTER(ctypes.c_uint), i]
     L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
     L.qd_decode_attention_plan_detail.argtypes = [vp, i, i, i, ctypes.POINTER(AttnPlan)]
@@ -215,6 +221,21 @@ class Context:
     def set_recompute_mask(self, mask: int) -> None:
         """qd_ctx_set_recompute_mask (test hook of the in-kernel merge)."""
         _check(load().qd_ctx_set_recompute_mask(self._h, mask & 0xFFFFFFFF))
+
+    def set_scan_depth(self, depth: int) -> None:
+        """qd_ctx_set_scan_depth: tiles per load round of split plans (0: planner's)."""
+        _check(load().qd_ctx_set_scan_depth(self._h, depth))
+
+    def count_xmerges(self, on: bool = True) -> None:
+        """qd_ctx_count_xmerges: count merges and slot reads (off by default)."""
+        _check(load().qd_ctx_count_xmerges(self._h, int(on)))
+
+    def xmerge_stats(self) -> tuple:
+        """qd_ctx_xmerge_stats: (heads merged, reads of their slots, splits scanned
+        again) over the context's in-kernel merges so far."""
+        m, r, x = ctypes.c_ulonglong(), ctypes.c_ulonglong(), ctypes.c_ulonglong()
+        _check(load().qd_ctx_xmerge_stats(self._h, ctypes.byref(m), ctypes.byref(r), ctypes.byref(x)))
+        return m.value, r.value, x.value
 
     def xcd_period(self) -> int:
         """qd_ctx_xcd_period: round-robin period of workgroup dispatch (0: not round-robin)."""

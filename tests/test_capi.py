@@ -83,6 +83,17 @@ def test_engine_cli_rejects_bad_options_before_any_gpu_work(qdiy):
         assert msg in res.stderr
 
 
+def test_bench_hooks_reject_bad_arguments(qdiy):
+    """Test and measurement hooks (qdiy/bench.h) check their arguments before
+    any GPU work."""
+    lib = qdiy.load()
+    assert lib.qd_ctx_set_scan_depth(None, 1) == qdiy.QD_EINVAL
+    assert lib.qd_ctx_count_xmerges(None, 1) == qdiy.QD_EINVAL
+    assert lib.qd_ctx_xmerge_stats(None, None, None, None) == qdiy.QD_EINVAL
+    assert lib.qd_ctx_set_merge(None, 0) == qdiy.QD_EINVAL
+    assert lib.qd_ctx_set_recompute_mask(None, 1) == qdiy.QD_EINVAL
+
+
 def test_version_and_limits(qdiy):
     assert re.match(r"^\d+\.\d+\.\d+$", qdiy.version())
     assert qdiy.max_splits() >= 64

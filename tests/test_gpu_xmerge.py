@@ -188,3 +188,54 @@ def test_stage_hook_with_in_kernel_merge(qdiy):
                 assert np.all(o == np.float16(7.0))
             else:
                 _same(o, expect, "scan stage")
+
+
+@pytest.mark.parametrize("L", [300, 768, 1280, 3000, 8192, 20000])
+def test_loads_per_round_give_the_same_bits(qdiy, L):
+    """A wave may issue the loads of 1, 2 or 4 of its tiles before consuming
+    them in order: the arithmetic is the same, so is every output bit, with the
+    merge in the kernel or in a merge kernel.  The planner's own choice (two
+    tiles per round with the merge in the kernel where a wave has two or more)
+    is what plan_detail reports."""
+    H = 16
+    case = AttnCase(L, H=H, seed=L + 1, kscale=0.5)
+    t = _upload(case)
+    with qdiy.Context(num_heads=H, max_seqlen=L) as ctx:
+        want = _oracle(case, ctx, L)
+        for mode in (qdiy.MERGE_IN_KERNEL, qdiy.MERGE_TWO_LAUNCHES):
+            ctx.set_merge(mode)
+            plan = ctx.plan_detail(L)
+            tiles = -(-plan.rows_per_split // (16 * plan.rows_per_tile))
+            auto = 2 if plan.merge_in_kernel and tiles >= 2 else 1
+            assert plan.loads_per_round == auto, (L, mode, plan.as_tuple(), plan.loads_per_round)
+            _same(_attend(ctx, t, L, H), want, f"L={L} mode={mode}, planner's depth {auto}")
+            for depth in (1, 2, 4):
+                ctx.set_scan_depth(depth)
+                assert ctx.plan_detail(L).loads_per_round == depth
+                _same(_attend(ctx, t, L, H), want, f"L={L} mode={mode} depth={depth}")
+            ctx.set_scan_depth(0)
+
+
+def test_merge_statistics(qdiy):
+    """qd_ctx_xmerge_stats: with counting on, one merge per head per call and at
+    least one read of the slots per merge; splits the test hook marks are
+    counted as scanned again whether or not counting is on."""
+    H, L = 16, 2000
+    case = AttnCase(L, H=H, seed=11, kscale=0.5)
+    t = _upload(case)
+    with qdiy.Context(num_heads=H, max_seqlen=L) as ctx:
+        ctx.set_merge(qdiy.MERGE_IN_KERNEL)
+        splits = ctx.plan_detail(L).num_splits
+        assert ctx.xmerge_stats() == (0, 0, 0)
+        _attend(ctx, t, L, H)
+        assert ctx.xmerge_stats()[:2] == (0, 0)          # counting is off by default
+        ctx.count_xmerges(True)
+        for _ in range(3):
+            _attend(ctx, t, L, H)
+        merges, reads, rescans = ctx.xmerge_stats()
+        assert merges == 3 * H and reads >= merges and rescans == 0
+        ctx.count_xmerges(False)
+        ctx.set_recompute_mask(0b101)                     # splits 0 and 2 of each head
+        _attend(ctx, t, L, H)
+        m2, r2, x2 = ctx.xmerge_stats()
+        assert (m2, r2) == (merges, reads) and x2 == 2 * H, (m2, r2, x2, splits)
