@@ -83,6 +83,12 @@ def lib() -> ctypes.CDLL:
         L.qd_oracle_generate.restype = i
         L.qd_oracle_model_new.argtypes = [vp, ll, i, i]
         L.qd_oracle_model_new.restype = vp
+        L.qd_oracle_model_new_order.argtypes = [vp, ll, i, i, i]
+        L.qd_oracle_model_new_order.restype = vp
+        L.qd_oracle_swiglu_ref.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
+        L.qd_oracle_swiglu_ref.restype = ctypes.c_uint16
+        L.qd_oracle_argmax_ref.argtypes = [u16p, i]
+        L.qd_oracle_argmax_ref.restype = i
         L.qd_oracle_model_free.argtypes = [vp]
         L.qd_oracle_model_forward.argtypes = [vp, i, i, ctypes.POINTER(Plan), i, u16p]
         L.qd_oracle_model_forward.restype = i
@@ -265,6 +271,18 @@ def swiglu(g, u) -> np.float16:
     return np.uint16(r).view(np.float16)
 
 
+def swiglu_ref(g, u) -> np.float16:
+    """The reference's SwiGLU of two fp16 scalars (swiglu.cuh:11-13, expf)."""
+    r = lib().qd_oracle_swiglu_ref(int(np.float16(g).view(np.uint16)), int(np.float16(u).view(np.uint16)))
+    return np.uint16(r).view(np.float16)
+
+
+def argmax_ref(logits) -> int:
+    """argmax_kernel's token for fp16 logits, its tie order included."""
+    lg = np.ascontiguousarray(logits, dtype=np.float16)
+    return lib().qd_oracle_argmax_ref(_u16(lg), lg.size)
+
+
 def ffn_up_swiglu(x, norm_w, W1, W2, hidden, inter, eps=1e-6, nthreads=4):
     x = np.ascontiguousarray(x, dtype=np.float16)
     norm_w = np.ascontiguousarray(norm_w, dtype=np.float16)
@@ -306,21 +324,26 @@ def generate(image, prompt, n_new, plans, stop_at_eos=False, nthreads=8):
 
 
 class Model:
-    """Stateful oracle model over a .bin image: forward(token, pos, plan)."""
+    """Stateful oracle model over a .bin image: forward(token, pos, plan).  order
+    ORDER_WAVE64 restates this build's kernels (plan: the library's attention
+    plan at length pos + 1); ORDER_REF the reference kernels' own arithmetic
+    (the plan is not used)."""
 
-    def __init__(self, image, max_pos, nthreads=8):
+    def __init__(self, image, max_pos, nthreads=8, order=None):
         self._img = np.ascontiguousarray(image).view(np.uint8)       # kept alive
         self.vocab = int(np.frombuffer(self._img[:28].tobytes(), np.uint32)[1])
-        self._h = lib().qd_oracle_model_new(self._img.ctypes.data_as(ctypes.c_void_p), self._img.size,
-                                            max_pos, nthreads)
+        order = ORDER_WAVE64 if order is None else order
+        self._h = lib().qd_oracle_model_new_order(self._img.ctypes.data_as(ctypes.c_void_p),
+                                                  self._img.size, max_pos, nthreads, order)
         if not self._h:
             raise ValueError("qd_oracle_model_new rejected its arguments")
 
-    def forward(self, token, pos, plan, want_logits=True):
+    def forward(self, token, pos, plan=None, want_logits=True):
         """Next token and logits (want_logits) or None."""
         logits = np.zeros(self.vocab, np.float16) if want_logits else None
-        r = lib().qd_oracle_model_forward(self._h, int(token), pos, ctypes.byref(plan), int(want_logits),
-                                          _u16(logits) if want_logits else None)
+        r = lib().qd_oracle_model_forward(self._h, int(token), pos,
+                                          None if plan is None else ctypes.byref(plan),
+                                          int(want_logits), _u16(logits) if want_logits else None)
         if r < 0:
             raise ValueError("qd_oracle_model_forward rejected its arguments")
         return (r, logits) if want_logits else None

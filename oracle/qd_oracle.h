@@ -173,6 +173,14 @@ void qd_oracle_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float ep
                              const uint16_t* w1, const uint16_t* w2, uint16_t* act, int hidden,
                              int inter, int nthreads);
 
+/* The reference's SwiGLU of two fp16 values, half(g * (u / (1 + expf(-u))))
+ * (swiglu.cuh:11-13 with glibc expf for __expf). */
+uint16_t qd_oracle_swiglu_ref(uint16_t g, uint16_t u);
+
+/* argmax_kernel<<<1, 512>>> over vocab fp16 logits (argmax.cuh:7-72), its tie
+ * order included; -1 when no value exceeds -inf. */
+int qd_oracle_argmax_ref(const uint16_t* logits, int vocab);
+
 /* logits[v] = half(W[v] . xn) (logits may be NULL); returns the argmax, ties
  * to the lowest index, -0 == +0, NaN never wins: qwen_infer.cu:725-731. */
 int qd_oracle_lm_head_argmax(const uint16_t* x, const uint16_t* norm_w, float eps,
@@ -184,6 +192,14 @@ int qd_oracle_lm_head_argmax(const uint16_t* x, const uint16_t* norm_w, float ep
  * max_pos positions.  NULL on invalid arguments. */
 typedef struct qd_oracle_model qd_oracle_model;
 qd_oracle_model* qd_oracle_model_new(const void* image, long long bytes, int max_pos, int nthreads);
+
+/* The same with the arithmetic `order` of every op: QD_ORDER_WAVE64 (as
+ * qd_oracle_model_new: this build's kernels) or QD_ORDER_REF (the reference
+ * kernels' own: 512-thread RMSNorm, GEMV sums with k ascending, the engine's
+ * attention dispatch of qd_oracle_decode_attention, SwiGLU with expf, and
+ * argmax_kernel's tie order).  Forward then ignores `plan` (may be NULL). */
+qd_oracle_model* qd_oracle_model_new_order(const void* image, long long bytes, int max_pos,
+                                           int nthreads, int order);
 void qd_oracle_model_free(qd_oracle_model* m);
 
 /* One token through all layers at `pos` (KV rows written), attention under

@@ -22,6 +22,17 @@
  * qd_oracle_exp2(-u * log2 e) instead of __expf, and argmax ties broken by the
  * lowest index.  Each of those is pinned on its own in tests/ against the
  * reference-order functions and float64.
+ *
+ * A model made with order QD_ORDER_REF instead follows the reference kernels'
+ * own arithmetic throughout: the 512-thread RMSNorm (rmsnorm.cuh:15-45), GEMV
+ * sums with k ascending (hgemm_final.cuh:278-293), the engine's attention
+ * dispatch with fp16 partials (qd_oracle_decode_attention, QD_ORACLE_ENGINE:
+ * qwen_infer.cu:646-678), SwiGLU as w1 * (w2 / (1 + exp(-w2)))
+ * (swiglu.cuh:11-13, with glibc expf and an IEEE division where the
+ * reference's fast-math build uses __expf and an approximate division), and
+ * argmax_kernel's tie order (argmax.cuh:7-72: per-thread chunks of
+ * ceil(V/512) ids, first maximum in a chunk, then xor-butterflies that keep
+ * their own value on ties).
  */
 #include <math.h>
 #include <pthread.h>
@@ -166,12 +177,22 @@ static float row_wave64(const float* xf, const uint16_t* w_row, int K, const flo
   return qd_oracle_wave64_sum(lanes);
 }
 
+/* sum_k xf[k] * W[row][k] with k ascending, one rounding per add: the
+ * reference's hgemv_kernel (hgemm_final.cuh:278-293; products of two fp16
+ * values are exact in fp32, so contraction cannot change them). */
+static float row_seq(const float* xf, const uint16_t* w_row, int K, const float* T) {
+  float s = 0.0f;
+  for (int k = 0; k < K; ++k) s += xf[k] * T[w_row[k]];
+  return s;
+}
+
 typedef struct {
   const float* xf;
   const uint16_t* W;
   int K;
   float* out;           /* fp32 row sums */
   int rows_per_task, n;
+  int order;            /* QD_ORDER_WAVE64 or QD_ORDER_REF */
 } gemv_job;
 
 static void gemv_task(void* a, int t) {
@@ -179,13 +200,17 @@ static void gemv_task(void* a, int t) {
   const float* T = h2f_table();
   const int b = t * j->rows_per_task;
   const int e = b + j->rows_per_task < j->n ? b + j->rows_per_task : j->n;
-  for (int r = b; r < e; ++r) j->out[r] = row_wave64(j->xf, j->W + (long long)r * j->K, j->K, T);
+  for (int r = b; r < e; ++r)
+    j->out[r] = j->order == QD_ORDER_REF ? row_seq(j->xf, j->W + (long long)r * j->K, j->K, T)
+                                         : row_wave64(j->xf, j->W + (long long)r * j->K, j->K, T);
 }
 
-static void gemv_sums(pool* p, const float* xf, const uint16_t* W, int N, int K, float* out) {
-  gemv_job j = {xf, W, K, out, 64, N};
+static void gemv_sums_order(pool* p, const float* xf, const uint16_t* W, int N, int K, float* out,
+                            int order) {
+  gemv_job j = {xf, W, K, out, 64, N, order};
   pool_run(p, gemv_task, &j, (N + 63) / 64);
 }
+
 
 static void to_float(const uint16_t* h, float* f, int n) {
   const float* T = h2f_table();
@@ -196,11 +221,12 @@ static void to_float(const uint16_t* h, float* f, int n) {
 /* Decode-step ops                                                           */
 
 static void proj_residual_pool(pool* p, const uint16_t* x, const uint16_t* W,
-                               const uint16_t* residual, uint16_t* out, int n_out, int k_in) {
+                               const uint16_t* residual, uint16_t* out, int n_out, int k_in,
+                               int order) {
   float* xf = (float*)malloc(sizeof(float) * (size_t)k_in);
   float* s = (float*)malloc(sizeof(float) * (size_t)n_out);
   to_float(x, xf, k_in);
-  gemv_sums(p, xf, W, n_out, k_in, s);
+  gemv_sums_order(p, xf, W, n_out, k_in, s, order);
   for (int n = 0; n < n_out; ++n)
     out[n] = qd_oracle_f2h(qd_oracle_h2f(residual[n]) + qd_oracle_h2f(qd_oracle_f2h(s[n])));
   free(s);
@@ -215,18 +241,27 @@ static uint16_t swiglu(float gsum, float usum) {
   return qd_oracle_f2h(g * silu);
 }
 
+/* swiglu.cuh:11-13: out = half(w1 * (w2 / (1 + exp(-w2)))) of the fp16 GEMV
+ * outputs, exp as glibc expf. */
+static uint16_t swiglu_ref(float gsum, float usum) {
+  const float g = qd_oracle_h2f(qd_oracle_f2h(gsum));
+  const float u = qd_oracle_h2f(qd_oracle_f2h(usum));
+  const float silu = u / (1.0f + expf(-u));
+  return qd_oracle_f2h(g * silu);
+}
+
 static void ffn_up_pool(pool* p, const uint16_t* x, const uint16_t* norm_w, float eps,
                         const uint16_t* w1, const uint16_t* w2, uint16_t* act, int hidden,
-                        int inter) {
+                        int inter, int order) {
   uint16_t* xn = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)hidden);
   float* xf = (float*)malloc(sizeof(float) * (size_t)hidden);
   float* g = (float*)malloc(sizeof(float) * (size_t)inter);
   float* u = (float*)malloc(sizeof(float) * (size_t)inter);
-  qd_oracle_rmsnorm(x, norm_w, hidden, eps, xn, QD_ORDER_WAVE64);
+  qd_oracle_rmsnorm(x, norm_w, hidden, eps, xn, order);
   to_float(xn, xf, hidden);
-  gemv_sums(p, xf, w1, inter, hidden, g);
-  gemv_sums(p, xf, w2, inter, hidden, u);
-  for (int i = 0; i < inter; ++i) act[i] = swiglu(g[i], u[i]);
+  gemv_sums_order(p, xf, w1, inter, hidden, g, order);
+  gemv_sums_order(p, xf, w2, inter, hidden, u, order);
+  for (int i = 0; i < inter; ++i) act[i] = order == QD_ORDER_REF ? swiglu_ref(g[i], u[i]) : swiglu(g[i], u[i]);
   free(u);
   free(g);
   free(xf);
@@ -241,14 +276,88 @@ static unsigned long long argmax_key(uint16_t b, int row) {
   return ((unsigned long long)k << 32) | (unsigned long long)(0xFFFFFFFFu - (unsigned)row);
 }
 
+/* argmax_kernel<<<1, 512>>> (argmax.cuh:7-72): thread t scans ids
+ * [t*c, t*c + c), c = ceil(V/512), keeping the first strictly larger value;
+ * each 32-lane warp then runs xor-butterflies (masks 16..1) in which a lane
+ * takes its partner's (value, id) only when strictly larger; warp w's lane 0
+ * result goes to slot w, and warp 0 repeats the butterfly over slots 0..15
+ * (-inf, id -1 beyond).  Thread 0's id is the token.  NaN never wins (every
+ * comparison with it is false); -1 if no value exceeds -inf. */
+static int argmax_ref(const uint16_t* logits, int vocab) {
+  enum { kThreads = 512, kWarps = 16 };
+  const int c = (vocab + kThreads - 1) / kThreads;
+  float val[kThreads];
+  int idx[kThreads];
+  for (int t = 0; t < kThreads; ++t) {
+    val[t] = -INFINITY;
+    idx[t] = -1;
+    for (int i = 0; i < c; ++i) {
+      const int id = t * c + i;
+      if (id < vocab) {
+        const float v = qd_oracle_h2f(logits[id]);
+        if (v > val[t]) { val[t] = v; idx[t] = id; }
+      }
+    }
+  }
+  float sv[32];
+  int si[32];
+  for (int w = 0; w < kWarps; ++w) {
+    float* v = val + 32 * w;
+    int* x = idx + 32 * w;
+    for (int mask = 16; mask >= 1; mask >>= 1) {
+      float nv[32];
+      int ni[32];
+      for (int l = 0; l < 32; ++l) {
+        nv[l] = v[l]; ni[l] = x[l];
+        if (v[l ^ mask] > v[l]) { nv[l] = v[l ^ mask]; ni[l] = x[l ^ mask]; }
+      }
+      memcpy(v, nv, sizeof(nv));
+      memcpy(x, ni, sizeof(ni));
+    }
+    sv[w] = v[0];
+    si[w] = x[0];
+  }
+  for (int l = kWarps; l < 32; ++l) { sv[l] = -INFINITY; si[l] = -1; }
+  for (int mask = 16; mask >= 1; mask >>= 1) {
+    float nv[32];
+    int ni[32];
+    for (int l = 0; l < 32; ++l) {
+      nv[l] = sv[l]; ni[l] = si[l];
+      if (sv[l ^ mask] > sv[l]) { nv[l] = sv[l ^ mask]; ni[l] = si[l ^ mask]; }
+    }
+    memcpy(sv, nv, sizeof(nv));
+    memcpy(si, ni, sizeof(ni));
+  }
+  return si[0];
+}
+
+int qd_oracle_argmax_ref(const uint16_t* logits, int vocab) {
+  if (!logits || vocab < 1) return -1;
+  return argmax_ref(logits, vocab);
+}
+
+uint16_t qd_oracle_swiglu_ref(uint16_t g, uint16_t u) {
+  return swiglu_ref(qd_oracle_h2f(g), qd_oracle_h2f(u));
+}
+
 static int lm_head_pool(pool* p, const uint16_t* x, const uint16_t* norm_w, float eps,
-                        const uint16_t* W, uint16_t* logits, int vocab, int hidden) {
+                        const uint16_t* W, uint16_t* logits, int vocab, int hidden, int order) {
   uint16_t* xn = (uint16_t*)malloc(sizeof(uint16_t) * (size_t)hidden);
   float* xf = (float*)malloc(sizeof(float) * (size_t)hidden);
   float* s = (float*)malloc(sizeof(float) * (size_t)vocab);
-  qd_oracle_rmsnorm(x, norm_w, hidden, eps, xn, QD_ORDER_WAVE64);
+  qd_oracle_rmsnorm(x, norm_w, hidden, eps, xn, order);
   to_float(xn, xf, hidden);
-  gemv_sums(p, xf, W, vocab, hidden, s);
+  gemv_sums_order(p, xf, W, vocab, hidden, s, order);
+  if (order == QD_ORDER_REF) {
+    uint16_t* lg = logits ? logits : (uint16_t*)malloc(sizeof(uint16_t) * (size_t)vocab);
+    for (int v = 0; v < vocab; ++v) lg[v] = qd_oracle_f2h(s[v]);
+    const int t = argmax_ref(lg, vocab);
+    if (!logits) free(lg);
+    free(s);
+    free(xf);
+    free(xn);
+    return t;
+  }
   unsigned long long best = 0;
   for (int v = 0; v < vocab; ++v) {
     const uint16_t h = qd_oracle_f2h(s[v]);
@@ -265,7 +374,7 @@ static int lm_head_pool(pool* p, const uint16_t* x, const uint16_t* norm_w, floa
 void qd_oracle_proj_residual(const uint16_t* x, const uint16_t* W, const uint16_t* residual,
                              uint16_t* out, int n_out, int k_in, int nthreads) {
   pool* p = pool_new(nthreads);
-  proj_residual_pool(p, x, W, residual, out, n_out, k_in);
+  proj_residual_pool(p, x, W, residual, out, n_out, k_in, QD_ORDER_WAVE64);
   pool_free(p);
 }
 
@@ -273,7 +382,7 @@ void qd_oracle_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float ep
                              const uint16_t* w1, const uint16_t* w2, uint16_t* act, int hidden,
                              int inter, int nthreads) {
   pool* p = pool_new(nthreads);
-  ffn_up_pool(p, x, norm_w, eps, w1, w2, act, hidden, inter);
+  ffn_up_pool(p, x, norm_w, eps, w1, w2, act, hidden, inter, QD_ORDER_WAVE64);
   pool_free(p);
 }
 
@@ -285,7 +394,7 @@ int qd_oracle_lm_head_argmax(const uint16_t* x, const uint16_t* norm_w, float ep
                              const uint16_t* W, uint16_t* logits, int vocab, int hidden,
                              int nthreads) {
   pool* p = pool_new(nthreads);
-  const int t = lm_head_pool(p, x, norm_w, eps, W, logits, vocab, hidden);
+  const int t = lm_head_pool(p, x, norm_w, eps, W, logits, vocab, hidden, QD_ORDER_WAVE64);
   pool_free(p);
   return t;
 }
@@ -307,6 +416,7 @@ struct qd_oracle_model {
   uint16_t *kc, *vc, *x, *qkv, *attn, *act, *xn, *logits;
   float *xf, *sums;
   pool* p;
+  int order;                    /* QD_ORDER_WAVE64 or QD_ORDER_REF */
 };
 
 void qd_oracle_model_free(qd_oracle_model* m) {
@@ -327,7 +437,13 @@ void qd_oracle_model_free(qd_oracle_model* m) {
 }
 
 qd_oracle_model* qd_oracle_model_new(const void* image, long long bytes, int max_pos, int nthreads) {
+  return qd_oracle_model_new_order(image, bytes, max_pos, nthreads, QD_ORDER_WAVE64);
+}
+
+qd_oracle_model* qd_oracle_model_new_order(const void* image, long long bytes, int max_pos,
+                                           int nthreads, int order) {
   if (!image || bytes < 28 || max_pos < 1) return NULL;
+  if (order != QD_ORDER_WAVE64 && order != QD_ORDER_REF) return NULL;
   uint32_t hdr[7];
   memcpy(hdr, image, sizeof(hdr));
   if (hdr[0] != 0x46445751u) return NULL;
@@ -337,7 +453,7 @@ qd_oracle_model* qd_oracle_model_new(const void* image, long long bytes, int max
   if (bytes != 28 + 2 * (V * H + NL * per_layer + H + V * H) || max_pos > (int)hdr[6]) return NULL;
   qd_oracle_model* m = (qd_oracle_model*)calloc(1, sizeof(qd_oracle_model));
   if (!m) return NULL;
-  m->V = V; m->H = H; m->NL = NL; m->NH = NH; m->I = I; m->max_pos = max_pos;
+  m->V = V; m->H = H; m->NL = NL; m->NH = NH; m->I = I; m->max_pos = max_pos; m->order = order;
   m->t = (const uint16_t*)((const char*)image + 28);
   m->lo = (layer_off*)malloc(sizeof(layer_off) * (size_t)NL);
   long long o = V * H;
@@ -376,7 +492,10 @@ qd_oracle_model* qd_oracle_model_new(const void* image, long long bytes, int max
 
 int qd_oracle_model_forward(qd_oracle_model* m, int token, int pos, const qd_oracle_plan* plan,
                             int want_logits, uint16_t* logits_out) {
-  if (!m || !plan || token < 0 || token >= m->V || pos < 0 || pos >= m->max_pos) return -1;
+  if (!m || (!plan && m->order != QD_ORDER_REF) || token < 0 || token >= m->V || pos < 0 ||
+      pos >= m->max_pos)
+    return -1;
+  const int order = m->order;
   const long long H = m->H, NH = m->NH, I = m->I;
   const float eps = 1e-6f;
   const uint16_t* t = m->t;
@@ -386,20 +505,25 @@ int qd_oracle_model_forward(qd_oracle_model* m, int token, int pos, const qd_ora
     uint16_t* K = m->kc + l * m->layer_cache;
     uint16_t* Vv = m->vc + l * m->layer_cache;
     /* front end: RMSNorm(ln_1), QKV GEMV, bias, RoPE, append (:626-642) */
-    qd_oracle_rmsnorm(xin, t + f->ln_1, (int)H, eps, m->xn, QD_ORDER_WAVE64);
+    qd_oracle_rmsnorm(xin, t + f->ln_1, (int)H, eps, m->xn, order);
     to_float(m->xn, m->xf, (int)H);
-    gemv_sums(m->p, m->xf, t + f->qkv_w, (int)(3 * H), (int)H, m->sums);
+    gemv_sums_order(m->p, m->xf, t + f->qkv_w, (int)(3 * H), (int)H, m->sums, order);
     for (long long n = 0; n < 3 * H; ++n) m->qkv[n] = qd_oracle_f2h(m->sums[n]);
     qd_oracle_qkv_bias_rope_cache(m->qkv, t + f->qkv_b, K, Vv, pos, (int)NH, 128, H, 128, 10000.0f);
-    if (qd_oracle_attention_planned(m->qkv, K, Vv, m->attn, pos + 1, (int)NH, H, 128, plan, 1) != 0)
-      return -1;
-    proj_residual_pool(m->p, m->attn, t + f->proj_w, xin, m->x, (int)H, (int)H);
-    ffn_up_pool(m->p, m->x, t + f->ln_2, eps, t + f->w1, t + f->w2, m->act, (int)H, (int)I);
-    proj_residual_pool(m->p, m->act, t + f->w_down, m->x, m->x, (int)H, (int)I);
+    const int rc = order == QD_ORDER_REF
+                       ? qd_oracle_decode_attention(m->qkv, K, Vv, m->attn, pos + 1, (int)NH, H, 128,
+                                                    QD_ORACLE_ENGINE, 1)
+                       : qd_oracle_attention_planned(m->qkv, K, Vv, m->attn, pos + 1, (int)NH, H, 128,
+                                                     plan, 1);
+    if (rc != 0) return -1;
+    proj_residual_pool(m->p, m->attn, t + f->proj_w, xin, m->x, (int)H, (int)H, order);
+    ffn_up_pool(m->p, m->x, t + f->ln_2, eps, t + f->w1, t + f->w2, m->act, (int)H, (int)I, order);
+    proj_residual_pool(m->p, m->act, t + f->w_down, m->x, m->x, (int)H, (int)I, order);
     xin = m->x;
   }
   if (!want_logits) return 0;
-  const int next = lm_head_pool(m->p, m->x, m->ln_f, eps, m->lm_head, m->logits, (int)m->V, (int)H);
+  const int next =
+      lm_head_pool(m->p, m->x, m->ln_f, eps, m->lm_head, m->logits, (int)m->V, (int)H, order);
   if (logits_out) memcpy(logits_out, m->logits, sizeof(uint16_t) * (size_t)m->V);
   return next;
 }
