@@ -90,6 +90,20 @@ int qd_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps, const
 int qd_gemm_nt(const uint16_t* x, long long ldx, const uint16_t* w, const uint16_t* residual,
                uint16_t* y, long long ldy, int m, int n, int k, int mode, hipStream_t stream);
 
+/* Batched FFN up-projection of m prompt rows on the matrix cores, gate and up
+ * GEMMs in one pass with the SwiGLU in the epilogue:
+ *   act[i][j] = half(g * (u / (1 + exp(-u)))),  g = half(x[i] . w1[j]),
+ *                                              u = half(x[i] . w2[j])
+ * for i < m, j < n (x rows ldx apart, act rows ldy apart; w1 and w2 [n][k]).
+ * Replaces the prompt's w1 and w2 gemms and swiglu_kernel
+ * (qwen_infer.cu:573-586).  exp(-u) is this library's exp2 of -u * log2(e)
+ * (as qd_ffn_up_swiglu); the sums are fp32 in the hardware's order, as in
+ * QD_GEMM_MFMA.  k a positive multiple of 64; x, w1 and w2 16-byte aligned,
+ * ldx a multiple of 8 and >= k, ldy >= n, act 2-byte aligned and not
+ * overlapping x, w1 or w2. */
+int qd_gemm_swiglu(const uint16_t* x, long long ldx, const uint16_t* w1, const uint16_t* w2,
+                   uint16_t* act, long long ldy, int m, int n, int k, hipStream_t stream);
+
 /* Causal attention of `tokens` prompt queries at positions pos0 .. pos0 +
  * tokens - 1 of one layer, all heads: query t attends over cache rows
  * [0, pos0 + t] (rows written beforehand, K rotated).  Query t's row is

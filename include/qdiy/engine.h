@@ -112,6 +112,14 @@ int qd_engine_step(qd_engine* eng, int token, int pos, int* next_token);
 /* Copies the last step's vocab_size fp16 logits to host memory. */
 int qd_engine_logits(qd_engine* eng, uint16_t* host_logits);
 
+/* Copies KV-cache rows [pos0, pos0 + n) of `layer` to host memory: n x
+ * hidden_size fp16 values of K (rotated) and of V, after the engine's queued
+ * work.  The reference engine keeps its caches as members a test or tool can
+ * read (d_kv_cache_k / d_kv_cache_v, qwen_infer.cu:245-249); this is that
+ * access.  Either pointer may be NULL. */
+int qd_engine_kv_rows(qd_engine* eng, int layer, int pos0, int n, uint16_t* host_k,
+                      uint16_t* host_v);
+
 /* main()'s per-request loop (qwen_infer.cu:780-817) without the printing:
  * prefill prompt[0..n_prompt-2] from position 0, then greedy steps from the
  * last prompt token, writing up to max_new tokens to out_tokens.  With

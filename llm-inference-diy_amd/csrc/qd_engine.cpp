@@ -366,6 +366,26 @@ int qd_gemm_nt(const uint16_t* x, long long ldx, const uint16_t* w, const uint16
   return e == hipSuccess ? QD_OK : hip_fail(e, "gemm launch");
 }
 
+int qd_gemm_swiglu(const uint16_t* x, long long ldx, const uint16_t* w1, const uint16_t* w2,
+                   uint16_t* act, long long ldy, int m, int n, int k, hipStream_t stream) {
+  if (!x || !w1 || !w2 || !act) return fail(QD_EINVAL, "x, w1, w2 and act must be non-NULL");
+  if (m < 1 || n < 1) return fail(QD_EINVAL, "m %d and n %d must be >= 1", m, n);
+  if (k < 64 || k % 64 != 0) return fail(QD_EINVAL, "k %d must be a positive multiple of 64", k);
+  if (ldx < k || ldx % 8 != 0 || ldy < n)
+    return fail(QD_EINVAL, "ldx %lld must be a multiple of 8 and at least k, ldy %lld at least n", ldx, ldy);
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(w2))
+    return fail(QD_EINVAL, "x, w1 and w2 must be 16-byte aligned");
+  if (!aligned2(act)) return fail(QD_EINVAL, "act must be 2-byte aligned");
+  const size_t ab = ((size_t)(m - 1) * ldy + n) * 2, wb = (size_t)n * k * 2;
+  if (overlaps(act, ab, x, ((size_t)(m - 1) * ldx + k) * 2) || overlaps(act, ab, w1, wb) ||
+      overlaps(act, ab, w2, wb))
+    return fail(QD_EINVAL, "act overlaps x, w1 or w2");
+  qd::BatchedGemvParams p{x, ldx, w1, n, k, m, act, ldy, nullptr};
+  p.w2 = w2;
+  const hipError_t e = qd::launch_gemm_mfma_swiglu(p, stream);
+  return e == hipSuccess ? QD_OK : hip_fail(e, "gate/up GEMM launch");
+}
+
 size_t qd_lm_head_workspace_bytes(int vocab) {
   return vocab < 1 ? 0 : (size_t)qd::lm_head_parts(vocab) * sizeof(unsigned long long);
 }
@@ -644,6 +664,19 @@ int qd_engine_logits(qd_engine* e, uint16_t* host_logits) {
   if (!host_logits) return fail(QD_EINVAL, "host_logits is NULL");
   hipError_t he = hipMemcpy(host_logits, e->logits, (size_t)e->cfg.vocab_size * 2, hipMemcpyDeviceToHost);
   return he == hipSuccess ? QD_OK : hip_fail(he, "logits copy");
+}
+
+int qd_engine_kv_rows(qd_engine* e, int layer, int pos0, int n, uint16_t* host_k, uint16_t* host_v) {
+  int rc = check_engine(e);
+  if (rc != QD_OK) return rc;
+  if (layer < 0 || layer >= e->cfg.num_layers || pos0 < 0 || n < 0 || pos0 + n > e->cfg.max_seqlen)
+    return fail(QD_EINVAL, "rows [%d, %d) of layer %d outside the cache (%d layers, %d rows)", pos0,
+                pos0 + n, layer, e->cfg.num_layers, e->cfg.max_seqlen);
+  hipError_t he = hipStreamSynchronize(e->stream);
+  const size_t off = (size_t)pos0 * e->cfg.hidden_size, bytes = (size_t)n * e->cfg.hidden_size * 2;
+  if (he == hipSuccess && host_k && n) he = hipMemcpy(host_k, e->kc(layer) + off, bytes, hipMemcpyDeviceToHost);
+  if (he == hipSuccess && host_v && n) he = hipMemcpy(host_v, e->vc(layer) + off, bytes, hipMemcpyDeviceToHost);
+  return he == hipSuccess ? QD_OK : hip_fail(he, "KV rows copy");
 }
 
 int qd_engine_generate(qd_engine* e, const int* prompt, int n_prompt, int max_new, int stop_at_eos,

@@ -33,8 +33,13 @@ constexpr float kLog2e = 1.44269504088896340736f;
 // Tokens per workgroup of the batched GEMV; tokens per LDS tile (up to 8, so
 // that a tile of NJ * 512 fp16 elements per token stays within 64 KB).
 constexpr int kTokPerWg = 32;
-constexpr int kGemvWaves = 8;           // two rows per wave: 16 rows per workgroup
 constexpr int tok_tile(int nj) { return nj <= 8 ? 8 : 64 / nj; }
+// Waves per workgroup, two rows each.  From NJ = 15 (K > 7168) the weights
+// (16 * NJ VGPRs) and the unrolled sums no longer fit the 256 VGPRs a wave has
+// at two waves per SIMD, so those workgroups have 4 waves (one per SIMD, whose
+// wave may also use the accumulation registers): no scratch.  Which workgroup
+// computes a row does not change its sums.
+constexpr int gemv_waves(int nj) { return nj >= 15 ? 4 : 8; }
 
 // One wave per token: the same normalisation as the decode kernels' normalise()
 // (qd_decode_ops.hip), written out as fp16.
@@ -77,7 +82,9 @@ __global__ __launch_bounds__(256) void rmsnorm_batched_kernel(const uint16_t* __
 // 16-byte chunks of one token tile that each thread stages into LDS: a tile
 // holds tok_tile(NJ) rows of at most NJ * 64 chunks, spread over the
 // workgroup's threads.
-constexpr int stage_chunks(int nj) { return (tok_tile(nj) * nj * 64 + kGemvWaves * 64 - 1) / (kGemvWaves * 64); }
+constexpr int stage_chunks(int nj) {
+  return (tok_tile(nj) * nj * 64 + gemv_waves(nj) * 64 - 1) / (gemv_waves(nj) * 64);
+}
 
 // DPP row rotations (gfx9 encodings): lane i of a 16-lane row reads lane
 // (i - n) mod 16.
@@ -119,8 +126,8 @@ __device__ __forceinline__ float block4_sum(float s0, float s1, float s2, float 
   return k;
 }
 
-// Y[t][n] for n in this workgroup's 16 rows and t in its kTokPerWg tokens.
-// Wave w holds rows n0 = 16*bx + 2w and n0 + 1 (NJ chunks of 8 per lane, the
+// Y[t][n] for n in this workgroup's 2W rows (W = gemv_waves(NJ)) and t in its
+// kTokPerWg tokens.  Wave w holds rows n0 = 2W*bx + 2w and n0 + 1 (NJ chunks of 8 per lane, the
 // last one masked when K is not a multiple of 512).  Token tiles of kTokTile
 // rows of X are staged in LDS; each lane reads its 16-byte chunks from them
 // (consecutive lanes, consecutive 16 B: conflict-free).  The next tile's
@@ -132,7 +139,8 @@ __device__ __forceinline__ float block4_sum(float s0, float s1, float s2, float 
 //   kEpi 0: Y[t][n] = half(sum)
 //   kEpi 1: Y[t][n] = half(R[t][n] + half(sum))     (residual add; R may be Y)
 template <int NJ, int kEpi>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_batched_kernel(BatchedGemvParams p) {
+__global__ __launch_bounds__(gemv_waves(NJ) * 64) void gemv_batched_kernel(BatchedGemvParams p) {
+  constexpr int kGemvWaves = gemv_waves(NJ);
   extern __shared__ __align__(16) uint16_t xs[];        // [kTokTile][NJ * 512]
   constexpr int kTokTile = tok_tile(NJ);
   constexpr int kStage = stage_chunks(NJ);
@@ -668,15 +676,17 @@ hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float ep
 
 hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t stream) {
   const int nj = (p.k + 511) / 512;
-  const dim3 grid((p.n + 2 * kGemvWaves - 1) / (2 * kGemvWaves), (p.t + kTokPerWg - 1) / kTokPerWg);
+  if (nj < 1 || nj > 16) return hipErrorInvalidValue;
+  const int waves = gemv_waves(nj);
+  const dim3 grid((p.n + 2 * waves - 1) / (2 * waves), (p.t + kTokPerWg - 1) / kTokPerWg);
   const size_t lds = (size_t)tok_tile(nj) * nj * 512 * sizeof(uint16_t);
   switch (nj * 2 + epi) {
 #define QD_CASE(n)                                                                                  \
     case 2 * n:                                                                                      \
-      hipLaunchKernelGGL((gemv_batched_kernel<n, 0>), grid, dim3(kGemvWaves * 64), lds, stream, p); \
+      hipLaunchKernelGGL((gemv_batched_kernel<n, 0>), grid, dim3(waves * 64), lds, stream, p);       \
       break;                                                                                         \
     case 2 * n + 1:                                                                                  \
-      hipLaunchKernelGGL((gemv_batched_kernel<n, 1>), grid, dim3(kGemvWaves * 64), lds, stream, p); \
+      hipLaunchKernelGGL((gemv_batched_kernel<n, 1>), grid, dim3(waves * 64), lds, stream, p);       \
       break;
     QD_CASE(1) QD_CASE(2) QD_CASE(3) QD_CASE(4) QD_CASE(5) QD_CASE(6) QD_CASE(7) QD_CASE(8)
     QD_CASE(9) QD_CASE(10) QD_CASE(11) QD_CASE(12) QD_CASE(13) QD_CASE(14) QD_CASE(15) QD_CASE(16)

@@ -36,11 +36,11 @@ EXPORTS = (
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
-    "qd_gemm_nt", "qd_prefill_attention",
+    "qd_gemm_nt", "qd_gemm_swiglu", "qd_prefill_attention",
     # qdiy/engine.h
     "qd_model_image_bytes", "qd_model_fill_random", "qd_model_write_random", "qd_engine_create",
     "qd_engine_create_from_image", "qd_engine_destroy", "qd_engine_config", "qd_engine_reset",
-    "qd_engine_prefill", "qd_engine_step", "qd_engine_logits", "qd_engine_generate",
+    "qd_engine_prefill", "qd_engine_step", "qd_engine_logits", "qd_engine_generate", "qd_engine_kv_rows",
     "qd_engine_set_prefill_mode",
 )
 
@@ -123,6 +123,7 @@ def load() -> ctypes.CDLL:
     ip = ctypes.POINTER(ctypes.c_int)
     L.qd_proj_residual.argtypes = [vp, vp, vp, vp, i, i, vp]
     L.qd_gemm_nt.argtypes = [vp, ll, vp, vp, vp, ll, i, i, i, i, vp]
+    L.qd_gemm_swiglu.argtypes = [vp, ll, vp, vp, vp, ll, i, i, i, vp]
     L.qd_prefill_attention.argtypes = [vp, vp, ll, vp, vp, vp, ll, i, i, i, i, i, vp]
     L.qd_engine_set_prefill_mode.argtypes = [vp, i]
     L.qd_ffn_up_swiglu.argtypes = [vp, vp, ctypes.c_float, vp, vp, vp, i, i, vp]
@@ -143,6 +144,7 @@ def load() -> ctypes.CDLL:
     L.qd_engine_prefill.argtypes = [vp, ip, i, ip]
     L.qd_engine_step.argtypes = [vp, i, i, ip]
     L.qd_engine_logits.argtypes = [vp, u16p]
+    L.qd_engine_kv_rows.argtypes = [vp, i, i, i, u16p, u16p]
     L.qd_engine_generate.argtypes = [vp, ip, i, i, i, ip, ip]
     L.qd_last_error.restype = ctypes.c_char_p
     L.qd_version.restype = ctypes.c_char_p
@@ -404,6 +406,21 @@ def gemm_nt(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, m: int, n: int, k
     return y
 
 
+def gemm_swiglu(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, act: torch.Tensor, m: int,
+                n: int, k: int, ldx: int | None = None, ldy: int | None = None,
+                stream=None) -> torch.Tensor:
+    """act[i][j] = half(g * silu(u)), g = half(x[i] . w1[j]), u = half(x[i] . w2[j]), on the
+    matrix cores (qd_gemm_swiglu); w1, w2 [n][k]; x rows ldx and act rows ldy apart."""
+    ldx = k if ldx is None else ldx
+    ldy = n if ldy is None else ldy
+    if (x.numel() < (m - 1) * ldx + k or w1.numel() < n * k or w2.numel() < n * k
+            or act.numel() < (m - 1) * ldy + n):
+        raise ValueError("x, w1, w2 or act too small for m, n, k and the strides")
+    _check(load().qd_gemm_swiglu(_ptr(x, "x"), ldx, _ptr(w1, "w1"), _ptr(w2, "w2"), _ptr(act, "act"),
+                                 ldy, m, n, k, _stream(stream)))
+    return act
+
+
 def ffn_up_swiglu(x: torch.Tensor, norm_w: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
                   act: torch.Tensor, hidden: int, inter: int, eps: float = 1e-6,
                   stream=None) -> torch.Tensor:
@@ -521,6 +538,14 @@ class Engine:
         out = np.empty(self.cfg.vocab_size, np.float16)
         _check(load().qd_engine_logits(self._h, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16))))
         return out
+
+    def kv_rows(self, layer: int, pos0: int, n: int):
+        """qd_engine_kv_rows: (K, V) rows [pos0, pos0 + n) of `layer`, fp16 [n][hidden]."""
+        k = np.empty((n, self.cfg.hidden_size), np.float16)
+        v = np.empty_like(k)
+        p = ctypes.POINTER(ctypes.c_uint16)
+        _check(load().qd_engine_kv_rows(self._h, layer, pos0, n, k.ctypes.data_as(p), v.ctypes.data_as(p)))
+        return k, v
 
     def generate(self, prompt, max_new: int, stop_at_eos: bool = True) -> list:
         p = (ctypes.c_int * len(prompt))(*prompt)

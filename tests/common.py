@@ -161,3 +161,56 @@ def model_logits_fp64(m: dict, tokens, rope_base: float = 10000.0, mutate: str =
                 g, u = u, g
             x = x + f(L["w_down"]) @ (g * u / (1.0 + np.exp(-u)))
     return f(m["lm_head"]) @ rms(x, m["ln_f"])
+
+
+def model_kv_fp64(m: dict, tokens, rope_base: float = 10000.0, mutate: str = "", terms: bool = False):
+    """Float64 K (rotated) and V cache rows of every layer for `tokens` at
+    positions 0..n-1, all positions at once with a causal mask (the same
+    textbook forward as model_logits_fp64): lists over layers of [n][hidden].
+    With terms=True also each element's sum of |addends| (|xn| |W| + |b|, the
+    two rotated halves' added for K), for rounding bounds."""
+    c = m["cfg"]
+    H, NH, D = c["hidden"], c["heads"], 128
+    f = lambda a: a.astype(np.float64)
+    n = len(tokens)
+    X = f(m["wte"][np.asarray(tokens)])                               # [n, H]
+
+    def rms(x, w):
+        return x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + 1e-6) * f(w)
+
+    inv = rope_base ** (-np.arange(64) * 2.0 / D)
+    th = np.arange(n)[:, None] * inv[None, :]
+    cs, sn = np.cos(th)[:, None, :], np.sin(th)[:, None, :]           # [n, 1, 64]
+    if mutate == "rope_sign":
+        sn = -sn
+
+    def rot(a):                                                       # [n, NH, D]
+        a1, a2 = a[..., :64], a[..., 64:]
+        return np.concatenate([a1 * cs - a2 * sn, a2 * cs + a1 * sn], axis=-1)
+
+    Ks, Vs, TK, TV = [], [], [], []
+    causal = np.triu(np.ones((n, n), bool), 1)
+    for L in m["layers"]:
+        xn = rms(X, L["ln_1"])
+        W, b = f(L["qkv_w"]), f(L["qkv_b"])
+        qkv = xn @ W.T + b
+        q, k, v = (qkv[:, i * H:(i + 1) * H].reshape(n, NH, D) for i in range(3))
+        q, k = rot(q), rot(k)
+        Ks.append(k.reshape(n, H))
+        Vs.append(v.reshape(n, H))
+        if terms:
+            t = np.abs(xn) @ np.abs(W).T + np.abs(b)
+            tk = t[:, H:2 * H].reshape(n, NH, D)
+            tk = np.concatenate([tk[..., :64] + tk[..., 64:]] * 2, axis=-1)
+            TK.append(tk.reshape(n, H))
+            TV.append(t[:, 2 * H:])
+        s = np.einsum("ihd,jhd->hij", q, k) / np.sqrt(D)
+        s[:, causal] = -np.inf
+        p = np.exp(s - s.max(axis=2, keepdims=True))
+        p /= p.sum(axis=2, keepdims=True)
+        a = np.einsum("hij,jhd->ihd", p, v).reshape(n, H)
+        X = X + a @ f(L["proj_w"]).T
+        xn2 = rms(X, L["ln_2"])
+        g, u = xn2 @ f(L["w1"]).T, xn2 @ f(L["w2"]).T
+        X = X + (g * u / (1.0 + np.exp(-u))) @ f(L["w_down"]).T
+    return (Ks, Vs, TK, TV) if terms else (Ks, Vs)

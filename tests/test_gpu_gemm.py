@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from common import normal_f16, ulp16
+from common import model_kv_fp64, model_tensors, normal_f16, ulp16
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu
@@ -86,6 +86,47 @@ def test_mfma_mode_within_fp32_summation_bound(qdiy, m, n, k, with_res):
     assert np.all(np.abs(got - want) <= tol), float(np.max(np.abs(got - want) - tol))
 
 
+@pytest.mark.parametrize("m,n,k,ldy", [(37, 100, 512, 100), (127, 1368, 2048, 1368),
+                                        # m >= 512: the 128 x 128 tile, a ragged last tile
+                                        # (n = 130, 1000) and a strided output
+                                        (600, 130, 512, 136), (1000, 1000, 1024, 1000),
+                                        (512, 5504, 2048, 5504)])
+def test_gemm_swiglu_within_bound(qdiy, m, n, k, ldy):
+    """qd_gemm_swiglu: gate and up GEMMs on the matrix cores with the SwiGLU in the
+    epilogue.  Each act is half(g * silu(u)) of g and u the fp16 roundings of
+    fp32 sums; those may round to the neighbour of the float64 sum's fp16
+    value when the fp32 sum lies within its summation bound of the boundary,
+    so act is within the propagated bound of half(g64) * silu(half(u64)):
+    |silu(u)| (ulp(g) + bound_g) + |g| 1.1 (ulp(u) + bound_u) + 2 ulp(act)."""
+    rng = np.random.default_rng(31 * m + n + k)
+    x = normal_f16(rng, (m, k))
+    W1, W2 = normal_f16(rng, (n, k), 0.03), normal_f16(rng, (n, k), 0.03)
+    act = torch.full((m * ldy + 64,), 9.0, dtype=torch.float16, device="cuda")
+    qdiy.gemm_swiglu(_dev(x.reshape(-1)), _dev(W1.reshape(-1)), _dev(W2.reshape(-1)), act, m, n, k,
+                     ldy=ldy)
+    torch.cuda.synchronize()
+    out = act.cpu().numpy()
+    assert np.all(out[(m - 1) * ldy + n:] == np.float16(9.0)), "write past the last row"
+    got = np.stack([out[i * ldy:i * ldy + n] for i in range(m)]).astype(np.float64)
+    if ldy > n:
+        gaps = np.stack([out[i * ldy + n:(i + 1) * ldy] for i in range(m - 1)])
+        assert np.all(gaps == np.float16(9.0)), "write between rows"
+    x64, W1d, W2d = x.astype(np.float64), W1.astype(np.float64), W2.astype(np.float64)
+    g, u = x64 @ W1d.T, x64 @ W2d.T
+    ax = np.abs(x64)
+    bg, bu = k * 2.0 ** -23 * (ax @ np.abs(W1d).T), k * 2.0 ** -23 * (ax @ np.abs(W2d).T)
+    gh = g.astype(np.float16).astype(np.float64)
+    uh = u.astype(np.float16).astype(np.float64)
+    silu = uh / (1.0 + np.exp(-uh))
+    want = gh * silu
+    tol = np.abs(silu) * (ulp16(gh) + bg) + np.abs(gh) * 1.1 * (ulp16(uh) + bu) + 2 * ulp16(want)
+    err = np.abs(got - want)
+    assert np.all(err <= tol), (float(np.max(err - tol)), np.unravel_index(np.argmax(err - tol), err.shape))
+    # the bound is tight enough to see a swapped gate and up
+    swapped = uh * (gh / (1.0 + np.exp(-gh)))
+    assert np.mean(np.abs(swapped - got) > tol) > 0.5
+
+
 def test_gemm_nt_rejects_bad_arguments(qdiy):
     x = torch.zeros(4 * 96, dtype=torch.float16, device="cuda")
     w = torch.zeros(16 * 96, dtype=torch.float16, device="cuda")
@@ -136,12 +177,13 @@ def test_engine_mfma_prefill(qdiy, hidden, inter):
                          intermediate_size=inter, max_seqlen=320)
     img = qdiy.random_model_image(cfg, 41 + hidden, 0.03, nthreads=8)
     prompt = [int(t) for t in np.random.default_rng(hidden).integers(0, 512, 300)]
-    res = {}
+    res, kv = {}, {}
     with qdiy.Engine(image=img) as eng:
         for mode in (qdiy.GEMM_EXACT, qdiy.GEMM_MFMA):
             eng.set_prefill_mode(mode)
             eng.reset()
             pos = eng.prefill(prompt[:-1])
+            kv[mode] = [eng.kv_rows(layer, 0, pos) for layer in range(cfg.num_layers)]
             eng.step(prompt[-1], pos)
             prefilled = eng.logits().astype(np.float64)
             eng.reset()
@@ -152,6 +194,29 @@ def test_engine_mfma_prefill(qdiy, hidden, inter):
     d = np.abs(exact[0] - mfma[0])
     assert float(np.max(d)) <= 0.02 * float(np.max(np.abs(exact[0]))) + 0.01, float(np.max(d))
     assert float(np.corrcoef(exact[0], mfma[0])[0, 1]) > 0.999
+    # The KV rows the prefill leaves, against a float64 recomputation of the prompt.
+    n = len(prompt) - 1
+    m = model_tensors(img)
+    ref_k, ref_v, term_k, term_v = model_kv_fp64(m, prompt[:-1], terms=True)
+    bad_k, _ = model_kv_fp64(m, prompt[:-1], mutate="rope_sign")
+    kv_terms = {"K": term_k, "V": term_v}
+    for layer in range(cfg.num_layers):
+        for mode in (qdiy.GEMM_EXACT, qdiy.GEMM_MFMA):
+            k, v = kv[mode][layer]
+            for name, got, ref in (("K", k, ref_k[layer]), ("V", v, ref_v[layer])):
+                err = np.abs(got.astype(np.float64) - ref)
+                scale = np.max(np.abs(ref), axis=1, keepdims=True)
+                if layer == 0:
+                    # fp16 roundings of the normalised input, the QKV sums, the bias add and
+                    # the rotation, each within an ulp of values at most the row's scale
+                    tol = 4 * ulp16(scale) + 2.0 ** -10 * kv_terms[name][layer]
+                else:
+                    # plus what the first layer's fp16 activations and attention carry over
+                    tol = 0.01 * scale
+                assert np.all(err <= tol), (layer, mode, name, float(np.max(err - tol)))
+        if layer == 0:
+            k0 = kv[qdiy.GEMM_MFMA][0][0].astype(np.float64)
+            assert np.mean(np.abs(k0 - bad_k[0]) > 4 * ulp16(np.max(np.abs(bad_k[0])))) > 0.3
 
 
 def test_engine_mfma_prefill_two_passes(qdiy):
