@@ -52,6 +52,7 @@ constexpr int kXcds = 8;                   // MI355X: workgroups are dealt to 8 
 constexpr int kVtLd = kFpKeys + 4;
 constexpr int kVtHalves = 128 * kVtLd;     // per wave
 constexpr int kOLd = 128 + 4;              // fp32 O row in the fold
+constexpr float kLazy = 8.0f;              // log2 of the largest softmax weight before a rescale
 static_assert((size_t)kFpWaves * 16 * kOLd * 4 <= (size_t)kFpWaves * kVtHalves * 2,
               "one query tile's fold reuses the V^T buffers");
 
@@ -151,40 +152,62 @@ __global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefi
       }
     load(j + kFpWaves);
     __builtin_amdgcn_sched_barrier(0);         // keep the next block's loads here
-    // online softmax of query (u, c) over keys kb + 16 t + 4 g + r
+    // Online softmax of query (u, c) over keys kb + 16 t + 4 g + r.  The
+    // reference m (log2 units) moves only when a block's maximum passes it by
+    // more than kLazy, so weights stay below 2^kLazy (fp16 holds them with the
+    // same relative precision) and O and l are rescaled in few blocks; the
+    // causal mask is applied only on blocks that reach past a query of the
+    // tile; each exponent is one fma of the raw score.
+    // The four query tiles go through each step together, with one
+    // wave-uniform branch per block, so their dependency chains interleave.
     f16x8 pb[kQt];
+    float sv[kQt][8], bm[kQt];
+    bool grow = false;
 #pragma unroll
     for (int u = 0; u < kQt; ++u) {
-      float sv[8];
+      const bool diag = kb + kFpKeys - 1 > p.pos0 + q0 + 16 * u;   // wave-uniform
       float bmax = -__builtin_inff();
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int key = kb + 16 * t + 4 * g + r;
-          const float s = key <= qpos[u] ? st[u][t][r] * p.scale_log2 : -__builtin_inff();
-          sv[4 * t + r] = s;
+          float s = st[u][t][r];
+          if (diag) s = kb + 16 * t + 4 * g + r <= qpos[u] ? s : -__builtin_inff();
+          sv[u][4 * t + r] = s;
           bmax = fmaxf(bmax, s);
         }
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-      const float mn = fmaxf(m[u], bmax);
-      const float mref = mn == -__builtin_inff() ? 0.0f : mn;   // no key yet: every weight is 0
-      const float alpha = __builtin_amdgcn_exp2f(m[u] - mref);
+      bm[u] = bmax;
+    }
+#pragma unroll
+    for (int u = 0; u < kQt; ++u) bm[u] = fmaxf(bm[u], __shfl_xor(bm[u], 16));
+#pragma unroll
+    for (int u = 0; u < kQt; ++u) {
+      bm[u] = fmaxf(bm[u], __shfl_xor(bm[u], 32)) * p.scale_log2;   // log2 units (scale > 0)
+      grow |= bm[u] > m[u] + kLazy;            // -inf + kLazy is -inf: a first finite block grows
+    }
+    if (__any(grow)) {
+#pragma unroll
+      for (int u = 0; u < kQt; ++u) {
+        const float mn = bm[u] > m[u] + kLazy ? bm[u] : m[u];
+        const float alpha = mn == m[u] ? 1.0f : __builtin_amdgcn_exp2f(m[u] - mn);
+        l[u] *= alpha;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) o[u][n] *= alpha;
+        m[u] = mn;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kQt; ++u) {
+      const float nref = m[u] == -__builtin_inff() ? 0.0f : -m[u];   // no key yet: every weight is 0
       float ps = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         // the sum takes the rounded weights the product uses, so O / l stays
         // a weighted mean of V rows
-        pb[u][e] = (_Float16)__builtin_amdgcn_exp2f(sv[e] - mref);
+        pb[u][e] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[u][e], p.scale_log2, nref));
         ps += (float)pb[u][e];
       }
-      l[u] = l[u] * alpha + ps;
-      m[u] = mn;
-      if (__any(alpha != 1.0f)) {              // the running maximum moved for some query
-#pragma unroll
-        for (int n = 0; n < 8; ++n) o[u][n] *= alpha;
-      }
+      l[u] += ps;
     }
     wave_lds_fence();                          // V^T stores visible to the wave
 #pragma unroll
