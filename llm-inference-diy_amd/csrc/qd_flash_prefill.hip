@@ -28,8 +28,11 @@
 //     P.V product sums over its 32 keys in any order, so element e of the lane
 //     stands for key pi(8 g + e) = 16 (e / 4) + 4 g + e % 4, and the V^T
 //     operand is read in the same order.
-//   - V^T is V transposed through LDS: each wave writes its block as [dim][key]
-//     and reads, per tile, the 4 + 4 keys pi(8 g ..) of dim 16 n + c.
+//   - V^T comes from LDS: each wave writes its V block there as it lies
+//     ([key][dim], 16-byte stores) and takes, per tile, the 4 + 4 keys
+//     pi(8 g ..) of dim 16 n + c with two transposed reads (gfx950's
+//     ds_read_b64_tr_b16).  (Writing the block transposed took 64 two-byte LDS
+//     stores per lane and block.)
 // P is rounded to fp16 for the product (as the reference's MMA kernel does)
 // and the softmax denominator sums the rounded weights; exponentials are the
 // hardware's exp2.  Nothing here is bit-reproducible on
@@ -47,14 +50,14 @@ constexpr int kFpQueries = 16 * kQt;       // queries per workgroup
 constexpr int kFpKeys = 32;                // keys per block: the P.V product's K
 constexpr int kFpWaves = 4;
 constexpr int kXcds = 8;                   // MI355X: workgroups are dealt to 8 XCDs in turn
-// V^T row: 32 keys + 4 halves of padding (18 words), so the two dims one
-// transposed store writes (8 apart) fall 16 banks apart.
-constexpr int kVtLd = kFpKeys + 4;
-constexpr int kVtHalves = 128 * kVtLd;     // per wave
+// V block in LDS as it lies in memory, [key][dim], rows padded to 144 halves
+// (288 bytes: the four rows one transposed read takes start 8 banks apart).
+constexpr int kVPitch = 128 + 16;
+constexpr int kVHalves = kFpKeys * kVPitch;  // per wave
 constexpr int kOLd = 128 + 4;              // fp32 O row in the fold
 constexpr float kLazy = 8.0f;              // log2 of the largest softmax weight before a rescale
-static_assert((size_t)kFpWaves * 16 * kOLd * 4 <= (size_t)kFpWaves * kVtHalves * 2,
-              "one query tile's fold reuses the V^T buffers");
+static_assert((size_t)kFpWaves * 16 * kOLd * 4 <= (size_t)kFpWaves * kVHalves * 2,
+              "one query tile's fold reuses the V buffers");
 
 __device__ __forceinline__ void wave_lds_fence() {
   // Lanes of one wave hand data to each other through LDS: the wave's LDS
@@ -66,7 +69,7 @@ __device__ __forceinline__ void wave_lds_fence() {
 }
 
 __global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefillParams p) {
-  __shared__ __align__(16) _Float16 lds[kFpWaves * kVtHalves];
+  __shared__ __align__(16) _Float16 lds[kFpWaves * kVHalves];
   __shared__ float fml[2][kFpWaves][kFpQueries];   // each wave's (m, l) per query
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -115,7 +118,7 @@ __global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefi
     for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const f16x8*>(row + 16 * i);
   };
 
-  _Float16* vt = lds + wave * kVtHalves;
+  _Float16* vrow = lds + wave * kVHalves;
   float m[kQt], l[kQt];
   f32x4 o[kQt][8];
 #pragma unroll
@@ -130,15 +133,14 @@ __global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefi
   if (j < nblk) load(j);
   for (; j < nblk; j += kFpWaves) {
     const int kb = j * kFpKeys;
-    // V^T into LDS (dim 16 i + 8 (l >> 5) + e, key l & 31), then S^T per tile;
-    // after that this block's K and V registers are free for the next block.
-    wave_lds_fence();                          // the previous block's V^T reads are done
+    // V into LDS as it lies (key l & 31, dims 16 i + 8 (l >> 5) ..), then S^T
+    // per tile; after that this block's K and V registers are free for the
+    // next block.
+    wave_lds_fence();                          // the previous block's V reads are done
     {
-      const int kk = lane & 31, dh = 8 * (lane >> 5);
+      _Float16* row = vrow + (lane & 31) * kVPitch + 8 * (lane >> 5);
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vt[(16 * i + dh + e) * kVtLd + kk] = vr[i][e];
+      for (int i = 0; i < 8; ++i) *reinterpret_cast<f16x8*>(row + 16 * i) = vr[i];
     }
     f32x4 st[kQt][2];
 #pragma unroll
@@ -209,13 +211,21 @@ __global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefi
       }
       l[u] += ps;
     }
-    wave_lds_fence();                          // V^T stores visible to the wave
+    wave_lds_fence();                          // V stores visible to the wave
+    // The V^T operand of dims tile n by transposed reads (ds_read_b64_tr_b16):
+    // within a 16-lane group, lane i's element e is element i % 4 of the four
+    // halves lane 4 e + i / 4 addresses.  Lane j of group g addresses key
+    // 4 g + j / 4 (+ 16 for the second read), dims 16 n + 4 (j % 4) .. +4, so
+    // lane (c, g) receives dim 16 n + c of keys 4 g + e and 16 + 4 g + e: the
+    // keys pi(8 g + e) its P^T operand holds.
+    const _Float16* vtr = vrow + (4 * g + (c >> 2)) * kVPitch + 4 * (c & 3);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      const _Float16* row = vt + (16 * n + c) * kVtLd + 4 * g;
-      const f16x4 lo = *reinterpret_cast<const f16x4*>(row);
-      const f16x4 hi = *reinterpret_cast<const f16x4*>(row + 16);
-      const f16x8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      typedef short i16x4 __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vtr + 16 * n));
+      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vtr + 16 * kVPitch + 16 * n));
+      const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
       for (int u = 0; u < kQt; ++u) o[u][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[u], o[u][n], 0, 0, 0);
     }
