@@ -147,7 +147,7 @@ struct qd_engine {
   int p_cap = 0;
   int* p_tokens = nullptr;
   uint16_t *p_x = nullptr, *p_xn = nullptr, *p_qkv = nullptr, *p_att = nullptr;
-  uint16_t *p_g = nullptr, *p_u = nullptr, *p_act = nullptr;
+  uint16_t *p_g = nullptr, *p_u = nullptr, *p_act = nullptr;   // p_u lies inside p_g's allocation
   float* p_split = nullptr;             // split-K partials of the MFMA prefill GEMMs
 
   const uint16_t* w(long long off) const { return weights + off; }
@@ -174,7 +174,7 @@ void engine_free(qd_engine* e) {
   (void)hipFree(e->lm_ws);
   (void)hipFree(e->p_split);
   for (void* q : {(void*)e->p_tokens, (void*)e->p_x, (void*)e->p_xn, (void*)e->p_qkv, (void*)e->p_att,
-                  (void*)e->p_g, (void*)e->p_u, (void*)e->p_act})
+                  (void*)e->p_g, (void*)e->p_act})
     (void)hipFree(q);
   if (e->h_token) (void)hipHostFree(e->h_token);
   if (e->attn) qd_ctx_destroy(e->attn);
@@ -189,12 +189,13 @@ void engine_free(qd_engine* e) {
 int resize_prefill_scratch(qd_engine* e, int cap) {
   const long long H = e->cfg.hidden_size, I = e->cfg.intermediate_size;
   int* tok = nullptr;
-  uint16_t *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *u = nullptr,
-           *act = nullptr;
+  uint16_t *x = nullptr, *xn = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr, *act = nullptr;
+  // g holds 2 * inter columns per token: [g | u] rows of the joint gate/up
+  // product, or g then u as two packed blocks
   struct { void** p; long long n; } allocs[] = {
       {(void**)&tok, (long long)cap * 4},    {(void**)&x, cap * H * 2},   {(void**)&xn, cap * H * 2},
-      {(void**)&qkv, cap * 3 * H * 2},       {(void**)&att, cap * H * 2}, {(void**)&g, cap * I * 2},
-      {(void**)&u, cap * I * 2},             {(void**)&act, cap * I * 2}};
+      {(void**)&qkv, cap * 3 * H * 2},       {(void**)&att, cap * H * 2}, {(void**)&g, cap * I * 4},
+      {(void**)&act, cap * I * 2}};
   for (auto& a : allocs) {
     const hipError_t he = hipMalloc(a.p, (size_t)a.n);
     if (he != hipSuccess) {
@@ -204,7 +205,7 @@ int resize_prefill_scratch(qd_engine* e, int cap) {
     }
   }
   for (void* q : {(void*)e->p_tokens, (void*)e->p_x, (void*)e->p_xn, (void*)e->p_qkv, (void*)e->p_att,
-                  (void*)e->p_g, (void*)e->p_u, (void*)e->p_act})
+                  (void*)e->p_g, (void*)e->p_act})
     (void)hipFree(q);
   e->p_tokens = tok;
   e->p_x = x;
@@ -212,7 +213,7 @@ int resize_prefill_scratch(qd_engine* e, int cap) {
   e->p_qkv = qkv;
   e->p_att = att;
   e->p_g = g;
-  e->p_u = u;
+  e->p_u = g + cap * I;
   e->p_act = act;
   e->p_cap = cap;
   return QD_OK;
@@ -275,7 +276,18 @@ int prefill_batched(qd_engine* e, const int* tokens, int T, int pos0) {
     he = gemv(e->p_att, H, e->w(f.proj_w), H, H, e->p_x, H, 1);
     if (he == hipSuccess) he = qd::launch_rmsnorm_batched(e->p_x, e->w(f.ln_2), kEps, e->p_xn, H, T, e->stream);
     bool joint = false;                          // gate/up GEMM with the SwiGLU in its epilogue
-    if (he == hipSuccess && e->prefill_mode == QD_GEMM_MFMA) {
+    if (he == hipSuccess && e->prefill_mode == QD_GEMM_MFMA && T >= 512 &&
+        f.w2 == f.w1 + (long long)I * H) {
+      // w1 and w2 lie back to back: one plain product of 2 * inter columns
+      // into [g | u] rows (the vendor library from 512 rows up), then the
+      // elementwise SwiGLU, is faster there than the fused 128 x 128 tile.
+      qd::BatchedGemvParams q{e->p_xn, H, e->w(f.w1), 2 * I, H, T, e->p_g, 2LL * I, nullptr};
+      he = qd::launch_gemm_mfma(q, 0, e->stream);
+      if (he == hipSuccess)
+        he = qd::launch_swiglu_batched(e->p_g, e->p_g + I, e->p_act, T, I, 2LL * I, e->stream);
+      joint = true;
+    }
+    if (he == hipSuccess && e->prefill_mode == QD_GEMM_MFMA && !joint) {
       qd::BatchedGemvParams q{e->p_xn, H, e->w(f.w1), I, H, T, e->p_act, I, nullptr};
       q.w2 = e->w(f.w2);
       const hipError_t je = qd::launch_gemm_mfma_swiglu(q, e->stream);
@@ -285,7 +297,7 @@ int prefill_batched(qd_engine* e, const int* tokens, int T, int pos0) {
     if (he == hipSuccess && !joint) he = gemv(e->p_xn, H, e->w(f.w1), I, H, e->p_g, I, 0);
     if (he == hipSuccess && !joint) he = gemv(e->p_xn, H, e->w(f.w2), I, H, e->p_u, I, 0);
     if (he == hipSuccess && !joint)
-      he = qd::launch_swiglu_batched(e->p_g, e->p_u, e->p_act, (long long)T * I, e->stream);
+      he = qd::launch_swiglu_batched(e->p_g, e->p_u, e->p_act, T, I, I, e->stream);
     if (he == hipSuccess) he = gemv(e->p_act, I, e->w(f.w_down), H, I, e->p_x, H, 1);
   }
   return he == hipSuccess ? QD_OK : hip_fail(he, "prefill launch");

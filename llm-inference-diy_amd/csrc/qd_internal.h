@@ -296,6 +296,9 @@ hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t 
 // The same product on the matrix cores (fp32 accumulation in the hardware's
 // order, not bit-reproducible on the host); p.k must be a multiple of 64.
 hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream);
+// qd_blaslt.cpp: the same product (epi 0 or 1) through hipBLASLt;
+// hipErrorNotSupported when the library has no kernel for it (nothing ran).
+hipError_t blaslt_gemm_nt(const BatchedGemvParams& p, int epi, hipStream_t stream);
 // The same, allowed to split K over up to 4 workgroups per tile when the tile
 // grid leaves CUs idle: fp32 partial sums in `workspace` (kGemmSplitWsBytes
 // suffice for every shape), then one launch folds them in slice order and
@@ -314,8 +317,9 @@ hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_
                                uint16_t* v_layer, const float2* rope_cs, long long row_stride,
                                long long head_stride, int pos0, int num_heads, int T,
                                hipStream_t stream);
-hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t* act, long long n,
-                                 hipStream_t stream);
+// act (rows x cols, packed) from g and u at row stride ld.
+hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t* act, int rows,
+                                 int cols, long long ld, hipStream_t stream);
 hipError_t launch_embed(const uint16_t* wte, const int* tokens, uint16_t* x, int hidden, int T,
                         hipStream_t stream);
 // qd_flash_prefill.hip: one workgroup per (head, 16 queries).

@@ -294,19 +294,36 @@ __global__ __launch_bounds__(kRopeHeads * 64) void rope_batched_kernel(uint16_t*
   vc[64 + i] = hv2;
 }
 
-// act = half(g * (u / (1 + exp2_rep(-u * log2 e)))) on fp16 g, u: the decode
-// kernel's SwiGLU epilogue (qd_decode_ops.hip), elementwise over T * inter.
+// act[r][c] = half(g * (u / (1 + exp2_rep(-u * log2 e)))) on fp16
+// g = g[r * ld + c], u = u[r * ld + c]: the decode kernel's SwiGLU epilogue
+// (qd_decode_ops.hip) over rows x cols, V consecutive columns per thread.
+template <int V>
 __global__ __launch_bounds__(256) void swiglu_batched_kernel(const uint16_t* __restrict__ g,
                                                             const uint16_t* __restrict__ u,
-                                                            uint16_t* __restrict__ act,
-                                                            long long n) {
-  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
-  if (i >= n) return;
-  const float gh = (float)reinterpret_cast<const _Float16*>(g)[i];
-  const float uh = (float)reinterpret_cast<const _Float16*>(u)[i];
-  const float e = exp2_rep(-uh * kLog2e);
-  const float silu = uh / (1.0f + e);
-  reinterpret_cast<_Float16*>(act)[i] = to_f16(gh * silu);
+                                                            uint16_t* __restrict__ act, int rows,
+                                                            int cols, long long ld) {
+  const long long i = ((long long)blockIdx.x * 256 + threadIdx.x) * V;
+  if (i >= (long long)rows * cols) return;
+  const long long r = i / cols, c = i - r * cols;
+  _Float16 gh[V], uh[V], out[V];
+  if constexpr (V == 8) {
+    *reinterpret_cast<f16x8*>(gh) = *reinterpret_cast<const f16x8*>(g + r * ld + c);
+    *reinterpret_cast<f16x8*>(uh) = *reinterpret_cast<const f16x8*>(u + r * ld + c);
+  } else {
+    gh[0] = reinterpret_cast<const _Float16*>(g)[r * ld + c];
+    uh[0] = reinterpret_cast<const _Float16*>(u)[r * ld + c];
+  }
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const float uf = (float)uh[j];
+    const float e = exp2_rep(-uf * kLog2e);
+    const float silu = uf / (1.0f + e);
+    out[j] = to_f16((float)gh[j] * silu);
+  }
+  if constexpr (V == 8)
+    *reinterpret_cast<f16x8*>(act + i) = *reinterpret_cast<const f16x8*>(out);
+  else
+    reinterpret_cast<_Float16*>(act)[i] = out[0];
 }
 
 // Embedding rows: x[t] = wte[tokens[t]].
@@ -706,15 +723,28 @@ hipError_t launch_rope_batched(uint16_t* qkv, const uint16_t* bias, uint16_t* k_
   return hipGetLastError();
 }
 
-hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t* act, long long n,
-                                 hipStream_t stream) {
-  hipLaunchKernelGGL(swiglu_batched_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                     g, u, act, n);
+hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t* act, int rows,
+                                 int cols, long long ld, hipStream_t stream) {
+  const long long n = (long long)rows * cols;
+  if (rows < 1 || cols < 1 || ld < cols) return hipErrorInvalidValue;
+  const bool vec8 = cols % 8 == 0 && ld % 8 == 0 &&
+                    ((reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(u) |
+                      reinterpret_cast<uintptr_t>(act)) & 15u) == 0;
+  if (vec8)
+    hipLaunchKernelGGL(swiglu_batched_kernel<8>, dim3((unsigned)((n / 8 + 255) / 256)), dim3(256), 0,
+                       stream, g, u, act, rows, cols, ld);
+  else
+    hipLaunchKernelGGL(swiglu_batched_kernel<1>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       stream, g, u, act, rows, cols, ld);
   return hipGetLastError();
 }
 
 hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream) {
   if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
+  if (p.t >= 512) {   // plain products of 512 rows and more: the vendor library (qd_blaslt.cpp)
+    const hipError_t e = blaslt_gemm_nt(p, epi, stream);
+    if (e != hipErrorNotSupported) return e;
+  }
   const bool vec8 = ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) == 0 &&
                     p.ldy % 4 == 0;
   if (p.t >= 512 && vec8 && p.k % kBk == 0) {

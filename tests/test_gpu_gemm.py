@@ -167,16 +167,18 @@ def test_mfma_large_m_unaligned_output_and_in_place_residual(qdiy):
     assert np.all(np.abs(got - want) <= ulp16(want) + ulp16(h) + bound + ulp16(s))
 
 
-@pytest.mark.parametrize("hidden,inter", [(512, 1368), (2048, 5504)])
-def test_engine_mfma_prefill(qdiy, hidden, inter):
+@pytest.mark.parametrize("hidden,inter,n_prompt", [(512, 1368, 300), (2048, 5504, 300), (512, 1408, 700)])
+def test_engine_mfma_prefill(qdiy, hidden, inter, n_prompt):
     """MFMA prefill against exact prefill on the same prompt (with c_proj exact
     where inter is not a multiple of 64): the next step's logits agree to the
     fp32-order difference, and plain decode steps are bit-identical in both
-    modes."""
+    modes.  From 512 prompt tokens the plain products go to the vendor library
+    and the gate/up product is one 2 * inter column product followed by the
+    elementwise SwiGLU; below, the hand-written tiles run."""
     cfg = qdiy.model_cfg(vocab_size=512, hidden_size=hidden, num_layers=2, num_heads=hidden // 128,
-                         intermediate_size=inter, max_seqlen=320)
+                         intermediate_size=inter, max_seqlen=n_prompt + 20)
     img = qdiy.random_model_image(cfg, 41 + hidden, 0.03, nthreads=8)
-    prompt = [int(t) for t in np.random.default_rng(hidden).integers(0, 512, 300)]
+    prompt = [int(t) for t in np.random.default_rng(hidden).integers(0, 512, n_prompt)]
     res, kv = {}, {}
     with qdiy.Engine(image=img) as eng:
         for mode in (qdiy.GEMM_EXACT, qdiy.GEMM_MFMA):
