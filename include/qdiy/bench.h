@@ -36,7 +36,7 @@ int qd_decode_attention_stage(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
  * gives the same bits.  The scan kernel can fold them itself when the context
  * found round-robin workgroup dispatch whose period divides num_heads
  * (qd_ctx_xcd_period) and the grid is at most one workgroup per CU;
- * QD_MERGE_AUTO (the default) does so up to 2048 rows, where it measured
+ * QD_MERGE_AUTO (the default) does so up to 3072 rows, where it measured
  * faster, and runs split plans with a merge kernel beyond.  A context that
  * merges in the kernel also runs fused plans only up to 128 rows (224
  * otherwise).  The other modes exist for A/B timing and tests. */

@@ -506,8 +506,11 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(A
 // the last slot becoming visible and the output store.  The counter is read
 // only to decide when a slot that stays stale may be scanned again (a slot
 // still stale in a read issued after the counter showed every other split
-// arrived was written where this workgroup cannot see it); that read is
-// consumed a round later, so it adds nothing to a read that finds every slot.
+// arrived was written where this workgroup cannot see it).  It is read with
+// every kXCntPeriod-th read of the slots only, and consumed a round later: an
+// agent-scope load is slower than the slot loads, which hit the XCD's L2, and
+// a read lasts as long as its slowest load (reading it with every read cost
+// 0.13-0.15 us per call at 160-3072 rows).
 //
 // The merger reads the slots through its XCD's L2.  With the launch's
 // workgroup i on XCD (k + i) mod NX (round-robin dispatch, checked at context
@@ -529,6 +532,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(A
 // Words of one tagged slot: O[128] as (O_d, tag), then (m, tag), (l, tag).
 constexpr int kXSlotWords = 144;   // 130 used; 1152 B, nine 128-B lines
 constexpr int kXPolls = 1 << 14;   // reads of the slots before the stale ones are scanned again
+constexpr int kXCntPeriod = 8;     // reads of the slots per read of the arrival counter
 static_assert(kXMaxSplits <= 64 && kXMaxSplits <= kMergeSlices * kMergeBatch,
               "one wave holds a head's split weights; merge_fold reads them in one batch");
 
@@ -592,7 +596,7 @@ __device__ __forceinline__ void fold_per_dim(const float* s_w, const float* s_l,
 
 // One read of the other splits' slots by a merging wave: lane l's dim
 // (value, tag) of every slot, lane c's slot record (lanes c < others), and,
-// issued last, the head's arrival counter (lane 0).
+// issued last when `counter` is not null, the head's arrival counter (lane 0).
 template <int SMAX>
 struct SlotRead {
   f32x2 o[SMAX];
@@ -613,7 +617,7 @@ __device__ __forceinline__ void issue_read(SlotRead<SMAX>& r, const char* head, 
     r.rec = __builtin_nontemporal_load(
         reinterpret_cast<const f32x4*>(head + (unsigned)(lane * kXSlotWords * 8 + kD * 8)));
   r.cnt = 0u;
-  if (lane == 0) r.cnt = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0 && counter) r.cnt = __hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Splits (< others) with a word in the read that is not this call's.
@@ -672,8 +676,8 @@ __device__ __forceinline__ void fold_store(const SlotRead<SMAX>& r, int lane, in
 // other splits' slots until every word it needs is this call's, then folds
 // and stores its 64 dims of the head's output and returns 0.  Returns the
 // splits to scan again instead: those in `force`, or those still stale in a
-// read issued after a completed counter read saw every other split arrived,
-// or after kXPolls reads.  (m_own, l_own, o_own): the merger's own partial
+// read issued after a completed counter read (one with every kXCntPeriod-th
+// read) saw every other split arrived, or after kXPolls reads.  (m_own, l_own, o_own): the merger's own partial
 // (o_own: this lane's dim).  One read is in flight at a time: a kernel ends
 // only when its loads have returned, and a second read in flight when the
 // first finds every slot measured 0.6 us slower per call at L=8192.
@@ -689,7 +693,8 @@ __device__ __forceinline__ unsigned long long merge_wave(const AttnParams& p, co
   bool arrived = false;   // a completed counter read, before this read was issued, saw all arrived
   SlotRead<SMAX> r;
   for (int round = 0;; ++round) {
-    issue_read<SMAX>(r, head, dim_off, last_slot, lane, others, m_own, l_own, counter);
+    const bool with_cnt = (round + 1) % kXCntPeriod == 0;
+    issue_read<SMAX>(r, head, dim_off, last_slot, lane, others, m_own, l_own, with_cnt ? counter : nullptr);
     ++reads;
     const unsigned long long stale = stale_splits<SMAX>(r, lane, others, p.tag);
     if ((stale | force) == 0ull) {
@@ -699,7 +704,7 @@ __device__ __forceinline__ unsigned long long merge_wave(const AttnParams& p, co
     const unsigned long long rescan = force | (arrived || round >= kXPolls ? stale : 0ull);
     if (rescan) return rescan;
     // This read's counter value: complete now, so it covers the next read.
-    arrived = (unsigned)__builtin_amdgcn_readfirstlane(r.cnt) - p.cnt_base >= (unsigned)others;
+    if (with_cnt) arrived = (unsigned)__builtin_amdgcn_readfirstlane(r.cnt) - p.cnt_base >= (unsigned)others;
   }
 }
 

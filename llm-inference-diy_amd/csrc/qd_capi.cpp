@@ -50,13 +50,13 @@ using qd::hip_fail;
 //     looping over its rows (qd::auto_split); other split counts or more waves
 //     per workgroup measured no better (L=8192: 14.7 us at 16 splits, 15.6 at
 //     32, 16.7 at 64, 17.1 at 24).  Up to kXMergeMaxRows rows the last split
-//     of each head merges in the scan kernel (5.1-5.4 us at 256-512 rows, 5.8
-//     at 768, 6.5-6.8 at 1280-1536, against 6.7-7.2 with a merge kernel; 7.37
-//     against 7.33 at 2048); beyond, a merge kernel follows (0.3-0.5 us faster
-//     there: 9.75 against 10.2 us at 4096, 14.7 against 15.05 at 8192).
+//     of each head merges in the scan kernel (4.9-5.2 us at 256-512 rows, 5.6
+//     at 768, 6.4-6.7 at 1280-1536, against 6.9-7.4 with a merge kernel; 7.24
+//     against 7.29 at 2048, 8.42 against 8.49 at 3072); beyond, a merge kernel
+//     follows (9.67 against 9.73-9.93 us at 4096, 14.7 against 15.0 at 8192).
 constexpr int kFusedMaxRows = 224;
 constexpr int kFusedMaxRowsX = 128;
-constexpr int kXMergeMaxRows = 2048;
+constexpr int kXMergeMaxRows = 3072;
 constexpr int kPrefillBatch = 256;   // split-plan prefill queries per batched launch pair
 
 qd::AttnPlan plan_fused(int seqlen) {

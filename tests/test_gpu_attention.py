@@ -282,14 +282,14 @@ def test_planner_follows_its_rules(qdiy, H):
     device's CU count, for automatic, fused and explicit split plans."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     lengths = sorted(set(list(range(1, 300)) + list(range(1000, 1100)) + list(range(2000, 2100)) +
-                         [4095, 4096, 4097, 8191, 8192, 8193, 16384, 32767, 32768]))
+                         [3071, 3072, 3073, 4095, 4096, 4097, 8191, 8192, 8193, 16384, 32767, 32768]))
     with qdiy.Context(num_heads=H, max_seqlen=32768) as ctx:
         period = ctx.xcd_period()
         for L in lengths:
             assert ctx.plan_detail(L).as_tuple() == _planner_rules(L, H, cus, period=period), (H, L)
             plan = ctx.plan_detail(L)
             want_in_kernel = int(plan.variant == qdiy.SPLIT and period >= 1 and H % period == 0
-                                 and L <= 2048 and plan.num_splits <= 64 and plan.num_splits * H <= cus)
+                                 and L <= 3072 and plan.num_splits <= 64 and plan.num_splits * H <= cus)
             assert plan.merge_in_kernel == want_in_kernel, (H, L)
         for L in (1, 300, 8192):
             assert ctx.plan_detail(L, "fused").as_tuple() == _planner_rules(L, H, cus, "fused"), L

@@ -60,7 +60,7 @@ def test_context_finds_round_robin_dispatch(qdiy):
                              f"now places workgroups 0..31 on {qdiy.xcd_placement(256)[:32]}")
         if cus == 256:
             assert period == 8          # MI355X: 8 XCDs of 32 CUs
-        for L, in_kernel in ((100, 0), (129, 1), (1024, 1), (2048, 1), (2049, 0), (8192, 0)):
+        for L, in_kernel in ((100, 0), (129, 1), (1024, 1), (2048, 1), (3072, 1), (3073, 0), (8192, 0)):
             plan = ctx.plan_detail(L)
             assert plan.merge_in_kernel == in_kernel, L           # 100 rows: fused, nothing to merge
             assert plan.variant == (qdiy.FUSED if L <= 128 else qdiy.SPLIT), L
@@ -91,7 +91,7 @@ def test_in_kernel_merge_equals_two_launches(qdiy, H, L, layout):
             plan = ctx.plan_detail(L)
             can = (plan.variant == qdiy.SPLIT and period >= 1 and H % period == 0
                    and plan.num_splits <= 64 and plan.num_splits * H <= cus)
-            want = {qdiy.MERGE_IN_KERNEL: can, qdiy.MERGE_AUTO: can and L <= 2048,
+            want = {qdiy.MERGE_IN_KERNEL: can, qdiy.MERGE_AUTO: can and L <= 3072,
                     qdiy.MERGE_TWO_LAUNCHES: False}[mode]
             assert plan.merge_in_kernel == int(want), (H, L, mode, plan.as_tuple(), period)
             outs.append(_attend(ctx, t, L, H))
