@@ -3,7 +3,7 @@
 // The prompt's QKV, o-proj and c_proj projections are plain GEMMs
 // (qwen_infer.cu:462, :542, :593 call the reference's tensor-core GEMM for
 // them), so from 512 rows up they go to the vendor library, whose kernels
-// took 58 / 27 / 50 us for Qwen-1.8B's 2048-row QKV / o-proj / c_proj in a
+// took 49 / 27 / 58 us for Qwen-1.8B's 2048-row QKV / o-proj / c_proj in a
 // kernel trace of the engine's prefill, against 71 us for QKV and 126 us for
 // o-proj plus c_proj with this library's 128 x 128 MFMA tile.  Below 512 rows the
 // library's kernels were slower than the split-K 64 x 64 tile (20 against 18
