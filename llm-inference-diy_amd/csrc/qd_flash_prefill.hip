@@ -5,75 +5,82 @@
 // launch per head, then scatter_interleaved_kernel), as one launch that reads
 // the rotated Q rows and the KV cache where they lie.
 //
-// Workgroup (h, tile) takes 64 consecutive queries of head h, four tiles of
-// 16 (the MFMA's N).  Its four waves all take the 64 queries and split the
-// keys: wave w takes key blocks w, w + 4, ... of 32 keys each, so every K/V
-// row a wave loads serves 64 queries; each wave keeps its own online-softmax
-// state per query, and the four states are folded in LDS at the end.  The
-// grid is one-dimensional and its linear index is remapped so that, with
+// Workgroup (h, tile) takes 64 consecutive queries of head h with eight waves
+// (two per SIMD, so one wave's matrix-core products can run while the other
+// computes its softmax).  The waves form two key groups of four: group k takes
+// the 64-key blocks k, k + 2, ..., and within a group wave w takes queries
+// 16 w .. 16 w + 15 (the MFMA's N).  A group's 256 threads load each of its
+// blocks once into LDS ([key][dim], rows padded), where its four waves read
+// it, so every K/V row read from memory serves 64 queries.  Loads run two
+// blocks ahead through two register stages; the LDS buffers alternate per
+// block, with one workgroup barrier per block.  At the end the two groups'
+// softmax states of each query are folded through LDS.
+//
+// The grid is one-dimensional and its linear index is remapped so that, with
 // workgroups dealt to the 8 XCDs in turn, the tiles of a head run on one XCD
 // and share its L2 copy of the head's K/V rows; within a head the latest
-// tiles (the longest key ranges) start first.  Per block and query tile a
-// wave computes
-//   S^T = K Q^T   (M = 16 keys per tile, two tiles; N = 16 queries; K = 128 dims)
-//   O^T += V^T P^T (M = 16 dims per tile, eight tiles; N = 16 queries; K = 32 keys)
+// tiles (the longest key ranges) start first, and a CU that finishes a short
+// tile takes a long one.  Per block a wave computes
+//   S^T = K Q^T    (M = 16 keys per tile, four tiles; N = 16 queries; K = 128 dims)
+//   O^T += V^T P^T (M = 16 dims per tile, eight tiles; N = 16 queries; K = 32 keys,
+//                   two halves of the block)
 // Transposing both products puts the query in the MFMA's column, which is the
 // lane's column l % 16 of every accumulator, so each lane's softmax state
-// (running max m, partial sum l) belongs to query l % 16 in every product and
+// (running max m, denominator) belongs to query l % 16 in every product and
 // rescaling O needs no lane exchange.  Operand lanes: A[l % 16][8 (l / 16) + e],
 // B[8 (l / 16) + e][l % 16]; accumulator D[4 (l / 16) + r][l % 16].
-//   - K rows feed A directly (the 8 dims of a lane are 16 contiguous bytes).
+//   - K rows feed A from LDS (a lane's 8 dims are 16 contiguous bytes; rows
+//     are 272 bytes apart, so the 16 rows of one read start 4 banks apart).
 //   - S^T's accumulator gives lane (g = l / 16, c = l % 16) the keys
 //     16 t + 4 g + r of query c, which become P^T's B operand as they are: the
 //     P.V product sums over its 32 keys in any order, so element e of the lane
-//     stands for key pi(8 g + e) = 16 (e / 4) + 4 g + e % 4, and the V^T
-//     operand is read in the same order.
-//   - V^T comes from LDS: each wave writes its V block there as it lies
-//     ([key][dim], 16-byte stores) and takes, per tile, the 4 + 4 keys
-//     pi(8 g ..) of dim 16 n + c with two transposed reads (gfx950's
-//     ds_read_b64_tr_b16).  (Writing the block transposed took 64 two-byte LDS
-//     stores per lane and block.)
+//     stands for key pi(8 g + e) = 16 (e / 4) + 4 g + e % 4 of the half, and
+//     the V^T operand is read in the same order.
+//   - V^T: per dims tile, the 4 + 4 keys pi(8 g ..) of dim 16 n + c, with two
+//     transposed reads (gfx950's ds_read_b64_tr_b16) of the V block as it
+//     lies in LDS.
 // P is rounded to fp16 for the product (as the reference's MMA kernel does)
-// and the softmax denominator sums the rounded weights; exponentials are the
-// hardware's exp2.  Nothing here is bit-reproducible on
-// the host; the exact prefill path (the decode kernels batched) is.
+// and the softmax denominator sums the rounded weights, on the matrix core (an
+// all-ones A operand), so each output is a weighted mean of V rows.  A query's
+// reference maximum moves only when a block's maximum passes it by more than
+// 2^kLazy, so weights stay below 2^kLazy (fp16 holds them with the same
+// relative precision) and O is rescaled in few blocks.  Exponentials are the
+// hardware's exp2.  Nothing here is bit-reproducible on the host; the exact
+// prefill path (the decode kernels batched) is.
 #include "qd_device.h"
 #include "qd_internal.h"
 
 namespace qd {
 namespace {
 
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kQt = 4;                     // 16-query tiles per workgroup
-constexpr int kFpQueries = 16 * kQt;       // queries per workgroup
-constexpr int kFpKeys = 32;                // keys per block: the P.V product's K
-constexpr int kFpWaves = 4;
+constexpr int kFpQueries = 64;             // queries per workgroup
+constexpr int kFpKeys = 64;                // keys per block
+constexpr int kQWaves = 4;                 // waves of a key group: 16 queries each
+constexpr int kKeyGroups = 2;
 constexpr int kXcds = 8;                   // MI355X: workgroups are dealt to 8 XCDs in turn
-// V block in LDS as it lies in memory, [key][dim], rows padded to 144 halves
-// (288 bytes: the four rows one transposed read takes start 8 banks apart).
-constexpr int kVPitch = 128 + 16;
-constexpr int kVHalves = kFpKeys * kVPitch;  // per wave
+constexpr int kKPitch = 128 + 8;           // K row in LDS (halves): 272 bytes
+constexpr int kVPitch = 128 + 16;          // V row in LDS (halves): 288 bytes, the four rows
+                                           // one transposed read takes start 8 banks apart
+constexpr int kKHalves = kFpKeys * kKPitch;
+constexpr int kVHalves = kFpKeys * kVPitch;
 constexpr int kOLd = 128 + 4;              // fp32 O row in the fold
 constexpr float kLazy = 8.0f;              // log2 of the largest softmax weight before a rescale
-static_assert((size_t)kFpWaves * 16 * kOLd * 4 <= (size_t)kFpWaves * kVHalves * 2,
-              "one query tile's fold reuses the V buffers");
+static_assert(kQWaves * 16 == kFpQueries, "a key group's waves cover the workgroup's queries");
+static_assert((size_t)kFpQueries * kOLd * 4 <= (size_t)kKeyGroups * 2 * kKHalves * 2,
+              "the fold's O rows fit in the K buffers");
 
-__device__ __forceinline__ void wave_lds_fence() {
-  // Lanes of one wave hand data to each other through LDS: the wave's LDS
-  // operations execute in order, and these fences keep the compiler from
-  // moving the accesses across this point.
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefillParams p) {
-  __shared__ __align__(16) _Float16 lds[kFpWaves * kVHalves];
-  __shared__ float fml[2][kFpWaves][kFpQueries];   // each wave's (m, l) per query
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+__global__ __launch_bounds__(kKeyGroups * kQWaves * 64) void flash_prefill_kernel(FlashPrefillParams p) {
+  __shared__ __align__(16) _Float16 lk[kKeyGroups][2][kKHalves];   // [group][buffer]
+  __shared__ __align__(16) _Float16 lv[kKeyGroups][2][kVHalves];
+  const int lane = threadIdx.x & 63;
+  const int wave8 = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int kg = wave8 / kQWaves;                // key group: blocks kg, kg + 2, ...
+  const int wave = wave8 % kQWaves;              // queries 16 wave .. 16 wave + 15
+  const int tid = threadIdx.x & 255;             // thread within the key group
   const int c = lane & 15;
   const int g = lane >> 4;
   const int ntile = (p.tokens + kFpQueries - 1) / kFpQueries;
@@ -85,196 +92,176 @@ __global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefi
   const int nq = min(kFpQueries, p.tokens - q0);
   const int nkeys = p.pos0 + q0 + nq;           // keys [0, nkeys) reach the last query
   const int nblk = (nkeys + kFpKeys - 1) / kFpKeys;
+  const int wq0 = 16 * wave;
+  const bool active = wq0 < nq;                 // wave-uniform: the wave has queries
 
-  // B operand of S^T per query tile u: Q[q0 + 16 u + c][32 s + 8 g .. +8]
-  // (rows past the last query repeat it; their outputs are not stored)
-  f16x8 qb[kQt][4];
-  int qpos[kQt];                                // this lane's query position per tile
+  // B operand of S^T: Q[q0 + wq0 + c][32 s + 8 g .. +8] (rows past the last
+  // query repeat it; their outputs are not stored)
+  f16x8 qb[4];
+  {
+    const int qi = min(wq0 + c, nq - 1);
+    const uint16_t* qrow = p.q + (long long)(q0 + qi) * p.q_stride + h * 128 + 8 * g;
 #pragma unroll
-  for (int u = 0; u < kQt; ++u) {
-    const uint16_t* qrow = p.q + (long long)(q0 + min(16 * u + c, nq - 1)) * p.q_stride + h * 128 + 8 * g;
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4) qb[u][s4] = *reinterpret_cast<const f16x8*>(qrow + 32 * s4);
-    qpos[u] = p.pos0 + q0 + 16 * u + c;
+    for (int s = 0; s < 4; ++s) qb[s] = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
   }
+  const int qpos = p.pos0 + q0 + wq0 + c;       // this lane's query position
+  const int wpos = p.pos0 + q0 + wq0;           // the wave's first query position
 
-  const uint16_t* kbase = p.k + (long long)h * p.head_stride + 8 * g;
-  const uint16_t* vbase = p.v + (long long)h * p.head_stride + 8 * (lane >> 5);
-  // K rows kb + 16 t + c (dims 32 s + 8 g .. +8) and V row kb + (l & 31)
-  // (dims 16 i + 8 (l >> 5) .. +8) of block j, clamped into [0, nblk) so every
-  // call issues them; keys past nkeys repeat key nkeys - 1 and are masked.
-  f16x8 kr[2][4], vr[8];
-  auto load = [&](int j) {
-    j = min(j, nblk - 1);
+  // A group's block: 64 rows of K and of V, 16 chunks of 16 bytes each; thread
+  // t moves chunks t + 256 i (i < 4) of both (row idx / 16, chunk idx % 16).
+  // Rows past nkeys repeat row nkeys - 1 and are masked.
+  const uint16_t* khead = p.k + (long long)h * p.head_stride;
+  const uint16_t* vhead = p.v + (long long)h * p.head_stride;
+  f16x8 sk0[4], sv0[4], sk1[4], sv1[4];         // two register stages
+  auto gload = [&](int j, f16x8 (&sk)[4], f16x8 (&sv)[4]) {
     const int kb = j * kFpKeys;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint16_t* row = kbase + (long long)min(kb + 16 * t + c, nkeys - 1) * p.row_stride;
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) kr[t][s4] = *reinterpret_cast<const f16x8*>(row + 32 * s4);
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      const long long row = min(kb + (idx >> 4), nkeys - 1);
+      sk[i] = *reinterpret_cast<const f16x8*>(khead + row * p.row_stride + 8 * (idx & 15));
+      sv[i] = *reinterpret_cast<const f16x8*>(vhead + row * p.row_stride + 8 * (idx & 15));
     }
-    const uint16_t* row = vbase + (long long)min(kb + (lane & 31), nkeys - 1) * p.row_stride;
+  };
+  auto lstore = [&](int b, const f16x8 (&sk)[4], const f16x8 (&sv)[4]) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) vr[i] = *reinterpret_cast<const f16x8*>(row + 16 * i);
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      *reinterpret_cast<f16x8*>(&lk[kg][b][(idx >> 4) * kKPitch + 8 * (idx & 15)]) = sk[i];
+      *reinterpret_cast<f16x8*>(&lv[kg][b][(idx >> 4) * kVPitch + 8 * (idx & 15)]) = sv[i];
+    }
   };
 
-  _Float16* vrow = lds + wave * kVHalves;
-  float m[kQt], l[kQt];
-  f32x4 o[kQt][8];
+  float m = -__builtin_inff();
+  f32x4 ls = {0.0f, 0.0f, 0.0f, 0.0f};          // the denominator, in every element
+  f32x4 o[8];
 #pragma unroll
-  for (int u = 0; u < kQt; ++u) {
-    m[u] = -__builtin_inff();
-    l[u] = 0.0f;
+  for (int n = 0; n < 8; ++n) o[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  f16x8 ones;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) o[u][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int e = 0; e < 8; ++e) ones[e] = (_Float16)1.0f;
+
+  // Block j of this group from LDS buffer b: the wave's online-softmax update.
+  auto compute = [&](int j, int b) {
+    const int kb = j * kFpKeys;
+    if (!active || j >= nblk || kb > wpos + 15) return;   // wave-uniform: no key reaches a query
+    f32x4 st[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      const _Float16* krow = &lk[kg][b][(16 * t + c) * kKPitch + 8 * g];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        st[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8*>(krow + 32 * s),
+                                                       qb[s], st[t], 0, 0, 0);
+    }
+    if (kb + kFpKeys - 1 > wpos) {              // wave-uniform: some key is past a query
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) st[t][r] = kb + 16 * t + 4 * g + r <= qpos ? st[t][r] : -__builtin_inff();
+    }
+    // Each lane tests its own 16 keys against the lazy bound; only when some
+    // lane's keys pass it are the block maxima formed across the lanes of a
+    // query (the decisions a block-wide maximum gives).
+    float lm = st[0][0];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lm = fmaxf(lm, st[t][r]);
+    if (__any(lm * p.scale_log2 > m + kLazy)) {   // -inf + kLazy is -inf: a first finite block grows
+      float bm = fmaxf(lm, __shfl_xor(lm, 16));
+      bm = fmaxf(bm, __shfl_xor(bm, 32)) * p.scale_log2;   // log2 units (scale > 0)
+      const float mn = bm > m + kLazy ? bm : m;
+      const float alpha = mn == m ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+      ls *= alpha;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) o[n] *= alpha;
+      m = mn;
+    }
+    const float nref = m == -__builtin_inff() ? 0.0f : -m;   // no key yet: every weight is 0
+    f16x8 pb[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        pb[hh][e] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * hh + e / 4][e % 4], p.scale_log2, nref));
+      ls = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pb[hh], ls, 0, 0, 0);
+    }
+    // O^T += V^T P^T per 32-key half.  Within a 16-lane group, lane i's element
+    // e of a transposed read is element i % 4 of the four halves lane
+    // 4 e + i / 4 addresses.  Lane j of group g addresses key 4 g + j / 4 (+ 16
+    // for the second read), dims 16 n + 4 (j % 4) .. +4, so lane (c, g)
+    // receives dim 16 n + c of keys 4 g + e and 16 + 4 g + e of the half: the
+    // keys pi(8 g + e) its P^T operand holds.
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const _Float16* vtr = &lv[kg][b][(32 * hh + 4 * g + (c >> 2)) * kVPitch + 4 * (c & 3)];
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vtr + 16 * n));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vtr + 16 * kVPitch + 16 * n));
+        const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[hh], o[n], 0, 0, 0);
+      }
+    }
+  };
+
+  // Iteration i computes the group's block 2 i + kg from LDS buffer i % 2; the
+  // block of iteration i + 1 waits in the register stage loaded during
+  // iteration i - 1 and goes to the other buffer at the end of iteration i.
+  const int nit = (nblk + 1) / 2;
+  if (kg < nblk) {
+    gload(kg, sk0, sv0);
+    lstore(0, sk0, sv0);
+  }
+  if (kg + 2 < nblk) gload(kg + 2, sk1, sv1);
+  __syncthreads();
+  for (int it = 0; it < nit; it += 2) {
+    {
+      const int j = 2 * it + kg;
+      if (j + 4 < nblk) gload(j + 4, sk0, sv0);
+      compute(j, 0);
+      if (j + 2 < nblk) lstore(1, sk1, sv1);
+      __syncthreads();
+    }
+    if (it + 1 < nit) {
+      const int j = 2 * (it + 1) + kg;
+      if (j + 4 < nblk) gload(j + 4, sk1, sv1);
+      compute(j, 1);
+      if (j + 2 < nblk) lstore(0, sk0, sv0);
+      __syncthreads();
+    }
   }
 
-  int j = wave;
-  if (j < nblk) load(j);
-  for (; j < nblk; j += kFpWaves) {
-    const int kb = j * kFpKeys;
-    // V into LDS as it lies (key l & 31, dims 16 i + 8 (l >> 5) ..), then S^T
-    // per tile; after that this block's K and V registers are free for the
-    // next block.
-    wave_lds_fence();                          // the previous block's V reads are done
-    {
-      _Float16* row = vrow + (lane & 31) * kVPitch + 8 * (lane >> 5);
+  // Fold the two key groups' states of each query: group 1 hands (m, l, O) to
+  // group 0 through LDS (the K/V buffers are free after the last barrier).
+  float* fo = reinterpret_cast<float*>(&lk[0][0][0]);       // [query][dim]
+  float* fm = reinterpret_cast<float*>(&lv[0][0][0]);       // [query][m, l]
+  const int qq = wq0 + c;                                   // the lane's query in the tile
+  if (kg == 1) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) *reinterpret_cast<f16x8*>(row + 16 * i) = vr[i];
+    for (int n = 0; n < 8; ++n) *reinterpret_cast<f32x4*>(fo + qq * kOLd + 16 * n + 4 * g) = o[n];
+    if (g == 0) {
+      fm[2 * qq] = m;
+      fm[2 * qq + 1] = ls[0];
     }
-    f32x4 st[kQt][2];
-#pragma unroll
-    for (int u = 0; u < kQt; ++u)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        st[u][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4)
-          st[u][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[t][s4], qb[u][s4], st[u][t], 0, 0, 0);
-      }
-    load(j + kFpWaves);
-    __builtin_amdgcn_sched_barrier(0);         // keep the next block's loads here
-    // Online softmax of query (u, c) over keys kb + 16 t + 4 g + r.  The
-    // reference m (log2 units) moves only when a block's maximum passes it by
-    // more than kLazy, so weights stay below 2^kLazy (fp16 holds them with the
-    // same relative precision) and O and l are rescaled in few blocks; the
-    // causal mask is applied only on blocks that reach past a query of the
-    // tile; each exponent is one fma of the raw score.
-    // The four query tiles go through each step together, with one
-    // wave-uniform branch per block, so their dependency chains interleave.
-    f16x8 pb[kQt];
-    float sv[kQt][8], bm[kQt];
-    bool grow = false;
-#pragma unroll
-    for (int u = 0; u < kQt; ++u) {
-      const bool diag = kb + kFpKeys - 1 > p.pos0 + q0 + 16 * u;   // wave-uniform
-      float bmax = -__builtin_inff();
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          float s = st[u][t][r];
-          if (diag) s = kb + 16 * t + 4 * g + r <= qpos[u] ? s : -__builtin_inff();
-          sv[u][4 * t + r] = s;
-          bmax = fmaxf(bmax, s);
-        }
-      bm[u] = bmax;
-    }
-#pragma unroll
-    for (int u = 0; u < kQt; ++u) bm[u] = fmaxf(bm[u], __shfl_xor(bm[u], 16));
-#pragma unroll
-    for (int u = 0; u < kQt; ++u) {
-      bm[u] = fmaxf(bm[u], __shfl_xor(bm[u], 32)) * p.scale_log2;   // log2 units (scale > 0)
-      grow |= bm[u] > m[u] + kLazy;            // -inf + kLazy is -inf: a first finite block grows
-    }
-    if (__any(grow)) {
-#pragma unroll
-      for (int u = 0; u < kQt; ++u) {
-        const float mn = bm[u] > m[u] + kLazy ? bm[u] : m[u];
-        const float alpha = mn == m[u] ? 1.0f : __builtin_amdgcn_exp2f(m[u] - mn);
-        l[u] *= alpha;
-#pragma unroll
-        for (int n = 0; n < 8; ++n) o[u][n] *= alpha;
-        m[u] = mn;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kQt; ++u) {
-      const float nref = m[u] == -__builtin_inff() ? 0.0f : -m[u];   // no key yet: every weight is 0
-      float ps = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // the sum takes the rounded weights the product uses, so O / l stays
-        // a weighted mean of V rows
-        pb[u][e] = (_Float16)__builtin_amdgcn_exp2f(__builtin_fmaf(sv[u][e], p.scale_log2, nref));
-        ps += (float)pb[u][e];
-      }
-      l[u] += ps;
-    }
-    wave_lds_fence();                          // V stores visible to the wave
-    // The V^T operand of dims tile n by transposed reads (ds_read_b64_tr_b16):
-    // within a 16-lane group, lane i's element e is element i % 4 of the four
-    // halves lane 4 e + i / 4 addresses.  Lane j of group g addresses key
-    // 4 g + j / 4 (+ 16 for the second read), dims 16 n + 4 (j % 4) .. +4, so
-    // lane (c, g) receives dim 16 n + c of keys 4 g + e and 16 + 4 g + e: the
-    // keys pi(8 g + e) its P^T operand holds.
-    const _Float16* vtr = vrow + (4 * g + (c >> 2)) * kVPitch + 4 * (c & 3);
+  }
+  __syncthreads();
+  if (kg == 0 && active && qq < nq) {
+    const float m1 = fm[2 * qq], l1 = fm[2 * qq + 1];
+    const float M = fmaxf(m, m1);                           // finite: key 0 reaches every query
+    const float a0 = m == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m - M);
+    const float a1 = m1 == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m1 - M);
+    const float inv = 1.0f / (a0 * ls[0] + a1 * l1);
+    _Float16* orow = reinterpret_cast<_Float16*>(p.out + (long long)(q0 + qq) * p.out_stride + h * 128);
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
-      typedef short i16x4 __attribute__((ext_vector_type(4)));
-      typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-      const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vtr + 16 * n));
-      const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vtr + 16 * kVPitch + 16 * n));
-      const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+      const f32x4 o1 = *reinterpret_cast<const f32x4*>(fo + qq * kOLd + 16 * n + 4 * g);
+      f16x4 v;
 #pragma unroll
-      for (int u = 0; u < kQt; ++u) o[u][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[u], o[u][n], 0, 0, 0);
-    }
-  }
-#pragma unroll
-  for (int u = 0; u < kQt; ++u) {
-    l[u] += __shfl_xor(l[u], 16);
-    l[u] += __shfl_xor(l[u], 32);
-    if (g == 0) {
-      fml[0][wave][16 * u + c] = m[u];
-      fml[1][wave][16 * u + c] = l[u];
-    }
-  }
-
-  // Fold the four waves' states one query tile at a time: O rows
-  // [wave][query][dim] in the V^T buffers, then each thread 8 dims of a query.
-  float* fo = reinterpret_cast<float*>(lds);
-  const int q = tid >> 4;
-  const int d0 = (tid & 15) * 8;
-#pragma unroll
-  for (int u = 0; u < kQt; ++u) {
-    __syncthreads();                           // V^T, or the previous tile's fold, is done
-#pragma unroll
-    for (int n = 0; n < 8; ++n)
-      *reinterpret_cast<f32x4*>(fo + (wave * 16 + c) * kOLd + 16 * n + 4 * g) = o[u][n];
-    __syncthreads();
-    const int qq = 16 * u + q;
-    if (qq < nq) {
-      float mw[kFpWaves];
-      float M = -__builtin_inff();
-#pragma unroll
-      for (int w = 0; w < kFpWaves; ++w) {
-        mw[w] = fml[0][w][qq];
-        M = fmaxf(M, mw[w]);
-      }
-      float L = 0.0f;
-      float acc[8] = {};
-#pragma unroll
-      for (int w = 0; w < kFpWaves; ++w) {
-        const float sc = mw[w] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mw[w] - M);
-        L += sc * fml[1][w][qq];
-        const float* row = fo + (w * 16 + q) * kOLd + d0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += sc * row[e];
-      }
-      f16x8 outv;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) outv[e] = (_Float16)(acc[e] / L);
-      *reinterpret_cast<f16x8*>(p.out + (long long)(q0 + qq) * p.out_stride + h * 128 + d0) = outv;
+      for (int r = 0; r < 4; ++r) v[r] = (_Float16)((a0 * o[n][r] + a1 * o1[r]) * inv);
+      *reinterpret_cast<f16x4*>(orow + 16 * n + 4 * g) = v;
     }
   }
 }
@@ -283,7 +270,7 @@ __global__ __launch_bounds__(kFpWaves * 64) void flash_prefill_kernel(FlashPrefi
 
 hipError_t launch_flash_prefill(const FlashPrefillParams& p, hipStream_t stream) {
   const dim3 grid(p.num_heads * ((p.tokens + kFpQueries - 1) / kFpQueries));
-  hipLaunchKernelGGL(flash_prefill_kernel, grid, dim3(kFpWaves * 64), 0, stream, p);
+  hipLaunchKernelGGL(flash_prefill_kernel, grid, dim3(kKeyGroups * kQWaves * 64), 0, stream, p);
   return hipGetLastError();
 }
 
