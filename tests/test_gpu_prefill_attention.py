@@ -139,7 +139,9 @@ def test_exact_mode_is_decode_attention(qdiy, H, pos0, T, layout, q_pad, out_pad
 
 
 @pytest.mark.parametrize("H,pos0,T,layout,q_pad,out_pad",
-                         CASES + [(16, 1792, 256, "engine", 4096, 0), (4, 0, 2048, "engine", 1024, 0)])
+                         CASES + [(16, 1792, 256, "engine", 4096, 0), (4, 0, 2048, "engine", 1024, 0),
+                                  (16, 0, 2048, "engine", 4096, 0),      # a full pass at Qwen-1.8B's heads
+                                  (8, 300, 1000, "head_major", 0, 8)])   # ragged last tile, continuing a prompt
 def test_mfma_mode_within_2e3(qdiy, H, pos0, T, layout, q_pad, out_pad):
     pr = Prompt(qdiy, H, pos0, T, seed=H * 11 + pos0 + T, layout=layout, q_pad=q_pad, out_pad=out_pad)
     try:
