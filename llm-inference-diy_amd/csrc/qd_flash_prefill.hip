@@ -9,12 +9,13 @@
 // (two per SIMD, so one wave's matrix-core products can run while the other
 // computes its softmax).  The waves form two key groups of four: group k takes
 // the 64-key blocks k, k + 2, ..., and within a group wave w takes queries
-// 16 w .. 16 w + 15 (the MFMA's N).  A group's 256 threads load each of its
-// blocks once into LDS ([key][dim], rows padded), where its four waves read
-// it, so every K/V row read from memory serves 64 queries.  Loads run two
-// blocks ahead through two register stages; the LDS buffers alternate per
-// block, with one workgroup barrier per block.  At the end the two groups'
-// softmax states of each query are folded through LDS.
+// 16 w .. 16 w + 15 (the MFMA's N).  A group's four waves load each of its
+// blocks once into LDS with direct loads (global_load_lds_dwordx4: no
+// registers, no LDS store instructions), where all four read it, so every K/V
+// row read from memory serves 64 queries.  The next block's loads go out while
+// the current block is computed; the LDS buffers alternate per block, with one
+// workgroup barrier per block.  At the end the two groups' softmax states of
+// each query are folded through LDS.
 //
 // The grid is one-dimensional and its linear index is remapped so that, with
 // workgroups dealt to the 8 XCDs in turn, the tiles of a head run on one XCD
@@ -29,8 +30,10 @@
 // (running max m, denominator) belongs to query l % 16 in every product and
 // rescaling O needs no lane exchange.  Operand lanes: A[l % 16][8 (l / 16) + e],
 // B[8 (l / 16) + e][l % 16]; accumulator D[4 (l / 16) + r][l % 16].
-//   - K rows feed A from LDS (a lane's 8 dims are 16 contiguous bytes; rows
-//     are 272 bytes apart, so the 16 rows of one read start 4 banks apart).
+//   - K rows feed A from LDS (a lane's 8 dims are 16 contiguous bytes).  Rows
+//     are 256 bytes with their 16-byte chunks swizzled: chunk q of row r sits
+//     at position q ^ (r % 16), so the 16 rows of one operand read fall on
+//     distinct banks.
 //   - S^T's accumulator gives lane (g = l / 16, c = l % 16) the keys
 //     16 t + 4 g + r of query c, which become P^T's B operand as they are: the
 //     P.V product sums over its 32 keys in any order, so element e of the lane
@@ -38,7 +41,8 @@
 //     the V^T operand is read in the same order.
 //   - V^T: per dims tile, the 4 + 4 keys pi(8 g ..) of dim 16 n + c, with two
 //     transposed reads (gfx950's ds_read_b64_tr_b16) of the V block as it
-//     lies in LDS.
+//     lies in LDS, its chunks swizzled by 2 (r % 4): the 4 rows x 2 chunks of
+//     one transposed read fall on distinct banks.
 // P is rounded to fp16 for the product (as the reference's MMA kernel does)
 // and the softmax denominator sums the rounded weights, on the matrix core (an
 // all-ones A operand), so each output is a weighted mean of V rows.  A query's
@@ -58,11 +62,13 @@ constexpr int kFpKeys = 64;                // keys per block
 constexpr int kQWaves = 4;                 // waves of a key group: 16 queries each
 constexpr int kKeyGroups = 2;
 constexpr int kXcds = 8;                   // MI355X: workgroups are dealt to 8 XCDs in turn
-constexpr int kKPitch = 128 + 8;           // K row in LDS (halves): 272 bytes
-constexpr int kVPitch = 128 + 16;          // V row in LDS (halves): 288 bytes, the four rows
-                                           // one transposed read takes start 8 banks apart
-constexpr int kKHalves = kFpKeys * kKPitch;
-constexpr int kVHalves = kFpKeys * kVPitch;
+constexpr int kRow = 128;                  // K and V rows in LDS: 256 bytes, 16-byte chunks swizzled
+constexpr int kKHalves = kFpKeys * kRow;
+constexpr int kVHalves = kFpKeys * kRow;
+// chunk q of row r sits at position q ^ swz(r): K by r % 16 (the 16 rows of one
+// operand read), V by 2 (r % 4) (the 4 rows x 2 chunks of one transposed read)
+__device__ __forceinline__ int kswz(int r) { return r & 15; }
+__device__ __forceinline__ int vswz(int r) { return 2 * (r & 3); }
 constexpr int kOLd = 128 + 4;              // fp32 O row in the fold
 constexpr float kLazy = 8.0f;              // log2 of the largest softmax weight before a rescale
 static_assert(kQWaves * 16 == kFpQueries, "a key group's waves cover the workgroup's queries");
@@ -107,28 +113,26 @@ __global__ __launch_bounds__(kKeyGroups * kQWaves * 64) void flash_prefill_kerne
   const int qpos = p.pos0 + q0 + wq0 + c;       // this lane's query position
   const int wpos = p.pos0 + q0 + wq0;           // the wave's first query position
 
-  // A group's block: 64 rows of K and of V, 16 chunks of 16 bytes each; thread
-  // t moves chunks t + 256 i (i < 4) of both (row idx / 16, chunk idx % 16).
-  // Rows past nkeys repeat row nkeys - 1 and are masked.
+  // A group's block: 64 rows of K and of V.  Rows past nkeys repeat row
+  // nkeys - 1 and are masked.
   const uint16_t* khead = p.k + (long long)h * p.head_stride;
   const uint16_t* vhead = p.v + (long long)h * p.head_stride;
-  f16x8 sk0[4], sv0[4], sk1[4], sv1[4];         // two register stages
-  auto gload = [&](int j, f16x8 (&sk)[4], f16x8 (&sv)[4]) {
+  // Direct loads into LDS: wave w of the group moves rows 16 w .. 16 w + 15 of
+  // the block, four rows (1 KB) per instruction; lane l fills position l % 16 of
+  // row l / 16 of the four, i.e. the row's chunk (l % 16) ^ swz(row).
+  auto dload = [&](int j, int b) {
     const int kb = j * kFpKeys;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i;
-      const long long row = min(kb + (idx >> 4), nkeys - 1);
-      sk[i] = *reinterpret_cast<const f16x8*>(khead + row * p.row_stride + 8 * (idx & 15));
-      sv[i] = *reinterpret_cast<const f16x8*>(vhead + row * p.row_stride + 8 * (idx & 15));
-    }
-  };
-  auto lstore = [&](int b, const f16x8 (&sk)[4], const f16x8 (&sv)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i;
-      *reinterpret_cast<f16x8*>(&lk[kg][b][(idx >> 4) * kKPitch + 8 * (idx & 15)]) = sk[i];
-      *reinterpret_cast<f16x8*>(&lv[kg][b][(idx >> 4) * kVPitch + 8 * (idx & 15)]) = sv[i];
+      const int row = 16 * wave + 4 * i + (lane >> 4);
+      const long long grow = min(kb + row, nkeys - 1);
+      const int kq = (lane & 15) ^ kswz(row), vq = (lane & 15) ^ vswz(row);
+      __builtin_amdgcn_global_load_lds(khead + grow * p.row_stride + 8 * kq,
+                                       (__attribute__((address_space(3))) void*)&lk[kg][b][(16 * wave + 4 * i) * kRow],
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vhead + grow * p.row_stride + 8 * vq,
+                                       (__attribute__((address_space(3))) void*)&lv[kg][b][(16 * wave + 4 * i) * kRow],
+                                       16, 0, 0);
     }
   };
 
@@ -149,11 +153,11 @@ __global__ __launch_bounds__(kKeyGroups * kQWaves * 64) void flash_prefill_kerne
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       st[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      const _Float16* krow = &lk[kg][b][(16 * t + c) * kKPitch + 8 * g];
+      const _Float16* krow = &lk[kg][b][(16 * t + c) * kRow];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        st[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const f16x8*>(krow + 32 * s),
-                                                       qb[s], st[t], 0, 0, 0);
+        st[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+            *reinterpret_cast<const f16x8*>(krow + 8 * ((4 * s + g) ^ kswz(16 * t + c))), qb[s], st[t], 0, 0, 0);
     }
     if (kb + kFpKeys - 1 > wpos) {              // wave-uniform: some key is past a query
 #pragma unroll
@@ -196,42 +200,35 @@ __global__ __launch_bounds__(kKeyGroups * kQWaves * 64) void flash_prefill_kerne
     // keys pi(8 g + e) its P^T operand holds.
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-      const _Float16* vtr = &lv[kg][b][(32 * hh + 4 * g + (c >> 2)) * kVPitch + 4 * (c & 3)];
+      const int vr = 32 * hh + 4 * g + (c >> 2);            // key of the low read; +16 for the high one
+      const _Float16* vrow = &lv[kg][b][vr * kRow];
 #pragma unroll
       for (int n = 0; n < 8; ++n) {
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vtr + 16 * n));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vtr + 16 * kVPitch + 16 * n));
+        const int q = 2 * n + ((c >> 1) & 1);              // dims 16 n + 4 (c % 4) .. +4 lie in chunk q
+        const int off = 8 * (q ^ vswz(vr)) + 4 * (c & 1);
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vrow + off));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(vrow + 16 * kRow + off));
         const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         o[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[hh], o[n], 0, 0, 0);
       }
     }
   };
 
-  // Iteration i computes the group's block 2 i + kg from LDS buffer i % 2; the
-  // block of iteration i + 1 waits in the register stage loaded during
-  // iteration i - 1 and goes to the other buffer at the end of iteration i.
+  // Iteration i computes the group's block 2 i + kg from LDS buffer i % 2 while
+  // the block of iteration i + 1 streams into the other buffer.  The direct
+  // loads are invisible to the compiler's waits: each wave waits for its own
+  // (vmcnt) before the barrier that hands the buffer to the group.
   const int nit = (nblk + 1) / 2;
-  if (kg < nblk) {
-    gload(kg, sk0, sv0);
-    lstore(0, sk0, sv0);
-  }
-  if (kg + 2 < nblk) gload(kg + 2, sk1, sv1);
+  if (kg < nblk) dload(kg, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  for (int it = 0; it < nit; it += 2) {
-    {
-      const int j = 2 * it + kg;
-      if (j + 4 < nblk) gload(j + 4, sk0, sv0);
-      compute(j, 0);
-      if (j + 2 < nblk) lstore(1, sk1, sv1);
-      __syncthreads();
-    }
-    if (it + 1 < nit) {
-      const int j = 2 * (it + 1) + kg;
-      if (j + 4 < nblk) gload(j + 4, sk1, sv1);
-      compute(j, 1);
-      if (j + 2 < nblk) lstore(0, sk0, sv0);
-      __syncthreads();
-    }
+  for (int it = 0; it < nit; ++it) {
+    const int j = 2 * it + kg;
+    const int b = it & 1;
+    if (j + 2 < nblk) dload(j + 2, b ^ 1);     // buffer b ^ 1 was last read before the previous barrier
+    compute(j, b);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
   }
 
   // Fold the two key groups' states of each query: group 1 hands (m, l, O) to
@@ -275,3 +272,4 @@ hipError_t launch_flash_prefill(const FlashPrefillParams& p, hipStream_t stream)
 }
 
 }  // namespace qd
+
