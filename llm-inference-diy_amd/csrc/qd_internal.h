@@ -322,7 +322,7 @@ hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t*
                                  int cols, long long ld, hipStream_t stream);
 hipError_t launch_embed(const uint16_t* wte, const int* tokens, uint16_t* x, int hidden, int T,
                         hipStream_t stream);
-// qd_flash_prefill.hip: one workgroup per (head, 16 queries).
+// qd_flash_prefill.hip: one workgroup per (head, 64 queries), eight waves.
 hipError_t launch_flash_prefill(const FlashPrefillParams& p, hipStream_t stream);
 
 }  // namespace qd
