@@ -2,13 +2,16 @@
 //
 // The prompt's QKV, o-proj and c_proj projections are plain GEMMs
 // (qwen_infer.cu:462, :542, :593 call the reference's tensor-core GEMM for
-// them), so from 512 rows up they go to the vendor library, whose kernels
-// took 49 / 27 / 58 us for Qwen-1.8B's 2048-row QKV / o-proj / c_proj in a
-// kernel trace of the engine's prefill, against 71 us for QKV and 126 us for
-// o-proj plus c_proj with this library's 128 x 128 MFMA tile.  Below 512 rows the
-// library's kernels were slower than the split-K 64 x 64 tile (20 against 18
-// us for QKV at 127 rows), which stays.  The fused products (the gate/up GEMM
-// with the SwiGLU epilogue, the flash attention) stay hand-written.
+// them), and so are gate and up taken as one product of 2 * inter columns, so
+// from 128 rows up they go to the vendor library.  For Qwen-1.8B its kernels
+// took 49 / 27 / 58 us for the 2048-row QKV / o-proj / c_proj in a kernel trace
+// of the engine's prefill, against 71 us for QKV and 126 us for o-proj plus
+// c_proj with this library's 128 x 128 MFMA tile; whole MFMA prompts of 255 /
+// 383 / 511 tokens took 2.6 / 3.1 / 3.2 ms against 3.2 / 4.5 / 5.1 ms with the
+// split-K 64 x 64 tile.  At 127 rows and fewer the two tie (2.2 ms) and the
+// tile, which needs no heuristic query for a new shape (~0.3 ms per prompt
+// length on first use), stays.  The fused products (the gate/up GEMM with the
+// SwiGLU epilogue below 128 rows, the flash attention) stay hand-written.
 //
 // Row-major y[t][n] = x[t][:] . w[n][:] is the column-major product
 // D (n x t, ld ldy) = op(A) B with A = w viewed as a k x n column-major matrix
@@ -20,6 +23,7 @@
 #include <hipblaslt/hipblaslt.h>
 
 #include <array>
+#include <atomic>
 #include <map>
 #include <mutex>
 
@@ -45,6 +49,7 @@ struct DeviceState {
 
 std::mutex g_mu;
 DeviceState g_state[kMaxDevices];
+std::atomic<int> g_vendor{1};   // qd_gemm_vendor_enable
 
 // Descriptors of one product, destroyed with the object.
 struct Desc {
@@ -78,6 +83,7 @@ long long align_class(const void* x, const void* w, const void* y, const void* r
 }  // namespace
 
 hipError_t blaslt_gemm_nt(const BatchedGemvParams& p, int epi, hipStream_t stream) {
+  if (!g_vendor.load(std::memory_order_relaxed)) return hipErrorNotSupported;
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorNotSupported;
   std::lock_guard<std::mutex> lock(g_mu);
@@ -131,3 +137,5 @@ hipError_t blaslt_gemm_nt(const BatchedGemvParams& p, int epi, hipStream_t strea
 }
 
 }  // namespace qd
+
+extern "C" int qd_gemm_vendor_enable(int enable) { return qd::g_vendor.exchange(enable ? 1 : 0); }

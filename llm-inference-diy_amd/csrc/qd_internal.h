@@ -298,11 +298,15 @@ hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t 
 hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream);
 // qd_blaslt.cpp: the same product (epi 0 or 1) through hipBLASLt;
 // hipErrorNotSupported when the library has no kernel for it (nothing ran).
+// launch_gemm_mfma takes this path from kBlasltMinRows rows up, and the engine
+// then runs gate and up as one product of 2 * inter columns.
+constexpr int kBlasltMinRows = 128;
 hipError_t blaslt_gemm_nt(const BatchedGemvParams& p, int epi, hipStream_t stream);
-// The same, allowed to split K over up to 4 workgroups per tile when the tile
-// grid leaves CUs idle: fp32 partial sums in `workspace` (kGemmSplitWsBytes
-// suffice for every shape), then one launch folds them in slice order and
-// applies the epilogue.  Without a workspace it is launch_gemm_mfma.
+// The same, allowed below kBlasltMinRows rows to split K over up to 4
+// workgroups per tile when the tile grid leaves CUs idle: fp32 partial sums in
+// `workspace` (kGemmSplitWsBytes suffice for every shape), then one launch
+// folds them in slice order and applies the epilogue.  Otherwise, and without
+// a workspace, it is launch_gemm_mfma.
 constexpr size_t kGemmSplitWsBytes = (size_t)4 << 20;
 hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* workspace,
                                   size_t workspace_bytes, hipStream_t stream);

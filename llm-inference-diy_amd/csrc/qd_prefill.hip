@@ -741,7 +741,7 @@ hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t*
 
 hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream) {
   if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
-  if (p.t >= 512) {   // plain products of 512 rows and more: the vendor library (qd_blaslt.cpp)
+  if (p.t >= kBlasltMinRows) {   // plain products from 128 rows: the vendor library (qd_blaslt.cpp)
     const hipError_t e = blaslt_gemm_nt(p, epi, stream);
     if (e != hipErrorNotSupported) return e;
   }
@@ -779,9 +779,10 @@ hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* wo
                                   size_t workspace_bytes, hipStream_t stream) {
   if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
   const long long tiles = (long long)((p.n + kMmTile - 1) / kMmTile) * ((p.t + kMmTile - 1) / kMmTile);
+  // the conditions under which launch_gemm_mfma takes the 64 x 64 tile
   const bool small = p.t < 512 || ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) ||
-                     p.ldy % 4 || p.k % kBk;    // the conditions under which launch_gemm_mfma takes the 64 x 64 tile
-  int splits = small && workspace ? (int)std::min<long long>(4, 256 / tiles) : 1;
+                     p.ldy % 4 || p.k % kBk;
+  int splits = small && workspace && p.t < kBlasltMinRows ? (int)std::min<long long>(4, 256 / tiles) : 1;
   if (splits > 1) {
     // slices of whole K tiles, none empty
     const int kslice = ((p.k + splits - 1) / splits + kMmK - 1) / kMmK * kMmK;

@@ -58,13 +58,23 @@ def test_exact_mode_is_the_decode_gemv(qdiy, m, n, k, with_res):
         assert _same(got[i], want), f"row {i}"
 
 
+@pytest.fixture(params=[True, False], ids=["vendor", "own_tiles"])
+def vendor(qdiy, request):
+    """GEMM_MFMA products from 128 rows in hipBLASLt (the default), or only in
+    the library's own tiles (the 64 x 64 tile below 512 rows, the 128 x 128
+    tile from 512): the fallback when the vendor library has no kernel."""
+    prev = qdiy.gemm_vendor_enable(request.param)
+    yield request.param
+    qdiy.gemm_vendor_enable(prev)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (37, 100, 512), (127, 6144, 2048), (256, 2048, 5504),
                                    (200, 5504, 2048),
-                                   # m >= 512: the 128 x 128 tile (ragged m and n, a partial
-                                   # group of four outputs at n = 130)
+                                   # m >= 512 (own tiles: the 128 x 128 tile; ragged m and n, a
+                                   # partial group of four outputs at n = 130)
                                    (600, 130, 512), (1024, 2048, 5504), (2048, 6144, 2048)])
 @pytest.mark.parametrize("with_res", [False, True])
-def test_mfma_mode_within_fp32_summation_bound(qdiy, m, n, k, with_res):
+def test_mfma_mode_within_fp32_summation_bound(qdiy, vendor, m, n, k, with_res):
     rng = np.random.default_rng(7 * m + n + k + with_res)
     x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
     y = torch.full((m * n + 64,), 9.0, dtype=torch.float16, device="cuda")
@@ -142,10 +152,10 @@ def test_gemm_nt_rejects_bad_arguments(qdiy):
     torch.cuda.synchronize()
 
 
-def test_mfma_large_m_unaligned_output_and_in_place_residual(qdiy):
-    """m >= 512 with y rows an odd number of elements apart (the 64 x 64 tile
-    takes it) and with the residual added in place (the 128 x 128 tile): both
-    within the fp32 summation bound."""
+def test_mfma_large_m_unaligned_output_and_in_place_residual(qdiy, vendor):
+    """m >= 512 with y rows an odd number of elements apart (among the own
+    tiles the 64 x 64 tile takes it) and with the residual added in place (the
+    128 x 128 tile): both within the fp32 summation bound."""
     m, n, k = 640, 96, 256
     rng = np.random.default_rng(3)
     x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
@@ -167,14 +177,15 @@ def test_mfma_large_m_unaligned_output_and_in_place_residual(qdiy):
     assert np.all(np.abs(got - want) <= ulp16(want) + ulp16(h) + bound + ulp16(s))
 
 
-@pytest.mark.parametrize("hidden,inter,n_prompt", [(512, 1368, 300), (2048, 5504, 300), (512, 1408, 700)])
-def test_engine_mfma_prefill(qdiy, hidden, inter, n_prompt):
+@pytest.mark.parametrize("hidden,inter,n_prompt", [(512, 1368, 100), (512, 1368, 300), (2048, 5504, 300),
+                                                  (512, 1408, 700)])
+def test_engine_mfma_prefill(qdiy, vendor, hidden, inter, n_prompt):
     """MFMA prefill against exact prefill on the same prompt (with c_proj exact
     where inter is not a multiple of 64): the next step's logits agree to the
     fp32-order difference, and plain decode steps are bit-identical in both
-    modes.  From 512 prompt tokens the plain products go to the vendor library
-    and the gate/up product is one 2 * inter column product followed by the
-    elementwise SwiGLU; below, the hand-written tiles run."""
+    modes.  From 128 prompt tokens the plain products go to the vendor library
+    (when enabled) and the gate/up product is one 2 * inter column product
+    followed by the elementwise SwiGLU; below, the hand-written tiles run."""
     cfg = qdiy.model_cfg(vocab_size=512, hidden_size=hidden, num_layers=2, num_heads=hidden // 128,
                          intermediate_size=inter, max_seqlen=n_prompt + 20)
     img = qdiy.random_model_image(cfg, 41 + hidden, 0.03, nthreads=8)
