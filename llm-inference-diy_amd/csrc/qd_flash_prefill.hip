@@ -15,8 +15,9 @@
 // LDS store instructions), where both read it, so every K/V row read from
 // memory serves 64 queries.  The next block's loads go out while the current
 // block is computed; the buffers alternate per block, with one workgroup
-// barrier per block.  At the end the four groups' softmax states of each query
-// are folded through LDS.
+// barrier per block.  The tile's Q rows come into LDS once, for all groups.  At
+// the end the four groups' softmax states of each query are folded through LDS
+// by all 512 threads.
 //
 // The two buffers are separate LDS variables and the loop is unrolled by two,
 // so every LDS access names its buffer statically: the compiler then knows that
@@ -80,9 +81,10 @@ __device__ __forceinline__ int vswz(int r) { return 2 * (r & 3); }
 constexpr float kLazy = 8.0f;              // log2 of the largest softmax weight before a rescale
 static_assert(kQWaves * kQTiles * 16 == kFpQueries, "a key group's waves cover the workgroup's queries");
 static_assert(kQWaves * 16 == kFpKeys, "a group's waves load 16 rows of each block");
-// The fold hands groups 1-3's fp32 O rows (64 queries x 128 dims, 32 KB each)
-// through three of the four block buffers and their (m, l) through the fourth.
+// The fold hands each group's fp32 O rows (64 queries x 128 dims, 32 KB) through
+// one of the four block buffers and the (m, l) pairs through the Q rows' space.
 static_assert((size_t)kFpQueries * 128 * 4 == (size_t)kKeyGroups * kBlk * 2, "an O tile fills one buffer");
+static_assert((size_t)kKeyGroups * 2 * kFpQueries * 4 <= (size_t)kFpQueries * kRow * 2, "(m, l) fit in the Q rows");
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -94,6 +96,7 @@ __global__ __launch_bounds__(kKeyGroups * kQWaves * 64) void flash_prefill_kerne
   __shared__ __align__(16) Blk lv0[kKeyGroups];
   __shared__ __align__(16) Blk lk1[kKeyGroups];   // buffer 1
   __shared__ __align__(16) Blk lv1[kKeyGroups];
+  __shared__ __align__(16) _Float16 lq[kFpQueries * kRow];   // the tile's Q rows, chunks swizzled as K's
   const int lane = threadIdx.x & 63;
   const int wave8 = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int kg = wave8 / kQWaves;                // key group: blocks kg, kg + 4, ...
@@ -113,17 +116,21 @@ __global__ __launch_bounds__(kKeyGroups * kQWaves * 64) void flash_prefill_kerne
   const bool active = wq0 < nq;                 // wave-uniform: the wave has queries
   const int wpos = p.pos0 + q0 + wq0;           // the wave's first query position
 
-  // B operand of S^T for tile u: Q[q0 + wq0 + 16 u + c][32 s + 8 g .. +8]
-  // (rows past the last query repeat it; their outputs are not stored)
+  // B operand of S^T for tile u: Q[q0 + wq0 + 16 u + c][32 s + 8 g .. +8],
+  // read from the tile's Q rows in LDS after the first barrier.  The rows come
+  // in once per workgroup (direct loads, like K: wave w moves rows 8 w ..
+  // 8 w + 7); rows past the last query repeat it and their outputs are not
+  // stored.
   f16x8 qb[kQTiles][4];
   int qpos[kQTiles];                            // the lane's query position in tile u
 #pragma unroll
-  for (int u = 0; u < kQTiles; ++u) {
-    const int qi = min(wq0 + 16 * u + c, nq - 1);
-    const uint16_t* qrow = p.q + (long long)(q0 + qi) * p.q_stride + h * 128 + 8 * g;
+  for (int u = 0; u < kQTiles; ++u) qpos[u] = wpos + 16 * u + c;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qb[u][s] = *reinterpret_cast<const f16x8*>(qrow + 32 * s);
-    qpos[u] = wpos + 16 * u + c;
+  for (int i = 0; i < 2; ++i) {
+    const int row = 8 * wave8 + 4 * i + (lane >> 4);
+    __builtin_amdgcn_global_load_lds(p.q + (long long)(q0 + min(row, nq - 1)) * p.q_stride + h * 128 +
+                                         8 * ((lane & 15) ^ kswz(row)),
+                                     (__attribute__((address_space(3))) void*)&lq[(8 * wave8 + 4 * i) * kRow], 16, 0, 0);
   }
 
   // A group's block: 32 rows of K and of V.  Rows past nkeys repeat row
@@ -281,63 +288,69 @@ __global__ __launch_bounds__(kKeyGroups * kQWaves * 64) void flash_prefill_kerne
   if (kg < nblk) dload(kg, lk0, lv0);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+#pragma unroll
+  for (int u = 0; u < kQTiles; ++u)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qb[u][s] = *reinterpret_cast<const f16x8*>(&lq[(wq0 + 16 * u + c) * kRow + 8 * ((4 * s + g) ^ kswz(c))]);
   for (int it = 0; it < nit; it += 2) {
     step(kKeyGroups * it + kg, lk0, lv0, lk1, lv1);
     if (it + 1 < nit) step(kKeyGroups * (it + 1) + kg, lk1, lv1, lk0, lv0);
   }
 
-  // Fold the four key groups' states of each query: groups 1-3 hand (m, l, O)
-  // to group 0 through LDS (the buffers are free after the last barrier).  O
-  // rows are 128 floats with their 16-byte chunks swizzled by the query
-  // (chunk q of query r at q ^ (r % 16)), so the 16 queries of a write fall on
-  // distinct banks.
-  float* const fo[3] = {reinterpret_cast<float*>(&lk1[0][0]), reinterpret_cast<float*>(&lv1[0][0]),
-                        reinterpret_cast<float*>(&lv0[0][0])};   // [query][dim], group 1, 2, 3
-  float* const fml = reinterpret_cast<float*>(&lk0[0][0]);      // [group - 1][m, l][query]
-  if (kg > 0) {
-    float* dst = kg == 1 ? fo[0] : kg == 2 ? fo[1] : fo[2];
+  // Fold the four key groups' states of each query through LDS (the buffers
+  // are free after the last barrier): every group writes its O rows to one of
+  // the four block buffers (128 floats per query, 16-byte chunks swizzled by
+  // the query: chunk q of query r at q ^ (r % 16), so the 16 queries of a write
+  // fall on distinct banks) and its (m, l) to the Q rows' space; then every
+  // thread folds 16 dims of one query.
+  float* const fo[4] = {reinterpret_cast<float*>(&lk0[0][0]), reinterpret_cast<float*>(&lv0[0][0]),
+                        reinterpret_cast<float*>(&lk1[0][0]), reinterpret_cast<float*>(&lv1[0][0])};
+  float* const fml = reinterpret_cast<float*>(&lq[0]);      // [group][m, l][query]
+  {
+    float* dst = kg == 0 ? fo[0] : kg == 1 ? fo[1] : kg == 2 ? fo[2] : fo[3];
 #pragma unroll
     for (int u = 0; u < kQTiles; ++u) {
       const int qq = wq0 + 16 * u + c;
 #pragma unroll
       for (int n = 0; n < 8; ++n) *reinterpret_cast<f32x4*>(dst + qq * 128 + 4 * ((4 * n + g) ^ c)) = o[u][n];
       if (g == 0) {
-        fml[(kg - 1) * 2 * kFpQueries + qq] = m[u];
-        fml[(kg - 1) * 2 * kFpQueries + kFpQueries + qq] = ls[u][0];
+        fml[kg * 2 * kFpQueries + qq] = m[u];
+        fml[kg * 2 * kFpQueries + kFpQueries + qq] = ls[u][0];
       }
     }
   }
   __syncthreads();
-  if (kg == 0 && active) {
+  {
+    const int qq = (int)threadIdx.x >> 3;                    // the thread's query in the tile
+    const int d4 = 4 * ((int)threadIdx.x & 7);               // its first 4-dim chunk: dims 4 d4 .. 4 d4 + 15
+    if (qq < nq) {
+      float mk[kKeyGroups], M = -__builtin_inff();
 #pragma unroll
-    for (int u = 0; u < kQTiles; ++u) {
-      const int qq = wq0 + 16 * u + c;
-      if (qq >= nq) continue;
-      float mk[4] = {m[u], 0.0f, 0.0f, 0.0f}, lk[4] = {ls[u][0], 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int w = 1; w < 4; ++w) {
-        mk[w] = fml[(w - 1) * 2 * kFpQueries + qq];
-        lk[w] = fml[(w - 1) * 2 * kFpQueries + kFpQueries + qq];
+      for (int w = 0; w < kKeyGroups; ++w) {
+        mk[w] = fml[w * 2 * kFpQueries + qq];
+        M = fmaxf(M, mk[w]);                                 // finite: key 0 reaches every query
       }
-      const float M = fmaxf(fmaxf(mk[0], mk[1]), fmaxf(mk[2], mk[3]));   // finite: key 0 reaches every query
-      float a[4], l = 0.0f;
+      float a[kKeyGroups], l = 0.0f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < kKeyGroups; ++w) {
         a[w] = mk[w] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(mk[w] - M);
-        l += a[w] * lk[w];
+        l += a[w] * fml[w * 2 * kFpQueries + kFpQueries + qq];
       }
       const float inv = 1.0f / l;
-      _Float16* orow = reinterpret_cast<_Float16*>(p.out + (long long)(q0 + qq) * p.out_stride + h * 128);
+      f16x8 v[2];
 #pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        f32x4 acc = a[0] * o[u][n];
+      for (int i = 0; i < 4; ++i) {
+        f32x4 acc = a[0] * *reinterpret_cast<const f32x4*>(fo[0] + qq * 128 + 4 * ((d4 + i) ^ (qq & 15)));
 #pragma unroll
-        for (int w = 1; w < 4; ++w) acc += a[w] * *reinterpret_cast<const f32x4*>(fo[w - 1] + qq * 128 + 4 * ((4 * n + g) ^ c));
-        f16x4 v;
+        for (int w = 1; w < kKeyGroups; ++w)
+          acc += a[w] * *reinterpret_cast<const f32x4*>(fo[w] + qq * 128 + 4 * ((d4 + i) ^ (qq & 15)));
 #pragma unroll
-        for (int r = 0; r < 4; ++r) v[r] = (_Float16)(acc[r] * inv);
-        *reinterpret_cast<f16x4*>(orow + 16 * n + 4 * g) = v;
+        for (int r = 0; r < 4; ++r) v[i / 2][4 * (i % 2) + r] = (_Float16)(acc[r] * inv);
       }
+      _Float16* orow = reinterpret_cast<_Float16*>(p.out + (long long)(q0 + qq) * p.out_stride + h * 128 + 4 * d4);
+      *reinterpret_cast<f16x8*>(orow) = v[0];
+      *reinterpret_cast<f16x8*>(orow + 8) = v[1];
     }
   }
 }
