@@ -350,105 +350,145 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* __restrict__
 //
 // Workgroup: 4 waves, a 64-token x 64-row tile; wave w takes tokens
 // 32 (w / 2) .. +32 and rows 32 (w % 2) .. +32 as 2 x 2 MFMA blocks.  K goes
-// in tiles of 256 staged through LDS (rows padded to 264 halves: the 16 lanes
-// of each 16-byte read fall on distinct banks).  The next tile's global loads
-// are in flight in registers while the current tile's 32 MFMAs per wave run;
-// at 8 tiles for K = 2048 the latency of each tile's loads is paid 8 times,
-// not 32.  Two workgroups fit a CU (2 x 67.6 KB of its 160 KB LDS).  Tokens
-// past t and rows past n load clamped rows and are not stored; the K past the
-// end of a partial last tile is staged as zeros, which add nothing.  K must be
-// a multiple of 64.  kEpi 2 is the split-K form: workgroup z = blockIdx.z sums
-// K slice [z kslice, (z + 1) kslice) and stores its fp32 tile to p.part.
-// kEpi 3 is the joint gate/up form: a workgroup takes 32 intermediate rows, its
-// W tile holding them from W1 (tile rows 0..31) and W2 (32..63); wave w's B
-// blocks are gate rows 16 (w % 2) .. +16 and the same up rows, so one lane
-// holds g and u of the same output and writes act = half(g * (u / (1 +
-// exp(-u)))) on the fp16-rounded g and u.
+// in tiles of 64 through a ring of 8 LDS stages (8 KB of X and 8 KB of W each),
+// filled by direct loads (global_load_lds_dwordx4: each thread moves two 16-byte
+// chunks of each operand per stage, no registers), with 7 tiles in flight: a
+// short prompt's product is a chain of memory round trips, not of arithmetic,
+// and one tile in flight per workgroup left each K tile waiting a full round
+// trip (QKV at 127 tokens 17.9 -> 13.2 us, gate/up with the SwiGLU 28.6 -> 24.9
+// us).  Rows are 128 bytes with their 16-byte chunks swizzled (chunk q of row r
+// at q ^ ((r / 2) % 8)), so the 16 rows of one operand read fall on distinct
+// banks.  Each stage is its own LDS variable and the loop is unrolled over the
+// ring, so every access names its stage; the operand reads are inline assembly
+// with their own waits, since the compiler, unable to tell eight stages apart,
+// would wait for every load in flight before each read.  Tiles past the last
+// repeat it, so every thread issues the same loads per stage and the wait
+// counts are fixed.  Tokens past t and rows past n load clamped rows and are
+// not stored.  K must be a multiple of 64.  kEpi 2 is the split-K form:
+// workgroup z = blockIdx.z sums K slice [z kslice, (z + 1) kslice) and stores
+// its fp32 tile to p.part.  kEpi 3 is the joint gate/up form: a workgroup
+// takes 32 intermediate rows, its W tile holding them from W1 (tile rows
+// 0..31) and W2 (32..63); wave w's B blocks are gate rows 16 (w % 2) .. +16
+// and the same up rows, so one lane holds g and u of the same output and writes
+// act = half(g * (u / (1 + exp(-u)))) on the fp16-rounded g and u.
 constexpr int kMmTile = 64;                 // tokens and rows per workgroup
-constexpr int kMmK = 256;                   // K per LDS tile
-constexpr int kMmLd = kMmK + 8;             // LDS row stride in halves
-constexpr int kMmStage = kMmTile * kMmK / 8 / 256;   // 16-byte chunks per thread per operand
+constexpr int kMmK = 64;                    // K per stage
+constexpr int kMmOps = kMmTile * kMmK / 8 / 256;   // direct loads per thread per operand per stage (2)
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 
+struct __align__(16) MmStage {
+  uint16_t x[kMmTile * kMmK];
+  uint16_t w[kMmTile * kMmK];
+};
+// rows r and r + 8 share banks (128-byte rows): (r / 2) % 8 gives the 16 rows
+// of one operand read 16 distinct (row parity, position) pairs
+__device__ __forceinline__ int mmswz(int r) { return (r >> 1) & 7; }
+
 template <int kEpi>
 __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) {
-  __shared__ __align__(16) uint16_t xs[kMmTile * kMmLd];
-  __shared__ __align__(16) uint16_t ws[kMmTile * kMmLd];
+  __shared__ MmStage s0, s1, s2, s3, s4, s5, s6, s7;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int n0 = blockIdx.x * (kEpi == 3 ? kMmTile / 2 : kMmTile);
   const int t0 = blockIdx.y * kMmTile;
-  // staging map: chunk c = tid + 256 i is row c / 32 of the tile, halves
-  // 8 (c % 32) .. +8 of its K tile
-  int sr[kMmStage], sc[kMmStage];
-  const uint16_t* xg[kMmStage];
-  const uint16_t* wg[kMmStage];
-#pragma unroll
-  for (int i = 0; i < kMmStage; ++i) {
-    const int c = tid + 256 * i;
-    sr[i] = c >> 5;
-    sc[i] = (c & 31) * 8;
-    xg[i] = p.x + (long long)min(t0 + sr[i], p.t - 1) * p.ldx + sc[i];
-    if constexpr (kEpi == 3)
-      wg[i] = (sr[i] < 32 ? p.w : p.w2) + (long long)min(n0 + (sr[i] & 31), p.n - 1) * p.k + sc[i];
-    else
-      wg[i] = p.w + (long long)min(n0 + sr[i], p.n - 1) * p.k + sc[i];
-  }
   int kbeg = 0, kend = p.k;
   if constexpr (kEpi == 2) {
     kbeg = blockIdx.z * p.kslice;
     kend = min(p.k, kbeg + p.kslice);
   }
-  f16x8 xr[kMmStage], wr[kMmStage];
-  const f16x8 zero = {};
-  auto fetch = [&](int k0) {
+  const int ktiles = kend > kbeg ? (kend - kbeg) / kMmK : 0;
+
+  // Load i of wave w writes 1 KB at chunk 256 i + 64 w + lane of the stage's
+  // operand: row 32 i + 8 w + lane / 8, position lane % 8.
+  const uint16_t* xg[kMmOps];
+  const uint16_t* wg[kMmOps];
 #pragma unroll
-    for (int i = 0; i < kMmStage; ++i) {
-      if (k0 + sc[i] < kend) {
-        xr[i] = *reinterpret_cast<const f16x8*>(xg[i] + k0);
-        wr[i] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(wg[i] + k0));
-      } else {
-        xr[i] = zero;
-        wr[i] = zero;
-      }
+  for (int i = 0; i < kMmOps; ++i) {
+    const int row = 32 * i + 8 * wave + (lane >> 3);
+    const int ch = (lane & 7) ^ mmswz(row);
+    xg[i] = p.x + (long long)min(t0 + row, p.t - 1) * p.ldx + kbeg + 8 * ch;
+    if constexpr (kEpi == 3)
+      wg[i] = (row < 32 ? p.w : p.w2) + (long long)min(n0 + (row & 31), p.n - 1) * p.k + kbeg + 8 * ch;
+    else
+      wg[i] = p.w + (long long)min(n0 + row, p.n - 1) * p.k + kbeg + 8 * ch;
+  }
+  auto issue = [&](int kt, MmStage& st) {
+    const long long ko = (long long)min(kt, ktiles - 1) * kMmK;
+#pragma unroll
+    for (int i = 0; i < kMmOps; ++i) {
+      __builtin_amdgcn_global_load_lds(xg[i] + ko, (__attribute__((address_space(3))) void*)&st.x[(256 * i + 64 * wave) * 8],
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(wg[i] + ko, (__attribute__((address_space(3))) void*)&st.w[(256 * i + 64 * wave) * 8],
+                                       16, 0, 0);
     }
   };
+
   const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  const int fr = lane & 15, fg = lane >> 4;
   f32x4_t acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const int ktiles = kend > kbeg ? (kend - kbeg + kMmK - 1) / kMmK : 0;
-  if (ktiles > 0) fetch(kbeg);
-  for (int kt = 0; kt < ktiles; ++kt) {
-    __syncthreads();                           // every wave is done with the previous tile
+  // Byte offsets within a stage of the lane's A (X) and B (W) fragments for K
+  // step ks of the tile: A[fr][8 fg .. +8] of token block i, B of row block j.
+  unsigned aoff[2][2], boff[2][2];
 #pragma unroll
-    for (int i = 0; i < kMmStage; ++i) {
-      *reinterpret_cast<f16x8*>(&xs[sr[i] * kMmLd + sc[i]]) = xr[i];
-      *reinterpret_cast<f16x8*>(&ws[sr[i] * kMmLd + sc[i]]) = wr[i];
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int ar = wm + 16 * i + fr;
+      aoff[ks][i] = (unsigned)((ar * kMmK + 8 * ((4 * ks + fg) ^ mmswz(ar))) * 2);
+      const int br = (kEpi == 3 ? 32 * i + 16 * (wave & 1) : wn + 16 * i) + fr;
+      boff[ks][i] = (unsigned)((kMmTile * kMmK + br * kMmK + 8 * ((4 * ks + fg) ^ mmswz(br))) * 2);
     }
-    __syncthreads();
-    if (kt + 1 < ktiles) fetch(kbeg + (kt + 1) * kMmK);
-    const int kn = min(kMmK, kend - kbeg - kt * kMmK);   // a multiple of 64
-    for (int ks = 0; ks < kn; ks += 32) {
-      f16x8 a[2], b[2];
+  auto compute = [&](const MmStage& st) {
+    const unsigned base = (unsigned)(size_t)(const __attribute__((address_space(3))) void*)&st;
+    f16x8 a[2][2], b[2][2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        a[i] = *reinterpret_cast<const f16x8*>(&xs[(wm + 16 * i + fr) * kMmLd + ks + fk]);
-        const int br = kEpi == 3 ? 32 * i + 16 * (wave & 1) : wn + 16 * i;
-        b[i] = *reinterpret_cast<const f16x8*>(&ws[(br + fr) * kMmLd + ks + fk]);
+        asm volatile("ds_read_b128 %0, %1" : "=v"(a[ks][i]) : "v"(base + aoff[ks][i]) : "memory");
+        asm volatile("ds_read_b128 %0, %1" : "=v"(b[ks][i]) : "v"(base + boff[ks][i]) : "memory");
       }
+    asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(a[0][0]), "+v"(a[0][1]), "+v"(b[0][0]), "+v"(b[0][1]));
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+      for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[0][i], b[0][j], acc[i][j], 0, 0, 0);
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[1][0]), "+v"(a[1][1]), "+v"(b[1][0]), "+v"(b[1][1]));
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[1][i], b[1][j], acc[i][j], 0, 0, 0);
+  };
+  // Tile kt sits in stage kt % 8.  Each thread waits for its own loads of it
+  // (6 newer stages of 4 loads each stay in flight) and for its reads of the
+  // previous stage; after the barrier every thread's part of tile kt is in LDS
+  // and the previous stage, read by all, takes tile kt + 7.  The barrier is
+  // s_barrier alone: __syncthreads' fence would wait for every load in flight.
+  auto body = [&](int kt, const MmStage& cur, MmStage& prev) {
+    asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    issue(kt + 7, prev);
+    compute(cur);
+  };
+  if (ktiles > 0) {
+    issue(0, s0); issue(1, s1); issue(2, s2); issue(3, s3); issue(4, s4); issue(5, s5); issue(6, s6);
+    for (int kt = 0; kt < ktiles; kt += 8) {
+      body(kt, s0, s7);
+      if (kt + 1 < ktiles) body(kt + 1, s1, s0);
+      if (kt + 2 < ktiles) body(kt + 2, s2, s1);
+      if (kt + 3 < ktiles) body(kt + 3, s3, s2);
+      if (kt + 4 < ktiles) body(kt + 4, s4, s3);
+      if (kt + 5 < ktiles) body(kt + 5, s5, s4);
+      if (kt + 6 < ktiles) body(kt + 6, s6, s5);
+      if (kt + 7 < ktiles) body(kt + 7, s7, s6);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeated tail loads land before the workgroup ends
   }
   if constexpr (kEpi == 3) {
     // blocks (i, 0) and (i, 1): gate and up of row n0 + 16 (w % 2) + l % 16 for
