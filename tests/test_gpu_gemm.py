@@ -137,6 +137,62 @@ def test_gemm_swiglu_within_bound(qdiy, m, n, k, ldy):
     assert np.mean(np.abs(swapped - got) > tol) > 0.5
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_mfma_random_shapes(qdiy, vendor, seed):
+    """Seeded random m (both sides of the 128-row vendor threshold and of the
+    64-token tile), n (ragged against 64), k (a multiple of 64 up to 6144, so the
+    K-tile ring wraps several times or runs short of its 8 stages), row strides
+    and the residual form of qd_gemm_nt, then qd_gemm_swiglu at the same m:
+    every output within the bounds of the fixed-shape tests."""
+    rng = np.random.default_rng(52000 + seed)
+    m = int(rng.integers(1, 130)) if rng.random() < 0.6 else int(rng.integers(130, 700))
+    n = int(rng.integers(1, 700))
+    k = 64 * int(rng.integers(1, 97))
+    ldy = n + int(rng.integers(0, 9))
+    with_res = bool(rng.random() < 0.5)
+    x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
+    y = torch.full((m * ldy + 64,), 9.0, dtype=torch.float16, device="cuda")
+    if with_res:
+        yv = y[:m * ldy].view(m, ldy)
+        yv[:, :n] = torch.from_numpy(R).cuda()
+    qdiy.gemm_nt(_dev(x.reshape(-1)), _dev(W.reshape(-1)), y, m, n, k, residual=y if with_res else None,
+                 mode=qdiy.GEMM_MFMA, ldy=ldy)
+    torch.cuda.synchronize()
+    out = y.cpu().numpy()
+    assert np.all(out[m * ldy:] == np.float16(9.0)), "write past the end of y"
+    rows = out[:m * ldy].reshape(m, ldy)
+    if ldy > n:
+        assert np.all(rows[:, n:] == np.float16(9.0)), "write into a row's padding"
+    got = rows[:, :n].astype(np.float64)
+    x64, W64 = x.astype(np.float64), W.astype(np.float64)
+    s = x64 @ W64.T
+    bound = k * 2.0 ** -23 * (np.abs(x64) @ np.abs(W64).T)
+    if with_res:
+        h = s.astype(np.float16).astype(np.float64)
+        want = R.astype(np.float64) + h
+        tol = ulp16(want) + ulp16(h) + bound + ulp16(s)
+    else:
+        want, tol = s, ulp16(s) + bound
+    assert np.all(np.abs(got - want) <= tol), (m, n, k, ldy, with_res, float(np.max(np.abs(got - want) - tol)))
+    # gate and up with the SwiGLU epilogue at the same m (ldy = n)
+    W1, W2 = normal_f16(rng, (n, k), 0.03), normal_f16(rng, (n, k), 0.03)
+    act = torch.full((m * n + 64,), 9.0, dtype=torch.float16, device="cuda")
+    qdiy.gemm_swiglu(_dev(x.reshape(-1)), _dev(W1.reshape(-1)), _dev(W2.reshape(-1)), act, m, n, k)
+    torch.cuda.synchronize()
+    a = act.cpu().numpy()
+    assert np.all(a[m * n:] == np.float16(9.0)), "write past the last row"
+    got = a[:m * n].reshape(m, n).astype(np.float64)
+    W1d, W2d = W1.astype(np.float64), W2.astype(np.float64)
+    g, u = x64 @ W1d.T, x64 @ W2d.T
+    ax = np.abs(x64)
+    bg, bu = k * 2.0 ** -23 * (ax @ np.abs(W1d).T), k * 2.0 ** -23 * (ax @ np.abs(W2d).T)
+    gh, uh = g.astype(np.float16).astype(np.float64), u.astype(np.float16).astype(np.float64)
+    silu = uh / (1.0 + np.exp(-uh))
+    want = gh * silu
+    tol = np.abs(silu) * (ulp16(gh) + bg) + np.abs(gh) * 1.1 * (ulp16(uh) + bu) + 2 * ulp16(want)
+    assert np.all(np.abs(got - want) <= tol), (m, n, k, float(np.max(np.abs(got - want) - tol)))
+
+
 def test_gemm_nt_rejects_bad_arguments(qdiy):
     x = torch.zeros(4 * 96, dtype=torch.float16, device="cuda")
     w = torch.zeros(16 * 96, dtype=torch.float16, device="cuda")

@@ -154,6 +154,28 @@ def test_mfma_mode_within_2e3(qdiy, H, pos0, T, layout, q_pad, out_pad):
         pr.close()
 
 
+@pytest.mark.parametrize("seed", range(24))
+def test_mfma_mode_random_prompts(qdiy, seed):
+    """Seeded random head counts, cache layouts, positions, query counts (ragged
+    against the 64-query tiles and 32-key blocks) and Q / out row padding: every
+    query within 2e-3 of float64, nothing written outside the output rows."""
+    rng = np.random.default_rng(91000 + seed)
+    H = int(rng.integers(1, 17))
+    pos0 = int(rng.integers(0, 1200)) if rng.random() < 0.6 else 0
+    T = int(rng.integers(1, 80)) if rng.random() < 0.4 else int(rng.integers(80, 420))
+    layout = ("engine", "head_major")[int(rng.integers(0, 2))]
+    q_pad, out_pad = 8 * int(rng.integers(0, 4)), 8 * int(rng.integers(0, 4))
+    pr = Prompt(qdiy, H, pos0, T, seed=91000 + seed, layout=layout, q_pad=q_pad, out_pad=out_pad)
+    try:
+        got = pr.run(qdiy, qdiy.GEMM_MFMA).astype(np.float64)
+        want = causal_fp64(pr.Q.astype(np.float64), pr.K.astype(np.float64), pr.V.astype(np.float64), pos0)
+        err = np.abs(got - want)
+        assert np.all(np.isfinite(got))
+        assert float(err.max()) <= 2e-3, (H, pos0, T, layout, float(err.max()))
+    finally:
+        pr.close()
+
+
 def test_mfma_mode_logit_spike(qdiy):
     """Keys equal to the last query dominate its softmax (logits ~ |q|^2 / sqrt(128)
     ~ 11 against ~N(0,1)): the running-max rescaling keeps every output in bounds."""
