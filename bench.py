@@ -44,6 +44,7 @@ and of a 2048-token one, exact and with the projections on the matrix cores).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
        python bench.py --only call|scan|merge|read|empty --kv L [--steps K]   (for rocprofv3)
+       python bench.py --only prefill --kv T [--steps K]   (MFMA prefill attention of T tokens)
 """
 from __future__ import annotations
 
@@ -203,6 +204,29 @@ def profile_loop(lib, L: int, only: str, steps: int, warmup: int, variant: int, 
     log(f"[bench] profile loop '{only}' at L={L}: {warmup + steps} launches, {n_layers} layers "
         f"rotated, plan {'fused' if d.variant == qdiy.FUSED else 'split'}x{d.num_splits}"
         f"{' merge in kernel' if d.merge_in_kernel else ''}")
+    ctx.close()
+
+
+def prefill_attention_loop(T: int, steps: int, warmup: int):
+    """For a profiler: warmup + steps calls of qd_prefill_attention in the MFMA mode
+    (the causal FlashAttention kernel) over a T-token prompt at position 0, 16 heads,
+    the engine's cache layout, fp16 N(0,1) inputs; nothing else launched after the
+    inputs are made."""
+    import torch
+
+    import qdiy
+
+    torch.manual_seed(0)
+    q = torch.randn(T, H * D, device="cuda").half()
+    k = torch.randn(T, H * D, device="cuda").half()
+    v = torch.randn(T, H * D, device="cuda").half()
+    out = torch.empty_like(q)
+    ctx = qdiy.Context(num_heads=H, max_seqlen=T)
+    torch.cuda.synchronize()
+    for _ in range(warmup + steps):
+        ctx.prefill_attention(q, k, v, out, 0, T, qdiy.GEMM_MFMA)
+    torch.cuda.synchronize()
+    log(f"[bench] profile loop 'prefill' at T={T}: {warmup + steps} qd_prefill_attention calls (MFMA)")
     ctx.close()
 
 
@@ -476,10 +500,11 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one 256 MiB device copy (known FETCH_SIZE/WRITE_SIZE) and exit")
-    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty"],
+    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty", "prefill"],
                     help="for a profiler: run warmup + steps launches of this loop per --kv length "
                          "(call: qd_decode_attention; scan / merge: that kernel alone; read: the "
-                         "read-ceiling kernel; empty: empty kernels), print no JSON, and exit")
+                         "read-ceiling kernel; empty: empty kernels; prefill: qd_prefill_attention "
+                         "in the MFMA mode over a --kv-token prompt), print no JSON, and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -506,6 +531,10 @@ def main() -> int:
         return 0
     lib = bench_lib()
     variant = {"auto": 0, "fused": 1, "split": 2}[args.variant]
+    if args.only == "prefill":
+        for T in args.kv:
+            prefill_attention_loop(T, args.steps, args.warmup)
+        return 0
     if args.only:
         for L in args.kv:
             profile_loop(lib, L, args.only, args.steps, args.warmup, variant, args.splits)
