@@ -681,9 +681,10 @@ int qd_engine_logits(qd_engine* e, uint16_t* host_logits) {
 int qd_engine_kv_rows(qd_engine* e, int layer, int pos0, int n, uint16_t* host_k, uint16_t* host_v) {
   int rc = check_engine(e);
   if (rc != QD_OK) return rc;
-  if (layer < 0 || layer >= e->cfg.num_layers || pos0 < 0 || n < 0 || pos0 + n > e->cfg.max_seqlen)
-    return fail(QD_EINVAL, "rows [%d, %d) of layer %d outside the cache (%d layers, %d rows)", pos0,
-                pos0 + n, layer, e->cfg.num_layers, e->cfg.max_seqlen);
+  if (layer < 0 || (uint32_t)layer >= e->cfg.num_layers || pos0 < 0 || n < 0 ||
+      (long long)pos0 + n > (long long)e->cfg.max_seqlen)
+    return fail(QD_EINVAL, "rows [%d, %lld) of layer %d outside the cache (%u layers, %u rows)", pos0,
+                (long long)pos0 + n, layer, e->cfg.num_layers, e->cfg.max_seqlen);
   hipError_t he = hipStreamSynchronize(e->stream);
   const size_t off = (size_t)pos0 * e->cfg.hidden_size, bytes = (size_t)n * e->cfg.hidden_size * 2;
   if (he == hipSuccess && host_k && n) he = hipMemcpy(host_k, e->kc(layer) + off, bytes, hipMemcpyDeviceToHost);

@@ -245,6 +245,167 @@ __global__ __launch_bounds__(gemv_waves(NJ) * 64) void gemv_batched_kernel(Batch
   }
 }
 
+// Four weight rows per wave, for K <= 2048 (NJ <= 4).  The fp16 x fp16 -> fp32
+// FMA (v_fma_mix_f32) issues at ~0.6x the rate of the plain fp32 FMA on gfx950
+// (35-37 against 52-59 T FMA/s in an ALU-only loop), so here both operands
+// reach the FMA as fp32: the weights are converted once into registers and the
+// token tile is staged in LDS as fp32.  That doubles the LDS bytes per token;
+// four rows per wave (each token value feeds four FMAs) keep the LDS reads per
+// FMA where two fp16 rows had them.  Each lane's sums and the wave reduction
+// are the decode order, so the outputs are gemv_batched_kernel's bit for bit
+// (an fp16 -> fp32 conversion is exact and the FMA rounds once either way).
+// The LDS reads (16 KB per wave and token pair) and two waves per SIMD (224
+// VGPRs) bound it, not the FMA rate: 6-12% faster than the two-row kernel.
+constexpr int kR4Waves = 4;     // waves per workgroup: 16 rows
+constexpr int kR4Tile = 8;      // tokens per LDS tile (64 KB at K = 2048)
+constexpr int r4_stage(int nj) { return (kR4Tile * nj * 64 + kR4Waves * 64 - 1) / (kR4Waves * 64); }
+constexpr int kDppRowRor12 = 0x12C;
+
+// The eight sums of a 2-token x 4-row block, v[q] with q = token + 2 * row,
+// reduced over the wave in one transposed butterfly.  Afterwards lane 8 + q of
+// each 16-lane row holds block output q's total.  As in block4_sum, every total
+// is the sum wave64_sum forms, node for node: lanes i, i^1 split the tokens;
+// lanes i, i^2 the rows' low bit (each lane then holds a quad sum of its own
+// output); lanes i, i^4 the rows' high bit while adding quad pairs (Q0 + Q1,
+// Q2 + Q3: wave64_sum's half-row mirror step); row_ror 8 adds the half-rows
+// (the mirror step); then xor 16 and xor 32 add the rows.
+__device__ __forceinline__ float block8_sum(const float (&v)[8], int lane) {
+  const bool b0 = lane & 1, b1 = lane & 2, b2 = lane & 4;
+  float k[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float keep = b0 ? v[2 * r + 1] : v[2 * r];
+    const float give = b0 ? v[2 * r] : v[2 * r + 1];
+    k[r] = keep + dpp_mov<kDppQuadSwap1>(give);
+  }
+  float m[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float keep = b1 ? k[2 * i + 1] : k[2 * i];
+    const float give = b1 ? k[2 * i] : k[2 * i + 1];
+    m[i] = keep + dpp_mov<kDppQuadSwap2>(give);
+  }
+  const float keep = b2 ? m[1] : m[0];
+  const float give = b2 ? m[0] : m[1];
+  // lane i ^ 4 within the row: i - 4 for lanes with bit 2 set, i + 4 otherwise.
+  // Both moves run in every lane before the select: under a branch a DPP move's
+  // partner lanes would be inactive and read as zero.
+  float up = dpp_mov<kDppRowRor4>(give), dn = dpp_mov<kDppRowRor12>(give);
+  asm volatile("" : "+v"(up), "+v"(dn));
+  float s = keep + (b2 ? up : dn);
+  s += dpp_mov<kDppRowRor8>(s);
+  s += __shfl_xor(s, 16);
+  s += __shfl_xor(s, 32);
+  return s;
+}
+
+// Y[t][n] for n in this workgroup's 16 rows and t in its kTokPerWg tokens;
+// wave w holds rows n0 = 16 bx + 4 w .. n0 + 3.  The LDS tile is fp32, each
+// token row split so that a lane's two 16-byte reads of a chunk are contiguous
+// across the wave: chunk c = 64 j + l of a row keeps elements 0..3 at float4
+// 128 j + l and 4..7 at float4 128 j + 64 + l.  Staging, prefetch of the next
+// tile and the epilogues are gemv_batched_kernel's.
+template <int NJ, int kEpi>
+__global__ __launch_bounds__(kR4Waves * 64) void gemv_batched_r4_kernel(BatchedGemvParams p) {
+  static_assert(NJ <= 4, "four fp32 rows per lane fit in registers up to K = 2048");
+  extern __shared__ __align__(16) float xf[];           // [kR4Tile][NJ * 512]
+  constexpr int kStage = r4_stage(NJ);
+  constexpr int kRow = NJ * 512;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int K = p.k;
+  const int rem = K - 512 * (NJ - 1);
+  const bool tail = 8 * lane < rem;
+  const int n0 = blockIdx.x * (4 * kR4Waves) + 4 * wave;
+  float wf[4][NJ][8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int n = min(n0 + r, p.n - 1);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      f16x8 h = {};
+      if (j < NJ - 1 || tail)
+        h = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p.w + (long long)n * K + 512 * j + 8 * lane));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wf[r][j][e] = (float)h[e];
+    }
+  }
+  const int t_begin = blockIdx.y * kTokPerWg;
+  const int t_end = min(p.t, t_begin + kTokPerWg);
+  const int chunks = K / 8;
+  int st_tok[kStage], st_kc[kStage];
+  f16x8 stage[kStage];
+#pragma unroll
+  for (int i = 0; i < kStage; ++i) {
+    const int c = threadIdx.x + i * kR4Waves * 64;
+    st_tok[i] = c / chunks;
+    st_kc[i] = c - st_tok[i] * chunks;
+  }
+  auto fetch = [&](int t0, int nt) {
+#pragma unroll
+    for (int i = 0; i < kStage; ++i) {
+      const int tk = min(st_tok[i], nt - 1);
+      stage[i] = *reinterpret_cast<const f16x8*>(p.x + (long long)(t0 + tk) * p.ldx + st_kc[i] * 8);
+    }
+  };
+  if (t_begin < t_end) fetch(t_begin, min(kR4Tile, t_end - t_begin));
+  for (int t0 = t_begin; t0 < t_end; t0 += kR4Tile) {
+    const int nt = min(kR4Tile, t_end - t0);
+    __syncthreads();                                     // previous tile fully consumed
+#pragma unroll
+    for (int i = 0; i < kStage; ++i)
+      if (st_tok[i] < nt) {
+        const int kc = st_kc[i];
+        float* dst = xf + st_tok[i] * kRow + 4 * (128 * (kc >> 6) + (kc & 63));
+        const f16x8 h = stage[i];
+        *reinterpret_cast<float4*>(dst) = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+        *reinterpret_cast<float4*>(dst + 256) = make_float4((float)h[4], (float)h[5], (float)h[6], (float)h[7]);
+      }
+    __syncthreads();
+    if (t0 + kR4Tile < t_end) fetch(t0 + kR4Tile, min(kR4Tile, t_end - t0 - kR4Tile));
+    for (int tt = 0; tt < nt; tt += 2) {
+      const bool two = tt + 1 < nt;
+      const float* x0 = xf + tt * kRow;
+      const float* x1 = xf + (two ? tt + 1 : tt) * kRow;
+      float acc[8] = {};                                 // [row][token]
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        if (j < NJ - 1 || tail) {
+          const float4 u0a = *reinterpret_cast<const float4*>(x0 + 4 * (128 * j + lane));
+          const float4 u0b = *reinterpret_cast<const float4*>(x0 + 4 * (128 * j + 64 + lane));
+          const float4 u1a = *reinterpret_cast<const float4*>(x1 + 4 * (128 * j + lane));
+          const float4 u1b = *reinterpret_cast<const float4*>(x1 + 4 * (128 * j + 64 + lane));
+          const float u0[8] = {u0a.x, u0a.y, u0a.z, u0a.w, u0b.x, u0b.y, u0b.z, u0b.w};
+          const float u1[8] = {u1a.x, u1a.y, u1a.z, u1a.w, u1b.x, u1b.y, u1b.z, u1b.w};
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              acc[2 * r] = __builtin_fmaf(wf[r][j][e], u0[e], acc[2 * r]);
+              acc[2 * r + 1] = __builtin_fmaf(wf[r][j][e], u1[e], acc[2 * r + 1]);
+            }
+        }
+      }
+      const float sum = block8_sum(acc, lane);
+      const int q = lane - 8;                            // lanes 8..15 store
+      if (q >= 0 && q < 8) {
+        const int t = t0 + tt + (q & 1);
+        const int n = n0 + (q >> 1);
+        if ((two || (q & 1) == 0) && n < p.n) {
+          const _Float16 y = to_f16(sum);
+          _Float16* dst = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
+          if constexpr (kEpi == 0) {
+            *dst = y;
+          } else {
+            const float r = (float)reinterpret_cast<const _Float16*>(p.res)[(long long)t * p.ldy + n];
+            *dst = (_Float16)(r + (float)y);
+          }
+        }
+      }
+    }
+  }
+}
+
 // Bias, rotate-half RoPE and KV append for token t at position pos0 + t, with
 // qkv_bias_rope_cache_kernel's arithmetic (qd_rope_cache.hip) element by
 // element: one thread per (head, four consecutive rotation pairs), 16 threads
@@ -751,6 +912,27 @@ hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float ep
 hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t stream) {
   const int nj = (p.k + 511) / 512;
   if (nj < 1 || nj > 16) return hipErrorInvalidValue;
+  // Four rows per wave where it measured faster: K in (1536, 2048] with n >= 2048
+  // (QKV, gate/up and o_proj of hidden 2048 in prompt chunks of up to 256 tokens:
+  // 6-12% per launch).  Narrow products have too few workgroups for its 16-row
+  // workgroups of four waves, and at 2048 x 2048 with 2048 tokens it ran 5% slower.
+  if (nj == 4 && p.n >= 2048 && (p.t <= 256 || p.n >= 4096)) {
+    const dim3 grid((p.n + 4 * kR4Waves - 1) / (4 * kR4Waves), (p.t + kTokPerWg - 1) / kTokPerWg);
+    const size_t lds = (size_t)kR4Tile * nj * 512 * sizeof(float);
+    switch (nj * 2 + epi) {
+#define QD_CASE(n)                                                                                  \
+    case 2 * n:                                                                                      \
+      hipLaunchKernelGGL((gemv_batched_r4_kernel<n, 0>), grid, dim3(kR4Waves * 64), lds, stream, p); \
+      break;                                                                                         \
+    case 2 * n + 1:                                                                                  \
+      hipLaunchKernelGGL((gemv_batched_r4_kernel<n, 1>), grid, dim3(kR4Waves * 64), lds, stream, p); \
+      break;
+      QD_CASE(1) QD_CASE(2) QD_CASE(3) QD_CASE(4)
+#undef QD_CASE
+      default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const int waves = gemv_waves(nj);
   const dim3 grid((p.n + 2 * waves - 1) / (2 * waves), (p.t + kTokPerWg - 1) / kTokPerWg);
   const size_t lds = (size_t)tok_tile(nj) * nj * 512 * sizeof(uint16_t);
