@@ -255,7 +255,8 @@ __global__ __launch_bounds__(gemv_waves(NJ) * 64) void gemv_batched_kernel(Batch
 // are the decode order, so the outputs are gemv_batched_kernel's bit for bit
 // (an fp16 -> fp32 conversion is exact and the FMA rounds once either way).
 // The LDS reads (16 KB per wave and token pair) and two waves per SIMD (224
-// VGPRs) bound it, not the FMA rate: 6-12% faster than the two-row kernel.
+// VGPRs) bound it, not the FMA rate: 4.5-12% faster than the two-row kernel
+// at n >= 4096.
 constexpr int kR4Waves = 4;     // waves per workgroup: 16 rows
 constexpr int kR4Tile = 8;      // tokens per LDS tile (64 KB at K = 2048)
 constexpr int r4_stage(int nj) { return (kR4Tile * nj * 64 + kR4Waves * 64 - 1) / (kR4Waves * 64); }
@@ -912,11 +913,12 @@ hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float ep
 hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t stream) {
   const int nj = (p.k + 511) / 512;
   if (nj < 1 || nj > 16) return hipErrorInvalidValue;
-  // Four rows per wave where it measured faster: K in (1536, 2048] with n >= 2048
-  // (QKV, gate/up and o_proj of hidden 2048 in prompt chunks of up to 256 tokens:
-  // 6-12% per launch).  Narrow products have too few workgroups for its 16-row
-  // workgroups of four waves, and at 2048 x 2048 with 2048 tokens it ran 5% slower.
-  if (nj == 4 && p.n >= 2048 && (p.t <= 256 || p.n >= 4096)) {
+  // Four rows per wave where it measured faster: K in (1536, 2048] with n >= 4096
+  // (QKV and the gate/up rows of hidden 2048: 4.5-5% per launch inside the
+  // engine's prefill, cold weights).  At n = 2048 (o_proj) it was no faster at
+  // 127 tokens and 4% slower in 256-token chunks; narrower products have too few
+  // workgroups for its 16-row workgroups of four waves.
+  if (nj == 4 && p.n >= 4096) {
     const dim3 grid((p.n + 4 * kR4Waves - 1) / (4 * kR4Waves), (p.t + kTokPerWg - 1) / kTokPerWg);
     const size_t lds = (size_t)kR4Tile * nj * 512 * sizeof(float);
     switch (nj * 2 + epi) {

@@ -40,11 +40,11 @@ def _dev(a):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (37, 100, 520), (127, 6144, 2048), (256, 2048, 5504),
-                                   (45, 2056, 1544), (300, 4100, 2000)])
+                                   (45, 4104, 1544), (300, 4100, 2000)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_exact_mode_is_the_decode_gemv(qdiy, m, n, k, with_res):
     """Exact-mode rows against the oracle's decode GEMV, bit for bit.  From K = 1544 to
-    2048 with n >= 2048 the four-rows-per-wave kernel runs: (45, 2056, 1544) has a last
+    2048 with n >= 4096 the four-rows-per-wave kernel runs: (45, 4104, 1544) has a last
     chunk of one lane, rows past n clamped in the last workgroup and odd token tiles;
     (300, 4100, 2000) more than 256 tokens.  The rows checked straddle the 8-token
     tiles and the 32-token workgroups."""
