@@ -254,9 +254,10 @@ __global__ __launch_bounds__(gemv_waves(NJ) * 64) void gemv_batched_kernel(Batch
 // FMA where two fp16 rows had them.  Each lane's sums and the wave reduction
 // are the decode order, so the outputs are gemv_batched_kernel's bit for bit
 // (an fp16 -> fp32 conversion is exact and the FMA rounds once either way).
-// The LDS reads (16 KB per wave and token pair) and two waves per SIMD (224
-// VGPRs) bound it, not the FMA rate: 4.5-12% faster than the two-row kernel
-// at n >= 4096.
+// At 224 VGPRs only two waves share a SIMD, so LDS round trips and the
+// per-tile barriers stay exposed: at 127 tokens it uses ~40% of the fp32 FMA
+// issue rate and ~25% of the LDS read rate, 4.5-12% faster than the two-row
+// kernel at n >= 4096.
 constexpr int kR4Waves = 4;     // waves per workgroup: 16 rows
 constexpr int kR4Tile = 8;      // tokens per LDS tile (64 KB at K = 2048)
 constexpr int r4_stage(int nj) { return (kR4Tile * nj * 64 + kR4Waves * 64 - 1) / (kR4Waves * 64); }
