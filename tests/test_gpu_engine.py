@@ -250,6 +250,14 @@ def test_engine_rejects_bad_input(qdiy, tmp_path):
             eng.step(1000, 0)                                 # token outside the vocabulary
         with pytest.raises(qdiy.QdError):
             eng.step(1, 600)                                  # pos == max_seqlen
+        with pytest.raises(qdiy.QdError):
+            eng.kv_rows(0, 590, 20)                           # rows past max_seqlen
+        with pytest.raises(qdiy.QdError):
+            eng.kv_rows(0, 2**31 - 8, 16)                     # pos0 + n past INT_MAX
+        with pytest.raises(qdiy.QdError):
+            eng.kv_rows(cfg.num_layers, 0, 1)                 # layer outside the model
+        k, v = eng.kv_rows(0, 0, 0)                           # an empty range is valid
+        assert k.shape == (0, cfg.hidden_size) and v.shape == (0, cfg.hidden_size)
 
 
 @pytest.mark.parametrize("how", ["default", "flag", "env"])
