@@ -31,9 +31,11 @@ namespace {
 constexpr float kLog2e = 1.44269504088896340736f;
 
 // Tokens per workgroup of the batched GEMV; tokens per LDS tile (up to 8, so
-// that a tile of NJ * 512 fp16 elements per token stays within 64 KB).
+// that a tile of NJ * 512 fp16 elements per token stays within 64 KB).  The
+// tile is even: tokens are consumed in pairs, and an odd tile would end every
+// tile on a half-used pair step.
 constexpr int kTokPerWg = 32;
-constexpr int tok_tile(int nj) { return nj <= 8 ? 8 : 64 / nj; }
+constexpr int tok_tile(int nj) { return nj <= 8 ? 8 : (64 / nj) & ~1; }
 // Waves per workgroup, two rows each.  From NJ = 15 (K > 7168) the weights
 // (16 * NJ VGPRs) and the unrolled sums no longer fit the 256 VGPRs a wave has
 // at two waves per SIMD, so those workgroups have 4 waves (one per SIMD, whose
