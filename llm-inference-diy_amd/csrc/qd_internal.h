@@ -196,6 +196,8 @@ struct BatchedGemvParams {
   // Joint gate/up form only (launch_gemm_mfma_swiglu): W2, the up weight, with
   // w as W1 and y = act.
   const uint16_t* w2;
+  // Exact two-row form only: tokens per workgroup (0: 32); set by launch_gemv_batched.
+  int tok_per_wg = 0;
 };
 
 // Causal prefill attention of `tokens` queries at positions pos0, pos0 + 1, ...

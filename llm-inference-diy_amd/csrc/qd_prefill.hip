@@ -21,6 +21,7 @@
 //   swiglu_batched_kernel      act = half(g * (u / (1 + exp(-u))))
 // Attention runs per token with qd_decode_attention's plan for that length.
 #include <algorithm>
+#include <atomic>
 
 #include "qd_device.h"
 #include "qd_internal.h"
@@ -161,8 +162,9 @@ __global__ __launch_bounds__(gemv_waves(NJ) * 64) void gemv_batched_kernel(Batch
       wb[j] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p.w + (long long)nb * K + 512 * j + 8 * lane));
     }
   }
-  const int t_begin = blockIdx.y * kTokPerWg;
-  const int t_end = min(p.t, t_begin + kTokPerWg);
+  const int tpw = p.tok_per_wg > 0 ? p.tok_per_wg : kTokPerWg;
+  const int t_begin = blockIdx.y * tpw;
+  const int t_end = min(p.t, t_begin + tpw);
   // This thread's staging chunks: chunk c = tid + 512 i is token c / chunks of
   // the tile, 16-byte chunk c % chunks of its row.  Up to NJ = 11 the map is
   // kept in registers and the next tile's loads are in flight while the
@@ -913,6 +915,19 @@ hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float ep
   return hipGetLastError();
 }
 
+// Compute units of the current device, read once per device.
+static int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cached[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
 hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t stream) {
   const int nj = (p.k + 511) / 512;
   if (nj < 1 || nj > 16) return hipErrorInvalidValue;
@@ -939,15 +954,27 @@ hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t 
     return hipGetLastError();
   }
   const int waves = gemv_waves(nj);
-  const dim3 grid((p.n + 2 * waves - 1) / (2 * waves), (p.t + kTokPerWg - 1) / kTokPerWg);
+  // From K > 4096 (one workgroup per CU) a workgroup takes 64 tokens instead of 32
+  // when the grid still covers every CU and the last 64-token block is more than
+  // half full: each weight row is then loaded half as often (c_proj at K = 5504:
+  // 78.9 -> 70.4 us at 127 tokens, 152.9 -> 139.9 us at 256).  Narrower grids and
+  // ragged last blocks ran slower that way.  Each output's sum is the same either way.
+  BatchedGemvParams q = p;
+  q.tok_per_wg = kTokPerWg;
+  if (nj >= 9) {
+    const long long wgs = (long long)((p.n + 2 * waves - 1) / (2 * waves)) * ((p.t + 63) / 64);
+    const int rem = p.t % 64;
+    if (wgs >= device_cus() && (rem == 0 || rem > 32)) q.tok_per_wg = 64;
+  }
+  const dim3 grid((p.n + 2 * waves - 1) / (2 * waves), (p.t + q.tok_per_wg - 1) / q.tok_per_wg);
   const size_t lds = (size_t)tok_tile(nj) * nj * 512 * sizeof(uint16_t);
   switch (nj * 2 + epi) {
 #define QD_CASE(n)                                                                                  \
     case 2 * n:                                                                                      \
-      hipLaunchKernelGGL((gemv_batched_kernel<n, 0>), grid, dim3(waves * 64), lds, stream, p);       \
+      hipLaunchKernelGGL((gemv_batched_kernel<n, 0>), grid, dim3(waves * 64), lds, stream, q);       \
       break;                                                                                         \
     case 2 * n + 1:                                                                                  \
-      hipLaunchKernelGGL((gemv_batched_kernel<n, 1>), grid, dim3(waves * 64), lds, stream, p);       \
+      hipLaunchKernelGGL((gemv_batched_kernel<n, 1>), grid, dim3(waves * 64), lds, stream, q);       \
       break;
     QD_CASE(1) QD_CASE(2) QD_CASE(3) QD_CASE(4) QD_CASE(5) QD_CASE(6) QD_CASE(7) QD_CASE(8)
     QD_CASE(9) QD_CASE(10) QD_CASE(11) QD_CASE(12) QD_CASE(13) QD_CASE(14) QD_CASE(15) QD_CASE(16)

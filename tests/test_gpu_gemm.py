@@ -46,8 +46,9 @@ def test_exact_mode_is_the_decode_gemv(qdiy, m, n, k, with_res):
     """Exact-mode rows against the oracle's decode GEMV, bit for bit.  From K = 1544 to
     2048 with n >= 4096 the four-rows-per-wave kernel runs: (45, 4104, 1544) has a last
     chunk of one lane, rows past n clamped in the last workgroup and odd token tiles;
-    (300, 4100, 2000) more than 256 tokens.  The rows checked straddle the 8-token
-    tiles and the 32-token workgroups."""
+    (300, 4100, 2000) more than 256 tokens.  (256, 2048, 5504) runs 64 tokens per
+    workgroup in 4-token tiles.  The rows checked straddle the token tiles and the 32-
+    and 64-token workgroups."""
     rng = np.random.default_rng(m * 1000 + n + k + with_res)
     x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
     y = torch.zeros(m * n, dtype=torch.float16, device="cuda")
@@ -55,7 +56,7 @@ def test_exact_mode_is_the_decode_gemv(qdiy, m, n, k, with_res):
                  residual=_dev(R.reshape(-1)) if with_res else None, mode=qdiy.GEMM_EXACT)
     torch.cuda.synchronize()
     got = y.cpu().numpy().reshape(m, n)
-    rows = sorted({i for i in (0, 1, 7, 8, 31, 32, m // 2, m - 2, m - 1) if 0 <= i < m})
+    rows = sorted({i for i in (0, 1, 7, 8, 31, 32, 63, 64, m // 2, m - 2, m - 1) if 0 <= i < m})
     for i in rows:
         if with_res:
             want = oracle.proj_residual(x[i], W.reshape(-1), R[i], n, k)
