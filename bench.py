@@ -30,7 +30,11 @@ launch.  The merge kernel is timed the same way (config.merge_kernel_us).
 config.read_ceiling_us is a load-only kernel over the same layers in the
 scan's launch shape: what one kernel streaming those bytes takes on this box.
 config.empty_kernel_us is an empty kernel of the merge's grid launched back to
-back: the dispatch floor any dependent launch pays.
+back: the dispatch floor any dependent launch pays.  config.read_sweep_L8192 times
+the same L=8192 bytes read by kernels of 161 other launch shapes (1, 2 or 4 waves
+per SIMD; 8-64 KB in flight per wave; contiguous, grid-strided, per-head and
+head-group access patterns); config.read_ceiling_best_us is the fastest of them:
+what any one-launch design reading those bytes could reach on this box.
 
 The CPU baseline is the repository's C restatement of the reference kernels
 (oracle/) on the host cores of the same box, on a bounded sample of the same
@@ -45,6 +49,7 @@ and of a 2048-token one, exact and with the projections on the matrix cores).
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
        python bench.py --only call|scan|merge|read|empty --kv L [--steps K]   (for rocprofv3)
        python bench.py --only prefill --kv T [--steps K]   (MFMA prefill attention of T tokens)
+       python bench.py --only sweep --kv L [--steps K]     (read-ceiling sweep over launch shapes)
 """
 from __future__ import annotations
 
@@ -101,6 +106,7 @@ def bench_lib():
     lib.qd_bench_decode_attention.argtypes = [vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
     lib.qd_bench_read_ceiling.argtypes = [vp, vp, ll, ll, i, i, i, vp, vp]
     lib.qd_bench_empty.argtypes = [i, i, vp]
+    lib.qd_bench_read_sweep.argtypes = [vp, vp, ll, i, i, i, i, i, i, i, i, i, vp, vp]
     lib.qd_bench_attn_front.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
     return lib
 
@@ -173,6 +179,55 @@ def read_loop(lib, L, n_layers, kc, vc, sh):
                                      n_layers, 256, iters, sink.data_ptr(), sh) != 0:
             raise RuntimeError("read-ceiling launch failed")
     return fn
+
+
+# Read-ceiling sweep shapes: (threads per workgroup, workgroups per CU) -> 1, 2 or 4
+# waves per SIMD on 256 CUs; loads per lane per stream (K and V) in flight: 8, 16,
+# 32 or 64 KB per wave at 2, 4, 8, 16; patterns: 0 contiguous per workgroup, 1 the
+# scan's per-head 256-byte slices, 2 grid-strided contiguous chunks, 3 per-head slices
+# with the rows dealt to the splits in blocks of one workgroup load round, 4-6
+# workgroups over 4, 8 or 16 heads reading 1, 2 or 4 KB of each row.
+SWEEP_SHAPES = [(256, 1), (512, 1), (256, 2), (1024, 1), (512, 2), (256, 4)]
+SWEEP_LOADS = (2, 4, 8, 16)
+SWEEP_PATTERNS = {0: "contiguous", 1: "per-head slices", 2: "grid-strided chunks",
+                  3: "per-head slices, split-interleaved blocks", 4: "4-head (1 KB) row slices",
+                  5: "8-head (2 KB) row slices", 6: "whole rows (16 heads)"}
+
+
+def read_sweep(lib, L, n_layers, kc, vc, sh, steps, num_cus):
+    """Times the read-sweep kernels over the same layers' K and V rows: us per launch,
+    back to back, for every shape in SWEEP_SHAPES x SWEEP_LOADS x SWEEP_PATTERNS.
+    Returns {name: us} and the best (name, us)."""
+    import torch
+
+    sink = torch.empty(65536 * 16, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream()
+    out = {}
+    for threads, per_cu in SWEEP_SHAPES:
+        grid = num_cus * per_cu
+        for loads in SWEEP_LOADS:
+            if threads == 1024 and loads == 16:
+                continue
+            for pat in SWEEP_PATTERNS:
+                def fn(iters):
+                    return lib.qd_bench_read_sweep(kc.data_ptr(), vc.data_ptr(), L * HID * 2, L, HID * 2,
+                                                   H, n_layers, threads, loads, pat, grid, iters,
+                                                   sink.data_ptr(), sh)
+                rc = fn(max(20, n_layers))
+                if rc == 1:
+                    continue          # shape does not divide this length's rows
+                if rc != 0:
+                    raise RuntimeError(f"read sweep launch failed ({threads}, {grid}, {loads}, {pat})")
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                fn(steps)
+                e1.record(stream)
+                e1.synchronize()
+                out[f"t{threads}_g{grid}_u{loads}_p{pat}"] = round(e0.elapsed_time(e1) * 1e3 / steps, 3)
+    best = min(out.items(), key=lambda kv: kv[1])
+    log(f"[bench] read sweep L={L}: best {best[0]} {best[1]:.2f} us "
+        f"({2 * L * HID * 2 / best[1] / 1e3:.0f} GB/s) over {len(out)} shapes")
+    return out, best
 
 
 def empty_loop(lib, sh, grid=H):
@@ -260,6 +315,7 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     warm_calls, warm_ms = warm_up(cold, warmup)
     us_cold = timed(steps, cold)
     scan_us = merge_us = ceiling_us = floor_us = None
+    sweep, sweep_best = None, (None, None)
     tail = max(20, int(WARMUP_TAIL_S / (us_cold * 1e-6)))
     if detail:
         # the call's kernels on their own, back to back over the same layers
@@ -282,6 +338,11 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     hot = lambda n: run(n, 1)
     warm_up(hot, warmup, floor_s=0.0)
     us_hot = timed(steps, hot)
+    if detail and L == HEADLINE_L:
+        # the same bytes read by other launch shapes: what any one-launch design could
+        # reach (last, so that its thousands of launches disturb no other figure)
+        num_cus = torch.cuda.get_device_properties(0).multi_processor_count
+        sweep, sweep_best = read_sweep(lib, L, n_layers, kc, vc, sh, max(steps, 200), num_cus)
     if not torch.isfinite(out).all():
         raise RuntimeError("non-finite attention output")
     d = ctx.plan_detail(L, {0: "auto", 1: "fused", 2: "split"}[variant], splits)
@@ -301,7 +362,8 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
            "layers": n_layers, "plan": f"{plan[0]}x{plan[1]}", "kernel": kernel,
            "warmup_calls": warm_calls, "warmup_ms": round(warm_ms, 1),
            "scan_us": scan_us, "merge_us": merge_us, "read_ceiling_us": ceiling_us,
-           "launch_floor_us": floor_us}
+           "launch_floor_us": floor_us, "read_sweep": sweep, "read_best_shape": sweep_best[0],
+           "read_best_us": sweep_best[1]}
     extra = ""
     if detail:
         res["scan_gbps"] = scan_bytes(L) / (scan_us * 1e-6) / 1e9
@@ -500,7 +562,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one 256 MiB device copy (known FETCH_SIZE/WRITE_SIZE) and exit")
-    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty", "prefill"],
+    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty", "prefill", "sweep"],
                     help="for a profiler: run warmup + steps launches of this loop per --kv length "
                          "(call: qd_decode_attention; scan / merge: that kernel alone; read: the "
                          "read-ceiling kernel; empty: empty kernels; prefill: qd_prefill_attention "
@@ -534,6 +596,16 @@ def main() -> int:
     if args.only == "prefill":
         for T in args.kv:
             prefill_attention_loop(T, args.steps, args.warmup)
+        return 0
+    if args.only == "sweep":
+        num_cus = torch.cuda.get_device_properties(0).multi_processor_count
+        for L in args.kv:
+            n_layers, kc, vc, _, _ = kv_layers(L)
+            sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            sweep, best = read_sweep(lib, L, n_layers, kc, vc, sh, args.steps, num_cus)
+            print(json.dumps({"L": L, "best": best, "sweep": sweep}), flush=True)
+            del kc, vc
+            torch.cuda.empty_cache()
         return 0
     if args.only:
         for L in args.kv:
@@ -597,6 +669,9 @@ def main() -> int:
             "merge_kernel_us": per_l("merge_us"),
             "read_ceiling_us": per_l("read_ceiling_us"),
             "read_ceiling_gbps": per_l("ceiling_gbps", 1),
+            "read_ceiling_best_us": head.get("read_best_us"),
+            "read_ceiling_best_shape": head.get("read_best_shape"),
+            "read_sweep_L8192": head.get("read_sweep"),
             "empty_kernel_us": per_l("launch_floor_us"),
             "traffic_over_algorithmic": {str(L): t.get("traffic_over_algorithmic")
                                          for L, t in traffic.items()},

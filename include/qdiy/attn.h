@@ -144,8 +144,14 @@ int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc), since
  * qd_ctx_create allocates.  Same outputs, bit for bit, as qd_decode_attention
- * with a context of these strides on the current device (same plan and
- * kernels); the KV strides are passed here instead of through a qd_cfg.
+ * with a default context (QD_MERGE_AUTO) of these strides on the current
+ * device: the same plan, with its partials folded by the merge kernel, whose
+ * fold is the in-kernel merge's, operation for operation; the KV strides are
+ * passed here instead of through a qd_cfg.  The plan depends on the device's
+ * workgroup placement over its XCDs, which the first call on a device probes
+ * (unless a context was created on it before): one small kernel on the null
+ * stream and a synchronous 1 KiB device-to-host copy, so make that first
+ * call outside graph capture.
  * The split partials live in a static device array (520 KiB per GPU, held
  * until the process ends) instead of context scratch, so the call makes no
  * hipMalloc/hipFree and no other allocating call.  Limit: the plan's

@@ -23,7 +23,9 @@ extern "C" {
  * itself.  A loop of scan-only calls times the call's dominant kernel back
  * to back; a merge-only call folds whatever partials the context's scratch
  * holds (the last scan's), so its output is meaningful only right after a
- * scan-only call of the same seqlen.  Arguments as qd_decode_attention. */
+ * scan-only call of the same seqlen.  A merge-only call at a length whose
+ * plan has no merge kernel (fused, or merged inside the scan kernel) returns
+ * QD_EINVAL.  Arguments as qd_decode_attention. */
 int qd_decode_attention_stage(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_layer,
                               const uint16_t* v_layer, uint16_t* out, int seqlen,
                               int num_heads, int head_dim, int stages, hipStream_t stream);

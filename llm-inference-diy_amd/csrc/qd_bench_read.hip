@@ -45,6 +45,156 @@ __global__ __launch_bounds__(256) void read_ceiling_kernel(const u32x4* __restri
     sink[blockIdx.x] = acc;
 }
 
+// Read-ceiling sweep: the same bytes (one layer's K and V: `rows` rows of
+// row_units 16-byte units each) read by kernels of other launch shapes, to find
+// what any one-launch design reading them could reach.  NT threads per
+// workgroup, U 16-byte loads per lane per stream (K and V) issued before any is
+// folded (2 * U * 16 * 64 bytes in flight per wave), `grid` workgroups.
+//   kPattern 0: workgroup w reads a contiguous 1/grid of each stream;
+//   kPattern 1: the scan kernel's per-head slices -- workgroup (split c, head h)
+//     with blockIdx.x = c * heads + h reads the 256-byte slice h of rows
+//     [c * rows / splits, ...), four rows per wave instruction (lane l: row
+//     4u + l / 16, bytes 16 (l % 16) of the slice);
+//   kPattern 2: grid-strided chunks -- round i of workgroup w reads chunk
+//     w + grid * i of NT * U units, so the whole grid reads one contiguous
+//     region of each stream per round;
+//   kPattern 3: per-head slices as in kPattern 1, but the rows in blocks of
+//     B = 4 U NT / 64 (one load round of the workgroup) dealt to the splits in
+//     turn: split c reads blocks c, c + splits, ..., so at any time the grid
+//     reads one contiguous run of rows, as in kPattern 2;
+//   kPattern 4, 5, 6: workgroups over groups of 4, 8 or 16 heads (HPW) --
+//     workgroup (split c, head group g) with blockIdx.x = c * (heads / HPW) + g
+//     reads the HPW * 256 contiguous bytes of group g in rows [c * rows /
+//     splits, ...); every wave instruction reads 1 KB of one row (four heads'
+//     slices), the workgroup's waves covering a row's HPW / 4 such pieces.
+template <int NT, int U, int kPattern>
+__global__ __launch_bounds__(NT) void read_sweep_kernel(const u32x4* __restrict__ k,
+                                                        const u32x4* __restrict__ v,
+                                                        unsigned total_units, unsigned row_units,
+                                                        int heads, u32x4* sink) {
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const unsigned tid = threadIdx.x;
+  if constexpr (kPattern == 0) {
+    const unsigned per_wg = total_units / gridDim.x;
+    const unsigned base = blockIdx.x * per_wg;
+    for (unsigned i = tid; i < per_wg; i += NT * U) {
+      u32x4 a[U], b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(k + base + min(i + NT * u, per_wg - 1u));
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __builtin_nontemporal_load(v + base + min(i + NT * u, per_wg - 1u));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
+    }
+  } else if constexpr (kPattern == 1) {
+    const unsigned splits = gridDim.x / heads;
+    const unsigned h = blockIdx.x % heads, c = blockIdx.x / heads;
+    const unsigned rows = total_units / row_units;
+    const unsigned rps = rows / splits;
+    const unsigned wave = tid >> 6, lane = tid & 63;
+    const unsigned col = h * 16u + (lane & 15u);
+    const unsigned r0 = c * rps;
+    constexpr unsigned kWaves = NT / 64;
+    for (unsigned blk = wave * 4u * U; blk < rps; blk += kWaves * 4u * U) {
+      u32x4 a[U], b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const unsigned r = r0 + min(blk + 4u * u + (lane >> 4), rps - 1u);
+        a[u] = __builtin_nontemporal_load(k + r * row_units + col);
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const unsigned r = r0 + min(blk + 4u * u + (lane >> 4), rps - 1u);
+        b[u] = __builtin_nontemporal_load(v + r * row_units + col);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
+    }
+  } else if constexpr (kPattern == 3) {
+    const unsigned splits = gridDim.x / heads;
+    const unsigned h = blockIdx.x % heads, c = blockIdx.x / heads;
+    const unsigned rows = total_units / row_units;
+    const unsigned wave = tid >> 6, lane = tid & 63;
+    const unsigned col = h * 16u + (lane & 15u);
+    constexpr unsigned kBlock = (NT / 64) * 4u * U;
+    for (unsigned b0 = c * kBlock; b0 < rows; b0 += splits * kBlock) {
+      const unsigned rb = b0 + wave * 4u * U + (lane >> 4);
+      u32x4 a[U], b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(k + min(rb + 4u * u, rows - 1u) * row_units + col);
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __builtin_nontemporal_load(v + min(rb + 4u * u, rows - 1u) * row_units + col);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
+    }
+  } else if constexpr (kPattern >= 4) {
+    constexpr unsigned kHpw = kPattern == 4 ? 4u : kPattern == 5 ? 8u : 16u;
+    constexpr unsigned kPieces = kHpw / 4;                 // 1 KB pieces per row
+    static_assert(NT / 64 >= kPieces, "a workgroup covers at least one row");
+    constexpr unsigned kRowsPerLoad = (NT / 64) / kPieces;
+    const unsigned groups = heads / kHpw;
+    const unsigned splits = gridDim.x / groups;
+    const unsigned g = blockIdx.x % groups, c = blockIdx.x / groups;
+    const unsigned rows = total_units / row_units;
+    const unsigned rps = rows / splits;
+    const unsigned wave = tid >> 6, lane = tid & 63;
+    const unsigned col = g * (kHpw * 16u) + (wave % kPieces) * 64u + lane;
+    const unsigned r0 = c * rps;
+    for (unsigned r = wave / kPieces; r < rps; r += kRowsPerLoad * U) {
+      u32x4 a[U], b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(k + (r0 + min(r + kRowsPerLoad * u, rps - 1u)) * row_units + col);
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __builtin_nontemporal_load(v + (r0 + min(r + kRowsPerLoad * u, rps - 1u)) * row_units + col);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
+    }
+  } else {
+    constexpr unsigned kChunk = NT * U;
+    const unsigned chunks = total_units / kChunk;
+    for (unsigned ch = blockIdx.x; ch < chunks; ch += gridDim.x) {
+      const unsigned base = ch * kChunk + tid;
+      u32x4 a[U], b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(k + base + NT * u);
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __builtin_nontemporal_load(v + base + NT * u);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
+    }
+  }
+  if (acc.x == 0x9E3779B9u && acc.y == 0x7F4A7C15u && acc.z == 0x85EBCA6Bu && acc.w == 0xC2B2AE35u)
+    sink[blockIdx.x] = acc;
+}
+
+typedef void (*SweepKernel)(const u32x4*, const u32x4*, unsigned, unsigned, int, u32x4*);
+
+// The sweep's shapes: (threads per workgroup, loads per lane per stream).
+struct SweepShape {
+  int nt, u;
+  SweepKernel fn[7];
+};
+
+#define QD_SWEEP_SHAPE(NT, U)                                                               \
+  SweepShape {                                                                              \
+    NT, U, { read_sweep_kernel<NT, U, 0>, read_sweep_kernel<NT, U, 1>, read_sweep_kernel<NT, U, 2>, \
+             read_sweep_kernel<NT, U, 3>, read_sweep_kernel<NT, U, 4>, read_sweep_kernel<NT, U, 5>, \
+             read_sweep_kernel<NT, U, 6> }                                                    \
+  }
+
+const SweepShape kSweepShapes[] = {
+    QD_SWEEP_SHAPE(256, 2),  QD_SWEEP_SHAPE(256, 4),  QD_SWEEP_SHAPE(256, 8),
+    QD_SWEEP_SHAPE(256, 16), QD_SWEEP_SHAPE(512, 2),  QD_SWEEP_SHAPE(512, 4),
+    QD_SWEEP_SHAPE(512, 8),  QD_SWEEP_SHAPE(512, 16), QD_SWEEP_SHAPE(1024, 2),
+    QD_SWEEP_SHAPE(1024, 4), QD_SWEEP_SHAPE(1024, 8),
+};
+#undef QD_SWEEP_SHAPE
+
 // Does nothing: back-to-back launches of it time the dispatch floor, the cost
 // any dependent kernel (such as a separate merge launch) pays before its work.
 __global__ __launch_bounds__(256) void empty_kernel() {}
@@ -79,6 +229,49 @@ int qd_bench_empty(int grid, int iters, hipStream_t stream) {
   if (grid < 1 || iters < 0) return 1;
   for (int it = 0; it < iters; ++it) {
     hipLaunchKernelGGL(empty_kernel, dim3(grid), dim3(256), 0, stream);
+    if (hipGetLastError() != hipSuccess) return 2;
+  }
+  return 0;
+}
+
+
+// `iters` launches of one read-sweep kernel, launch i reading layer
+// i % n_layers (`rows` rows of row_bytes bytes of K at k + layer *
+// layer_stride_bytes, and of V).  threads in {256, 512, 1024}, loads in
+// {2, 4, 8, 16} (not 16 with 1024 threads), pattern 0-6 (read_sweep_kernel),
+// grid workgroups; patterns 1 and 3 need grid a multiple of heads and 16
+// units per head in a row (pattern 1 also rows a multiple of grid / heads;
+// patterns 4-6 heads a multiple of 4, 8, 16 and rows of grid / (heads / 4, 8,
+// 16) splits),
+// patterns 0 and 2 a whole number of units per workgroup or chunk.  Returns 0, or 1 for arguments outside those.
+int qd_bench_read_sweep(const void* k, const void* v, long long layer_stride_bytes, int rows,
+                        int row_bytes, int heads, int n_layers, int threads, int loads,
+                        int pattern, int grid, int iters, void* sink, hipStream_t stream) {
+  if (!k || !v || !sink || rows < 1 || row_bytes < 16 || row_bytes % 16 || heads < 1 ||
+      n_layers < 1 || grid < 1 || grid > 65536 || iters < 0 || pattern < 0 || pattern > 6)
+    return 1;
+  const long long units = (long long)rows * (row_bytes / 16);
+  if (units > 0xFFFFFFFFLL) return 1;
+  const SweepShape* shape = nullptr;
+  for (const SweepShape& s : kSweepShapes)
+    if (s.nt == threads && s.u == loads) shape = &s;
+  if (!shape) return 1;
+  if (pattern == 0 && units % grid) return 1;
+  if (pattern == 1 && (grid % heads || rows % (grid / heads) || row_bytes / 16 != 16 * heads)) return 1;
+  if (pattern == 2 && units % ((long long)threads * loads)) return 1;
+  if (pattern == 3 && (grid % heads || row_bytes / 16 != 16 * heads)) return 1;
+  if (pattern >= 4) {
+    const int hpw = pattern == 4 ? 4 : pattern == 5 ? 8 : 16;
+    if (heads % hpw || threads / 64 < hpw / 4 || row_bytes / 16 != 16 * heads) return 1;
+    const int groups = heads / hpw;
+    if (grid % groups || rows % (grid / groups)) return 1;
+  }
+  for (int it = 0; it < iters; ++it) {
+    const long long off = (long long)(it % n_layers) * layer_stride_bytes;
+    hipLaunchKernelGGL(shape->fn[pattern], dim3(grid), dim3(threads), 0, stream,
+                       reinterpret_cast<const u32x4*>(static_cast<const char*>(k) + off),
+                       reinterpret_cast<const u32x4*>(static_cast<const char*>(v) + off),
+                       (unsigned)units, (unsigned)(row_bytes / 16), heads, static_cast<u32x4*>(sink));
     if (hipGetLastError() != hipSuccess) return 2;
   }
   return 0;

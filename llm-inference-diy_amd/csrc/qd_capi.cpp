@@ -96,8 +96,45 @@ qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
   return plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, requested);
 }
 
-qd::AttnPlan plan_auto(int num_cus, int num_heads, int seqlen) {
-  return seqlen <= kFusedMaxRows ? plan_fused(seqlen) : plan_split(num_cus, num_heads, seqlen, 0);
+// The automatic plan: fused up to fused_max rows, else the automatic split.
+qd::AttnPlan plan_auto(int num_cus, int num_heads, int seqlen, int fused_max) {
+  return seqlen <= fused_max ? plan_fused(seqlen) : plan_split(num_cus, num_heads, seqlen, 0);
+}
+
+// Round-robin period of workgroup dispatch over the XCDs of `device` (workgroup
+// i of a 256-workgroup launch on XCD (k + i) mod period; 1 if every workgroup
+// ran on one XCD, 0 if the placement was not round-robin in three tries).
+// Probed once per device and process, into the 256-word device buffer
+// `probe_buf` (whose contents it overwrites) with one kernel on the null
+// stream and a synchronous 1 KiB copy to the host; later calls return the
+// cached answer, so every context and every allocation-free call of a process
+// plans the same way on one device.  Must be called with `device` current.
+int dispatch_period(int device, unsigned* probe_buf, int* period) {
+  static std::mutex mu;
+  static int cached[64];
+  static bool probed[64];
+  std::lock_guard<std::mutex> lock(mu);
+  const int slot = device >= 0 && device < 64 ? device : -1;
+  if (slot >= 0 && probed[slot]) {
+    *period = cached[slot];
+    return QD_OK;
+  }
+  constexpr int kProbe = 256;
+  unsigned xcc[kProbe];
+  int p = 0;
+  for (int attempt = 0; attempt < 3 && p == 0; ++attempt) {
+    hipError_t e;
+    if ((e = qd::launch_xcd_probe(probe_buf, kProbe, nullptr)) != hipSuccess ||
+        (e = hipMemcpy(xcc, probe_buf, sizeof(xcc), hipMemcpyDeviceToHost)) != hipSuccess)
+      return hip_fail(e, "XCD placement probe");
+    p = qd::round_robin_period(xcc, kProbe);
+  }
+  if (slot >= 0) {
+    probed[slot] = true;
+    cached[slot] = p;
+  }
+  *period = p;
+  return QD_OK;
 }
 
 // Whether the context's split plans can merge in the scan kernel: it found
@@ -113,7 +150,7 @@ int fused_max_rows(const qd_ctx* ctx) {
 }
 
 qd::AttnPlan plan_auto(const qd_ctx* ctx, int seqlen) {
-  return seqlen <= fused_max_rows(ctx) ? plan_fused(seqlen) : plan_split(ctx, seqlen, 0);
+  return plan_auto(ctx->num_cus, ctx->cfg.num_heads, seqlen, fused_max_rows(ctx));
 }
 
 
@@ -393,38 +430,16 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   }
   if ((e = hipMemset(ctx->xcnt, 0, xcnt_bytes)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMemset of the merge counters"));
-  // Probe which XCD each workgroup of a 256-workgroup launch runs on, into the
-  // slot area (cleared afterwards).  Round-robin with period n (workgroup i on
-  // XCD (k + i) mod n for some start k) puts every split of head h on one XCD
-  // when num_heads is a multiple of n; a single XCD for all is period 1.
-  // Anything else, in three tries, leaves the in-kernel merge off (it would
-  // still be correct, but would re-scan the splits it cannot see).  The
-  // device's first context probes; later ones reuse its answer, so every
-  // context of a process plans the same way on one device.
+  // Which XCD each workgroup runs on, probed into the slot area (cleared
+  // afterwards).  Round-robin with period n (workgroup i on XCD (k + i) mod n
+  // for some start k) puts every split of head h on one XCD when num_heads is
+  // a multiple of n; a single XCD for all is period 1.  Anything else leaves
+  // the in-kernel merge off (it would still be correct, but would re-scan the
+  // splits it cannot see).
   {
-    static std::mutex probe_mu;
-    static int probed_period[64];
-    static bool probed[64];
-    std::lock_guard<std::mutex> lock(probe_mu);
-    const int slot = ctx->device >= 0 && ctx->device < 64 ? ctx->device : -1;
     int period = 0;
-    if (slot >= 0 && probed[slot]) {
-      period = probed_period[slot];
-    } else {
-      constexpr int kProbe = 256;
-      unsigned xcc[kProbe];
-      unsigned* dprobe = reinterpret_cast<unsigned*>(ctx->xpart);
-      for (int attempt = 0; attempt < 3 && period == 0; ++attempt) {
-        if ((e = qd::launch_xcd_probe(dprobe, kProbe, nullptr)) != hipSuccess ||
-            (e = hipMemcpy(xcc, dprobe, sizeof(xcc), hipMemcpyDeviceToHost)) != hipSuccess)
-          return cleanup(hip_fail(e, "XCD placement probe"));
-        period = qd::round_robin_period(xcc, kProbe);
-      }
-      if (slot >= 0) {
-        probed[slot] = true;
-        probed_period[slot] = period;
-      }
-    }
+    const int rc = dispatch_period(ctx->device, reinterpret_cast<unsigned*>(ctx->xpart), &period);
+    if (rc != QD_OK) return cleanup(rc);
     if ((e = hipMemset(ctx->xpart, 0, xpart_bytes)) != hipSuccess ||
         (e = hipDeviceSynchronize()) != hipSuccess)
       return cleanup(hip_fail(e, "clearing the in-kernel merge slots"));
@@ -650,6 +665,10 @@ int qd_decode_attention_stage(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
   if (rc != QD_OK) return rc;
   if (stages < 1 || stages > (QD_STAGE_SCAN | QD_STAGE_MERGE))
     return fail(QD_EINVAL, "stages %d is not a non-empty set of QD_STAGE_SCAN, QD_STAGE_MERGE", stages);
+  const qd::AttnPlan plan = finish_plan(ctx, plan_auto(ctx, seqlen), seqlen);
+  if (stages == QD_STAGE_MERGE && (plan.variant == 0 || plan.xmerge))
+    return fail(QD_EINVAL, "seqlen %d plans %s: there is no merge kernel to run alone", seqlen,
+                plan.variant == 0 ? "one fused launch" : "the merge inside the scan kernel");
   return run_attention(ctx, q, k_layer, v_layer, out, seqlen, plan_auto(ctx, seqlen), stream,
                        stages);
 }
@@ -699,8 +718,23 @@ int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, cons
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   e = hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev);
   if (e != hipSuccess || num_cus < 1) return hip_fail(e, "hipDeviceGetAttribute(multiProcessorCount)");
-  // the plan qd_decode_attention picks for a context of this device and head count
-  const qd::AttnPlan plan = plan_auto(num_cus, num_heads, seqlen);
+  float* scratch_o = nullptr;
+  float2* scratch_ml = nullptr;
+  int rc = qd::static_scratch(&scratch_o, &scratch_ml);
+  if (rc != QD_OK) return rc;
+  // The plan qd_decode_attention picks with a default context of this device
+  // and head count: such a context merges split plans inside the scan kernel,
+  // and so runs fused plans only up to kFusedMaxRowsX rows, when the device's
+  // dispatch is round-robin with a period dividing num_heads (probed once per
+  // device; here into the static scratch, whose contents need not survive).
+  // The partials are folded by a merge kernel here, which gives the in-kernel
+  // merge's bits.
+  int period = 0;
+  rc = dispatch_period(dev, reinterpret_cast<unsigned*>(scratch_o), &period);
+  if (rc != QD_OK) return rc;
+  const bool ctx_merges_in_kernel = period > 0 && num_heads % period == 0;
+  const qd::AttnPlan plan = plan_auto(num_cus, num_heads, seqlen,
+                                      ctx_merges_in_kernel ? kFusedMaxRowsX : kFusedMaxRows);
   const long long slots = (long long)num_heads * plan.splits;
   if (plan.variant == 1 && slots > qd::kStaticScratchSlots)
     return fail(QD_EINVAL,
@@ -712,12 +746,8 @@ int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, cons
   p.k = k_layer;
   p.v = v_layer;
   p.out = out;
-  p.part_o = nullptr;
-  p.part_ml = nullptr;
-  if (plan.variant == 1) {
-    const int rc = qd::static_scratch(&p.part_o, &p.part_ml);
-    if (rc != QD_OK) return rc;
-  }
+  p.part_o = scratch_o;
+  p.part_ml = scratch_ml;
   p.row_stride = kv_row_stride;
   p.head_stride = kv_head_stride;
   p.seqlen = seqlen;

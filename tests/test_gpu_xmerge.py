@@ -6,7 +6,8 @@ Its outputs must equal the two-launch path's bit for bit (and so the
 kernel-order oracle's), also on the path where the merging workgroup scans
 again the splits whose partials it cannot see (forced here through the test
 hook qd_ctx_set_recompute_mask), and across calls of changing length on one
-context (arrival counters reset by each call's mergers, per-call tags).
+context (per-call tags; the arrival counters are never reset: each call's
+host side passes the value they hold when it starts).
 """
 import numpy as np
 import pytest
@@ -163,8 +164,9 @@ def test_explicit_split_counts(qdiy):
 
 
 def test_stage_hook_with_in_kernel_merge(qdiy):
-    """With the merge in the kernel, the scan stage is the whole call and the merge
-    stage launches nothing."""
+    """With the merge in the kernel, the scan stage is the whole call, and a merge-only
+    call is refused (QD_EINVAL, nothing launched, out untouched): there is no merge
+    kernel to run alone.  The same holds for a fused plan."""
     import ctypes
 
     H, L = 16, 3000
@@ -181,13 +183,22 @@ def test_stage_hook_with_in_kernel_merge(qdiy):
                                                ctypes.c_void_p(vc.data_ptr()),
                                                ctypes.c_void_p(out.data_ptr()), L, H, 128, stages,
                                                ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-            assert rc == 0
+            assert rc == (0 if expect is not None else qdiy.QD_EINVAL)
+            if expect is None:
+                assert b"no merge kernel" in lib.qd_last_error()
             torch.cuda.synchronize()
             o = out.cpu().numpy().reshape(H, 128)
             if expect is None:
                 assert np.all(o == np.float16(7.0))
             else:
                 _same(o, expect, "scan stage")
+        # a fused plan (100 rows) has no merge kernel either
+        rc = lib.qd_decode_attention_stage(ctx._h, ctypes.c_void_p(q.data_ptr()),
+                                           ctypes.c_void_p(kc.data_ptr()),
+                                           ctypes.c_void_p(vc.data_ptr()),
+                                           ctypes.c_void_p(out.data_ptr()), 100, H, 128, 2,
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == qdiy.QD_EINVAL
 
 
 @pytest.mark.parametrize("L", [300, 768, 1280, 3000, 8192, 20000])

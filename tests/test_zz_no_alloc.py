@@ -79,18 +79,23 @@ def _run_pair(qdiy, ctx, case, L):
 @pytest.mark.gpu
 def test_noalloc_equals_context_entry_point_on_calls_in_a_row(qdiy):
     torch.cuda.set_device(0)
-    # (L, heads, layout, seed): each call smaller than the one before it
-    # (8192 -> 2000 -> 300 -> 100 rows); 8 heads at 2000 rows plan two split
-    # workgroups per CU (512 partial slots), 16 heads at 300 rows 15 splits
-    # (240 slots), 100 rows the fused plan, which uses no scratch.
+    # (L, heads, layout, seed): each call smaller than the one before it.  On a
+    # 256-CU MI355X: 8192 rows plan 16 splits per head (256 partial slots); 8 heads
+    # at 2000 rows 32 splits (256 slots); 16 heads at 300 rows 15 splits (240
+    # slots); 129-224 rows are where a default context (round-robin dispatch, 16
+    # heads a multiple of its period, so the merge runs in the scan kernel) runs
+    # split plans although a context that never merges in the kernel would run
+    # them fused; 100 rows is fused either way and uses no scratch.
     calls = [(8192, 16, "engine", 1), (2000, 8, "head_major", 2), (300, 16, "engine", 3),
-             (100, 16, "engine", 4)]
+             (224, 16, "engine", 5), (200, 16, "engine", 6), (160, 16, "head_major", 7),
+             (129, 16, "engine", 8), (100, 16, "engine", 4)]
     for L, H, layout, seed in calls:
         case = AttnCase(L, H=H, seed=seed, kscale=0.5, layout=layout)
         with qdiy.Context(num_heads=H, max_seqlen=case.max_seqlen, kv_row_stride=case.row_stride,
                           kv_head_stride=case.head_stride) as ctx:
             want, got = _run_pair(qdiy, ctx, case, L)
             plan = ctx.plan_detail(L)
+        print(f"noalloc L={L} H={H} {layout}: plan {plan.as_tuple()}", flush=True)
         same = want.view(np.uint16) == got.view(np.uint16)
         assert same.all(), (f"L={L} H={H}: {np.count_nonzero(~same)} outputs differ from "
                             f"qd_decode_attention under {plan.as_tuple()}")
@@ -100,6 +105,24 @@ def test_noalloc_equals_context_entry_point_on_calls_in_a_row(qdiy):
             if ref is not None:
                 err = float(np.max(np.abs(got.astype(np.float32) - ref.astype(np.float32))))
                 assert err <= ATOL, f"L={L}: max abs err {err} vs the reference-order oracle"
+
+
+@pytest.mark.gpu
+def test_noalloc_fills_the_top_of_its_static_scratch(qdiy):
+    """Head counts above the CU count plan one split per head: 1000 heads at 300 rows
+    use 1000 of the 1024 static partial slots, then 520 heads at 260 rows 520 of them
+    (the second call finds the first's partials in the shared scratch).  Bit for bit
+    against qd_decode_attention with a context."""
+    torch.cuda.set_device(0)
+    for L, H, seed in ((300, 1000, 11), (260, 520, 12)):
+        case = AttnCase(L, H=H, seed=seed, kscale=0.5)
+        with qdiy.Context(num_heads=H, max_seqlen=L) as ctx:
+            want, got = _run_pair(qdiy, ctx, case, L)
+            plan = ctx.plan_detail(L)
+        print(f"noalloc L={L} H={H}: plan {plan.as_tuple()}", flush=True)
+        assert plan.variant == qdiy.SPLIT and plan.num_splits == 1
+        same = want.view(np.uint16) == got.view(np.uint16)
+        assert same.all(), f"L={L} H={H}: {np.count_nonzero(~same)} outputs differ"
 
 
 @pytest.mark.gpu
