@@ -182,6 +182,12 @@ typedef struct qd_attn_plan {
                          merge kernel follows (two launches); same bits */
   int loads_per_round;/* tiles whose loads a wave issues before consuming them
                          in order (1 or 2; same bits) */
+  int block_rows;     /* split plans: 0 if split c scans the contiguous rows
+                         [c * rows_per_split, ...); else the rows form blocks
+                         of block_rows (waves * 4 * rows_per_tile) dealt to the
+                         splits in turn, split c scanning blocks c,
+                         c + num_splits, ... (rows_per_split is then split 0's
+                         row count, the largest) */
 } qd_attn_plan;
 
 /* Plan of the call selected by `entry` (0: qd_decode_attention,

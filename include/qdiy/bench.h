@@ -55,6 +55,15 @@ int qd_ctx_set_recompute_mask(qd_ctx* ctx, unsigned mask);
  * bits); 0 (the default) lets the planner choose.  For sweeps and tests. */
 int qd_ctx_set_scan_depth(qd_ctx* ctx, int depth);
 
+/* Shape of the context's split plans, for A/B timing and tests: `waves`
+ * waves per workgroup, `rows_per_tile` rows per 16-lane group per tile, and,
+ * with interleave 1, the rows dealt to the splits in blocks of waves * 4 *
+ * rows_per_tile (qd_attn_plan.block_rows).  Supported: (8, 2, 1), (8, 4, 1),
+ * (4, 4, 1); (0, 0, 0) restores the planner's shape.  Each shape has its own
+ * summation order, so its bits differ from the default plan's; the plan of
+ * every call is reported by qd_decode_attention_plan_detail. */
+int qd_ctx_set_split_shape(qd_ctx* ctx, int waves, int rows_per_tile, int interleave);
+
 /* Turns counting of in-kernel merges and their slot reads on (nonzero) or
  * off (the default: the counts are atomics issued after the output, and a
  * kernel ends only when they have completed, so they lengthen a call). */

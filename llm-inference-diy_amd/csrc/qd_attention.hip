@@ -140,20 +140,32 @@ struct KvTile {
 // base + 32-bit lane offset).  KV rows are read once, so the loads carry the
 // non-temporal hint: streamed lines do not displace L2 contents (measured ~15%
 // faster per call at L=32768).
-template <int U>
+// Layer row of a split's row j: j itself for a contiguous range (the range's
+// first row is in the base), or, for interleaved blocks of kBlock rows (a power
+// of two), row ((j / kBlock) * splits + c) * kBlock + j % kBlock.
+template <int kBlock>
+__device__ __forceinline__ unsigned split_row(int j, int c, int splits) {
+  if constexpr (kBlock == 0) {
+    return (unsigned)j;
+  } else {
+    static_assert((kBlock & (kBlock - 1)) == 0, "interleaved blocks of a power-of-two row count");
+    return (unsigned)(((j / kBlock) * splits + c) * kBlock + (j & (kBlock - 1)));
+  }
+}
+
+template <int U, int kBlock = 0>
 __device__ __forceinline__ void load_tile(KvTile<U>& tl, const char* __restrict__ kbase,
                                           const char* __restrict__ vbase, unsigned row_bytes,
-                                          int blk, int nrows, int g, int t) {
+                                          int blk, int nrows, int g, int t, int c = 0, int splits = 1) {
+  unsigned r[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const unsigned r = (unsigned)min(blk + 4 * u + g, nrows - 1);
-    tl.k[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kbase + (r * row_bytes + t * 16u)));
-  }
+  for (int u = 0; u < U; ++u) r[u] = split_row<kBlock>(min(blk + 4 * u + g, nrows - 1), c, splits);
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const unsigned r = (unsigned)min(blk + 4 * u + g, nrows - 1);
-    tl.v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vbase + (r * row_bytes + t * 16u)));
-  }
+  for (int u = 0; u < U; ++u)
+    tl.k[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kbase + (r[u] * row_bytes + t * 16u)));
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    tl.v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vbase + (r[u] * row_bytes + t * 16u)));
 }
 
 // Online-softmax update of a group with one tile: scores s_u (rows >= nrows
@@ -218,17 +230,19 @@ __device__ __forceinline__ void consume_tile(GroupState& st, const KvTile<U>& tl
 // for, not the arithmetic.  (Prefetching tile i+1 while consuming tile i was
 // measured: it was slower at L = 8192-32768, where the launch already streams
 // at the box's read ceiling, by 4-8%.)
-template <int NW, int U, int D = 1>
+template <int NW, int U, int D = 1, bool kInter = false>
 __device__ __forceinline__ void scan_rows(GroupState& st, const char* __restrict__ kbase,
                                           const char* __restrict__ vbase, unsigned row_bytes,
                                           int nrows, int wave, int g, int t, const f16x8 qv,
-                                          float scale_log2) {
+                                          float scale_log2, int c = 0, int splits = 1) {
   constexpr int kStep = NW * 4 * U;   // rows from one of a wave's tiles to its next
+  constexpr int kBlock = kInter ? kStep : 0;
   for (int blk = wave * 4 * U; blk < nrows; blk += kStep * D) {
     KvTile<U> tl[D];
 #pragma unroll
     for (int d = 0; d < D; ++d)
-      if (d == 0 || blk + d * kStep < nrows) load_tile<U>(tl[d], kbase, vbase, row_bytes, blk + d * kStep, nrows, g, t);
+      if (d == 0 || blk + d * kStep < nrows)
+        load_tile<U, kBlock>(tl[d], kbase, vbase, row_bytes, blk + d * kStep, nrows, g, t, c, splits);
     // keep the scheduler from sinking loads next to their uses
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -287,10 +301,10 @@ struct ScanLds {
 // states in LDS, max-first: for tid < 128, (M, L, O) is the workgroup's
 // partial for dim tid (M and L the same in every thread).  Ends with the LDS
 // reads of the fold; a caller that reuses `lds` synchronises first.
-template <int NW, int U, int D = 1>
+template <int NW, int U, int D = 1, bool kInter = false>
 __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q, int h, int r0,
                                           int nrows, ScanLds<NW>& lds, float& M, float& L,
-                                          float& O) {
+                                          float& O, int c = 0) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
@@ -300,9 +314,9 @@ __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q
   const long long off = h * p.head_stride + (long long)r0 * p.row_stride;
   GroupState st;
   init_state(st);
-  scan_rows<NW, U, D>(st, reinterpret_cast<const char*>(p.k + off),
-                   reinterpret_cast<const char*>(p.v + off), (unsigned)(p.row_stride * 2), nrows,
-                   wave, g, t, qv, p.scale_log2);
+  scan_rows<NW, U, D, kInter>(st, reinterpret_cast<const char*>(p.k + off),
+                              reinterpret_cast<const char*>(p.v + off), (unsigned)(p.row_stride * 2),
+                              nrows, wave, g, t, qv, p.scale_log2, c, p.splits);
   wave_merge(st);
   if (lane < 16) {
     *reinterpret_cast<f32x4*>(&lds.so[wave][t * 8]) = f32x4{st.o[0], st.o[1], st.o[2], st.o[3]};
@@ -329,8 +343,9 @@ __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q
   }
 }
 
-template <int NW, int U, bool kSplit, bool kBatch = false, int D = 1>
+template <int NW, int U, bool kSplit, bool kBatch = false, int D = 1, bool kInter = false>
 __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnParams p) {
+  static_assert(!(kBatch && kInter), "batched queries plan contiguous splits");
   __shared__ ScanLds<NW> lds;
   const int tid = threadIdx.x;
   const int h = blockIdx.x % p.num_heads;
@@ -343,10 +358,11 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
     auto_split(seqlen, p.num_cus, p.num_heads, &splits, &rows_per_split);
     if (c >= splits) return;                  // workgroup-uniform: this query has fewer splits
   }
-  const int r0 = c * rows_per_split;
-  const int nrows = min(seqlen - r0, rows_per_split);
+  const int r0 = kInter ? 0 : c * rows_per_split;
+  const int nrows = kInter ? interleaved_rows(seqlen, NW * 4 * U, splits, c)
+                           : min(seqlen - r0, rows_per_split);
   float M, L, O;
-  scan_fold<NW, U, D>(p, p.q + b * p.q_batch_stride, h, r0, nrows, lds, M, L, O);
+  scan_fold<NW, U, D, kInter>(p, p.q + b * p.q_batch_stride, h, r0, nrows, lds, M, L, O, c);
   if (tid < kD) {
     if constexpr (kSplit) {
       const long long slot = kBatch ? ((long long)b * p.num_heads + h) * p.split_stride + c
@@ -709,11 +725,11 @@ __device__ __forceinline__ unsigned long long merge_wave(const AttnParams& p, co
 }
 
 // SMAX: a bound on p.splits (16, 32 or 64): the slots each merging wave reads.
-template <int U, int SMAX, int D = 1>
-__global__ __launch_bounds__(kMergeThreads) void decode_attention_xmerge_kernel(AttnParams p) {
+// NW scanning waves (4 or 8); kInter: interleaved blocks of NW * 4 * U rows.
+template <int U, int SMAX, int D = 1, int NW = 4, bool kInter = false>
+__global__ __launch_bounds__(NW * 64) void decode_attention_xmerge_kernel(AttnParams p) {
   static_assert(SMAX % 4 == 0 && SMAX <= kXMaxSplits, "SMAX: a multiple of 4, at most the slot count");
-  constexpr int NW = kMergeThreads / 64;
-  static_assert(NW == 4, "four waves scan; waves 0 and 1 hold the 128 dims");
+  static_assert(NW == 4 || NW == 8, "four or eight waves scan; waves 0 and 1 hold the 128 dims");
   __shared__ ScanLds<NW> slds;
   __shared__ unsigned long long s_need[2];   // splits to scan again, per merging wave
   const int tid = threadIdx.x;
@@ -727,9 +743,13 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_xmerge_kernel(
   float2* head_slots = p.xpart + (long long)h * kXMaxSplits * kXSlotWords;
   const char* head = reinterpret_cast<const char*>(head_slots);
 
-  const int r0 = c * p.rows_per_split;
+  constexpr int kBlock = NW * 4 * U;
+  const int r0 = kInter ? 0 : c * p.rows_per_split;
   float M, L, O;   // valid in threads tid < kD
-  scan_fold<NW, U, D>(p, p.q, h, r0, min(p.seqlen - r0, p.rows_per_split), slds, M, L, O);
+  scan_fold<NW, U, D, kInter>(p, p.q, h, r0,
+                              kInter ? interleaved_rows(p.seqlen, kBlock, splits, c)
+                                     : min(p.seqlen - r0, p.rows_per_split),
+                              slds, M, L, O, c);
   if (c != merger) {
     // This split's partial, published as tagged words.
     float2* slot = head_slots + (long long)c * kXSlotWords;
@@ -744,7 +764,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_xmerge_kernel(
     return;
   }
 
-  // The merger.  Waves 2 and 3 wait at the barrier below; they take part only
+  // The merger.  Waves 2 and up wait at the barrier below; they take part only
   // in scanning splits again.
   unsigned long long force = 0ull;   // test hook: splits treated as never visible
   if (p.recompute_mask)
@@ -768,9 +788,12 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_xmerge_kernel(
     rescanned += (unsigned)__builtin_popcountll(all);
     for (int cc = 0; cc < merger; ++cc) {
       if (!((all >> cc) & 1ull)) continue;
-      const int rr = cc * p.rows_per_split;
+      const int rr = kInter ? 0 : cc * p.rows_per_split;
       float Mc, Lc, Oc;
-      scan_fold<NW, U, D>(p, p.q, h, rr, min(p.seqlen - rr, p.rows_per_split), slds, Mc, Lc, Oc);
+      scan_fold<NW, U, D, kInter>(p, p.q, h, rr,
+                                  kInter ? interleaved_rows(p.seqlen, kBlock, splits, cc)
+                                         : min(p.seqlen - rr, p.rows_per_split),
+                                  slds, Mc, Lc, Oc, cc);
       float2* slot = head_slots + (long long)cc * kXSlotWords;
       if (tid < kD) slot[tid] = float2{Oc, tagf};
       if (tid == 0) *reinterpret_cast<f32x4*>(slot + kD) = f32x4{Mc, tagf, Lc, tagf};
@@ -861,14 +884,39 @@ static void launch_xmerge_d(const AttnParams& p, int rows_per_tile, dim3 grid, h
     hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, SMAX, D>), grid, dim3(kMergeThreads), 0, stream, p);
 }
 
+// Interleaved-block split plans merged in the kernel: NW waves, U rows per tile.
 template <int SMAX>
-static void launch_xmerge(const AttnParams& p, int rows_per_tile, int depth, dim3 grid, hipStream_t stream) {
-  if (depth == 4)
-    launch_xmerge_d<SMAX, 4>(p, rows_per_tile, grid, stream);
-  else if (depth == 2)
-    launch_xmerge_d<SMAX, 2>(p, rows_per_tile, grid, stream);
+static void launch_xmerge_inter(const AttnParams& p, int waves, int rows_per_tile, dim3 grid,
+                                hipStream_t stream) {
+  if (waves == 8 && rows_per_tile == 2)
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, SMAX, 1, 8, true>), grid, dim3(512), 0, stream, p);
+  else if (waves == 8)
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, 1, 8, true>), grid, dim3(512), 0, stream, p);
   else
-    launch_xmerge_d<SMAX, 1>(p, rows_per_tile, grid, stream);
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, 1, 4, true>), grid, dim3(256), 0, stream, p);
+}
+
+template <int SMAX>
+static void launch_xmerge(const AttnParams& p, const AttnPlan& plan, dim3 grid, hipStream_t stream) {
+  if (plan.block_rows)
+    launch_xmerge_inter<SMAX>(p, plan.waves, plan.rows_per_tile, grid, stream);
+  else if (plan.depth == 4)
+    launch_xmerge_d<SMAX, 4>(p, plan.rows_per_tile, grid, stream);
+  else if (plan.depth == 2)
+    launch_xmerge_d<SMAX, 2>(p, plan.rows_per_tile, grid, stream);
+  else
+    launch_xmerge_d<SMAX, 1>(p, plan.rows_per_tile, grid, stream);
+}
+
+// Scan-only launch of an interleaved-block split plan.
+static void launch_scan_inter(const AttnParams& p, int waves, int rows_per_tile, dim3 grid,
+                              hipStream_t stream) {
+  if (waves == 8 && rows_per_tile == 2)
+    hipLaunchKernelGGL((decode_attention_scan_kernel<8, 2, true, false, 1, true>), grid, dim3(512), 0, stream, p);
+  else if (waves == 8)
+    hipLaunchKernelGGL((decode_attention_scan_kernel<8, 4, true, false, 1, true>), grid, dim3(512), 0, stream, p);
+  else
+    hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, false, 1, true>), grid, dim3(256), 0, stream, p);
 }
 
 hipError_t launch_decode_attention_fused_batch(const AttnParams& p, int tokens, hipStream_t stream) {
@@ -897,20 +945,30 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
     if (stages & kStageScan) launch_scan<16, false>(p, plan.rows_per_tile, 1, dim3(p.num_heads), stream);
     return hipGetLastError();
   }
+  if (plan.block_rows && (plan.block_rows != plan.waves * 4 * plan.rows_per_tile ||
+                          p.block_rows != plan.block_rows ||
+                          !((plan.waves == 8 && (plan.rows_per_tile == 2 || plan.rows_per_tile == 4)) ||
+                            (plan.waves == 4 && plan.rows_per_tile == 4))))
+    return hipErrorInvalidValue;
   if (plan.xmerge) {
-    if (plan.waves != 4 || p.splits > kXMaxSplits || !p.xpart || !p.xcnt) return hipErrorInvalidValue;
+    if ((plan.waves != 4 && !plan.block_rows) || p.splits > kXMaxSplits || !p.xpart || !p.xcnt)
+      return hipErrorInvalidValue;
     if (stages & kStageScan) {
       const dim3 grid(p.num_heads * p.splits);
       if (p.splits <= 16)
-        launch_xmerge<16>(p, plan.rows_per_tile, plan.depth, grid, stream);
+        launch_xmerge<16>(p, plan, grid, stream);
       else if (p.splits <= 32)
-        launch_xmerge<32>(p, plan.rows_per_tile, plan.depth, grid, stream);
+        launch_xmerge<32>(p, plan, grid, stream);
       else
-        launch_xmerge<64>(p, plan.rows_per_tile, plan.depth, grid, stream);
+        launch_xmerge<64>(p, plan, grid, stream);
     }
     return hipGetLastError();
   }
-  if (stages & kStageScan) {
+  if ((stages & kStageScan) && plan.block_rows) {
+    launch_scan_inter(p, plan.waves, plan.rows_per_tile, dim3(p.num_heads * p.splits), stream);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  } else if (stages & kStageScan) {
     const dim3 grid(p.num_heads * p.splits);
     switch (plan.waves) {
       case 16: launch_scan<16, true>(p, plan.rows_per_tile, 1, grid, stream); break;

@@ -68,6 +68,7 @@ qd::AttnPlan plan_fused(int seqlen) {
   plan.waves = 16;
   plan.xmerge = 0;
   plan.depth = 1;
+  plan.block_rows = 0;
   return plan;
 }
 
@@ -89,11 +90,33 @@ qd::AttnPlan plan_split(int num_cus, int num_heads, int seqlen, int requested) {
   plan.rows_per_tile = rows >= 64 ? 4 : 2;
   plan.xmerge = 0;
   plan.depth = 1;
+  plan.block_rows = 0;
+  return plan;
+}
+
+// A split plan recast with `waves` waves of `rows_per_tile`-row tiles per
+// workgroup, and, when `interleave`, its rows dealt to the splits in blocks of
+// one load round (waves * 4 * rows_per_tile rows): same split count, at most
+// one split per block.
+qd::AttnPlan reshape_split(const qd::AttnPlan& in, int seqlen, int waves, int rows_per_tile,
+                           int interleave) {
+  qd::AttnPlan plan = in;
+  if (plan.variant != 1) return plan;
+  plan.waves = waves;
+  plan.rows_per_tile = rows_per_tile;
+  if (interleave) {
+    const int block = waves * 4 * rows_per_tile;
+    plan.block_rows = block;
+    plan.splits = std::max(1, std::min(plan.splits, (seqlen + block - 1) / block));
+    plan.rows_per_split = qd::interleaved_rows(seqlen, block, plan.splits, 0);   // split 0's, the most
+  }
   return plan;
 }
 
 qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
-  return plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, requested);
+  const qd::AttnPlan plan = plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, requested);
+  return ctx->shape_waves ? reshape_split(plan, seqlen, ctx->shape_waves, ctx->shape_tile, ctx->shape_inter)
+                          : plan;
 }
 
 // The automatic plan: fused up to fused_max rows, else the automatic split.
@@ -150,7 +173,7 @@ int fused_max_rows(const qd_ctx* ctx) {
 }
 
 qd::AttnPlan plan_auto(const qd_ctx* ctx, int seqlen) {
-  return plan_auto(ctx->num_cus, ctx->cfg.num_heads, seqlen, fused_max_rows(ctx));
+  return seqlen <= fused_max_rows(ctx) ? plan_fused(seqlen) : plan_split(ctx, seqlen, 0);
 }
 
 
@@ -206,6 +229,7 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.tag = 0u;
   p.recompute_mask = ctx->recompute_mask;
   p.count_merges = ctx->count_merges;
+  p.block_rows = plan.block_rows;
   return p;
 }
 
@@ -219,7 +243,7 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
 bool use_xmerge(const qd_ctx* ctx, const qd::AttnPlan& plan, int seqlen) {
   return plan.variant == 1 && xmerge_available(ctx) &&
          (seqlen <= kXMergeMaxRows || ctx->merge_mode == QD_MERGE_IN_KERNEL) &&
-         plan.waves == 4 && plan.splits <= qd::kXMaxSplits &&
+         (plan.waves == 4 || plan.block_rows) && plan.splits <= qd::kXMaxSplits &&
          (long long)plan.splits * ctx->cfg.num_heads <= ctx->num_cus;
 }
 
@@ -233,7 +257,7 @@ bool use_xmerge(const qd_ctx* ctx, const qd::AttnPlan& plan, int seqlen) {
 qd::AttnPlan finish_plan(const qd_ctx* ctx, const qd::AttnPlan& plan_in, int seqlen) {
   qd::AttnPlan plan = plan_in;
   plan.xmerge = use_xmerge(ctx, plan, seqlen) ? 1 : 0;
-  if (plan.variant == 1 && plan.waves == 4) {
+  if (plan.variant == 1 && plan.waves == 4 && !plan.block_rows) {
     const int tiles = (plan.rows_per_split + 16 * plan.rows_per_tile - 1) / (16 * plan.rows_per_tile);
     plan.depth = ctx->scan_depth ? ctx->scan_depth : (plan.xmerge && tiles >= 2 ? 2 : 1);
   } else {
@@ -278,6 +302,9 @@ int attention_prefill(qd_ctx* ctx, const uint16_t* q, long long q_stride, const 
   if (tokens < 1) return QD_OK;
   int rc = check_attention_args(ctx, q, k, v, out, pos0 + 1, ctx ? ctx->cfg.num_heads : 0, QD_HEAD_DIM);
   if (rc != QD_OK) return rc;
+  if (ctx->shape_waves)
+    return fail(QD_EINVAL, "the context's split shape is forced (qd_ctx_set_split_shape): batched "
+                           "queries plan the automatic shape, so they would not give its bits");
   if (pos0 + tokens > ctx->cfg.max_seqlen)
     return fail(QD_EINVAL, "positions up to %d exceed max_seqlen %d", pos0 + tokens, ctx->cfg.max_seqlen);
   // queries whose length plan_auto makes fused: one launch for all of them
@@ -452,6 +479,7 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   ctx->recompute_mask = 0u;
   ctx->count_merges = 0;
   ctx->scan_depth = 0;
+  ctx->shape_waves = ctx->shape_tile = ctx->shape_inter = 0;
   *out_ctx = ctx;
   return QD_OK;
 }
@@ -584,6 +612,21 @@ int qd_decode_attention_plan_detail(const qd_ctx* ctx, int seqlen, int entry, in
   plan->waves = p.waves;
   plan->merge_in_kernel = p.xmerge;
   plan->loads_per_round = p.depth;
+  plan->block_rows = p.block_rows;
+  return QD_OK;
+}
+
+int qd_ctx_set_split_shape(qd_ctx* ctx, int waves, int rows_per_tile, int interleave) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  const bool off = waves == 0 && rows_per_tile == 0 && interleave == 0;
+  const bool ok = (waves == 8 && (rows_per_tile == 2 || rows_per_tile == 4) && interleave == 1) ||
+                  (waves == 4 && rows_per_tile == 4 && interleave == 1);
+  if (!off && !ok)
+    return fail(QD_EINVAL, "split shape (%d waves, %d rows per tile, interleave %d) unsupported",
+                waves, rows_per_tile, interleave);
+  ctx->shape_waves = waves;
+  ctx->shape_tile = rows_per_tile;
+  ctx->shape_inter = interleave;
   return QD_OK;
 }
 
@@ -765,6 +808,7 @@ int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, cons
   p.tag = 0u;
   p.recompute_mask = 0u;
   p.count_merges = 0;
+  p.block_rows = plan.block_rows;
   e = qd::launch_decode_attention(p, plan, stream);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return QD_OK;

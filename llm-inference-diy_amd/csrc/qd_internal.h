@@ -74,6 +74,11 @@ struct AttnParams {
   // split_stride + c.
   int num_cus;
   int split_stride;
+  // Split plans with interleaved blocks (0 for contiguous ranges): the rows
+  // form blocks of block_rows (one load round of a workgroup), dealt to the
+  // splits in turn -- split c scans blocks c, c + splits, ... (see
+  // interleaved_rows) -- so that at any time the grid reads one run of rows.
+  int block_rows;
   // In-kernel merge (decode_attention_xmerge_kernel) only: tagged slots
   // [H][kXMaxSplits][kXSlotWords] (value, tag) words, per-head arrival
   // counters (kXCounterStride apart; every head's counter holds cnt_base when
@@ -222,12 +227,23 @@ struct FlashPrefillParams {
 struct AttnPlan {
   int variant;            // 0 fused, 1 split
   int splits;             // workgroups per head
-  int rows_per_split;     // rows each workgroup scans
+  int rows_per_split;     // rows each workgroup scans (the longest split's when interleaved)
   int rows_per_tile;      // rows per group per tile (template U)
   int waves;              // waves per split workgroup (4, 8 or 16)
   int xmerge;             // split plans: merge inside the scan kernel (one launch)
   int depth;              // 4-wave split plans: tiles per load round (1, 2 or 4; same bits)
+  int block_rows;         // split plans: interleaved blocks of this many rows, 0 contiguous
 };
+
+// Rows of split c when the rows [0, seqlen) form blocks of block_rows dealt to
+// `splits` splits in turn (split c takes blocks c, c + splits, ...; the last
+// block may be short).  Its j-th row is row ((j / block_rows) * splits + c) *
+// block_rows + j % block_rows of the layer.
+__host__ __device__ inline int interleaved_rows(int seqlen, int block_rows, int splits, int c) {
+  const int full = seqlen / block_rows, rem = seqlen % block_rows;
+  const int nfull = full > c ? (full - 1 - c) / splits + 1 : 0;
+  return nfull * block_rows + (rem > 0 && full % splits == c ? rem : 0);
+}
 
 // Error reporting of the C ABI: records a printf-style message for
 // qd_last_error() on this host thread and returns `code`.
@@ -379,4 +395,8 @@ struct qd_ctx {
   unsigned recompute_mask;
   int count_merges;
   int scan_depth;         // 0: the planner's tiles per load round; else forced for split plans
+  // Split-plan shape forced by qd_ctx_set_split_shape (0: the planner's).
+  int shape_waves;
+  int shape_tile;
+  int shape_inter;
 };

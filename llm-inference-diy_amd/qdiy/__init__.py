@@ -33,6 +33,7 @@ EXPORTS = (
     # qdiy/bench.h
     "qd_decode_attention_stage", "qd_ctx_set_merge", "qd_ctx_set_recompute_mask",
     "qd_ctx_xcd_period", "qd_xcd_placement", "qd_ctx_xmerge_stats", "qd_ctx_count_xmerges", "qd_ctx_set_scan_depth",
+    "qd_ctx_set_split_shape",
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
@@ -79,12 +80,13 @@ class AttnPlan(ctypes.Structure):
     _fields_ = [("variant", ctypes.c_int), ("num_splits", ctypes.c_int),
                 ("rows_per_split", ctypes.c_int), ("rows_per_tile", ctypes.c_int),
                 ("waves", ctypes.c_int), ("merge_in_kernel", ctypes.c_int),
-                ("loads_per_round", ctypes.c_int)]
+                ("loads_per_round", ctypes.c_int), ("block_rows", ctypes.c_int)]
 
     def as_tuple(self):
         """The plan fields that fix the output bits (merge_in_kernel and
-        loads_per_round do not)."""
-        return (self.variant, self.num_splits, self.rows_per_split, self.rows_per_tile, self.waves)
+        loads_per_round do not), in oracle.Plan's field order."""
+        return (self.variant, self.num_splits, self.rows_per_split, self.rows_per_tile, self.waves,
+                self.block_rows)
 
 
 _lib = None
@@ -116,6 +118,7 @@ def load() -> ctypes.CDLL:
     L.qd_ctx_xmerge_stats.argtypes = [vp, ull_p, ull_p, ull_p]
     L.qd_ctx_count_xmerges.argtypes = [vp, i]
     L.qd_ctx_set_scan_depth.argtypes = [vp, i]
+    L.qd_ctx_set_split_shape.argtypes = [vp, i, i, i]
     L.qd_xcd_placement.argtypes = [ctypes.POINTER(ctypes.c_uint), i]
     L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
     L.qd_decode_attention_plan_detail.argtypes = [vp, i, i, i, ctypes.POINTER(AttnPlan)]
@@ -228,6 +231,11 @@ class Context:
     def set_scan_depth(self, depth: int) -> None:
         """qd_ctx_set_scan_depth: tiles per load round of split plans (0: planner's)."""
         _check(load().qd_ctx_set_scan_depth(self._h, depth))
+
+    def set_split_shape(self, waves: int, rows_per_tile: int, interleave: int) -> None:
+        """qd_ctx_set_split_shape: waves, rows per tile and interleaved blocks of split
+        plans ((0, 0, 0): the planner's shape)."""
+        _check(load().qd_ctx_set_split_shape(self._h, waves, rows_per_tile, interleave))
 
     def count_xmerges(self, on: bool = True) -> None:
         """qd_ctx_count_xmerges: count merges and slot reads (off by default)."""

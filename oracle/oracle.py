@@ -24,11 +24,12 @@ class Plan(ctypes.Structure):
     """qd_oracle_plan: the launch plan of one decode-attention call."""
     _fields_ = [("variant", ctypes.c_int), ("num_splits", ctypes.c_int),
                 ("rows_per_split", ctypes.c_int), ("rows_per_tile", ctypes.c_int),
-                ("waves", ctypes.c_int)]
+                ("waves", ctypes.c_int), ("block_rows", ctypes.c_int)]
 
     def __repr__(self):
         return (f"Plan(variant={self.variant}, num_splits={self.num_splits}, rows_per_split="
-                f"{self.rows_per_split}, rows_per_tile={self.rows_per_tile}, waves={self.waves})")
+                f"{self.rows_per_split}, rows_per_tile={self.rows_per_tile}, waves={self.waves}, "
+                f"block_rows={self.block_rows})")
 
 
 def build() -> None:
@@ -241,6 +242,18 @@ def split_plan(seqlen, num_splits, rows_per_tile=None, waves=4) -> Plan:
     if rows_per_tile is None:
         rows_per_tile = 4 if rows >= 64 else 2
     return Plan(1, -(-seqlen // rows), rows, rows_per_tile, waves)
+
+
+def interleaved_plan(seqlen, num_splits, rows_per_tile=2, waves=8) -> Plan:
+    """A split plan whose rows form blocks of one load round (waves * 4 *
+    rows_per_tile rows) dealt to the splits in turn; at most one split per
+    block.  rows_per_split is split 0's row count (the largest)."""
+    block = waves * 4 * rows_per_tile
+    splits = max(1, min(num_splits, -(-seqlen // block)))
+    full, rem = divmod(seqlen, block)
+    nfull = (full - 1) // splits + 1 if full > 0 else 0
+    rows0 = nfull * block + (rem if rem > 0 and full % splits == 0 else 0)
+    return Plan(1, splits, rows0, rows_per_tile, waves, block)
 
 
 def attention_planned(q, k, v, seqlen, num_heads, row_stride, head_stride, plan, nthreads=1):

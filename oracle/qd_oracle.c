@@ -579,11 +579,28 @@ static float group_score(const float* qf, const uint16_t* krow) {
 
 static float gfx_scale_log2(void) { return (float)(1.4426950408889634 / sqrt(128.0)); }
 
-/* One workgroup of decode_attention_scan_kernel<NW, U, *>: rows [0, nrows) at
- * k/v + r*row_stride.  Returns the LDS fold (M, L, O[128]). */
+/* Layer row of a split's j-th row (decode_attention_scan_kernel's split_row):
+ * j for a contiguous range (whose first row the k/v base already holds), or,
+ * for blocks of `block` rows dealt to `splits` splits in turn, row
+ * ((j / block) * splits + c) * block + j % block. */
+static long long split_row(int j, int block, int splits, int c) {
+  if (block == 0) return j;
+  return ((long long)(j / block) * splits + c) * block + j % block;
+}
+
+/* Rows of split c of an interleaved plan (qd::interleaved_rows). */
+static int interleaved_rows(int seqlen, int block, int splits, int c) {
+  const int full = seqlen / block, rem = seqlen % block;
+  const int nfull = full > c ? (full - 1 - c) / splits + 1 : 0;
+  return nfull * block + (rem > 0 && full % splits == c ? rem : 0);
+}
+
+/* One workgroup of decode_attention_scan_kernel<NW, U, *>: the split's rows
+ * j in [0, nrows), row j at k/v + split_row(j, block, splits, c)*row_stride.
+ * Returns the LDS fold (M, L, O[128]). */
 static void scan_workgroup(const float* qf, const uint16_t* k, const uint16_t* v,
-                           long long row_stride, int nrows, int nw, int u_rows,
-                           float* M_out, float* L_out, float* O_out) {
+                           long long row_stride, int nrows, int nw, int u_rows, int block,
+                           int splits, int c, float* M_out, float* L_out, float* O_out) {
   const float scale = gfx_scale_log2();
   gstate* st = (gstate*)malloc(sizeof(gstate) * (size_t)nw * 4);
   float* s = (float*)malloc(sizeof(float) * (size_t)u_rows);
@@ -596,7 +613,7 @@ static void scan_workgroup(const float* qf, const uint16_t* k, const uint16_t* v
         for (int u = 0; u < u_rows; ++u) {
           const int row = blk + 4 * u + g;
           rr[u] = row < nrows - 1 ? row : nrows - 1;       /* clamped load row */
-          const float d = group_score(qf, k + (long long)rr[u] * row_stride);
+          const float d = group_score(qf, k + split_row(rr[u], block, splits, c) * row_stride);
           s[u] = row < nrows ? d * scale : -INFINITY;
         }
         float mt = s[0];
@@ -609,7 +626,7 @@ static void scan_workgroup(const float* qf, const uint16_t* k, const uint16_t* v
         for (int u = 0; u < u_rows; ++u) {
           const float p = qd_oracle_exp2(s[u] - base);
           x->l += p;
-          const uint16_t* vrow = v + (long long)rr[u] * row_stride;
+          const uint16_t* vrow = v + split_row(rr[u], block, splits, c) * row_stride;
           for (int d = 0; d < QD_D; ++d) x->o[d] = fmaf(qd_oracle_h2f(vrow[d]), p, x->o[d]);
         }
         x->m = mn;
@@ -689,7 +706,8 @@ static void gfx_head(gfx_job* j, int h) {
   const qd_oracle_plan* pl = &j->plan;
   if (pl->variant == 0) {
     float M, L, O[QD_D];
-    scan_workgroup(qf, kh, vh, j->row_stride, j->seqlen, pl->waves, pl->rows_per_tile, &M, &L, O);
+    scan_workgroup(qf, kh, vh, j->row_stride, j->seqlen, pl->waves, pl->rows_per_tile, 0, 1, 0,
+                   &M, &L, O);
     for (int d = 0; d < QD_D; ++d) oh[d] = qd_oracle_f2h(O[d] / L);
     return;
   }
@@ -698,11 +716,17 @@ static void gfx_head(gfx_job* j, int h) {
   float* pm = (float*)malloc(sizeof(float) * (size_t)S);
   float* plv = (float*)malloc(sizeof(float) * (size_t)S);
   for (int c = 0; c < S; ++c) {
+    if (pl->block_rows) {
+      scan_workgroup(qf, kh, vh, j->row_stride, interleaved_rows(j->seqlen, pl->block_rows, S, c),
+                     pl->waves, pl->rows_per_tile, pl->block_rows, S, c, &pm[c], &plv[c],
+                     po + (long long)c * QD_D);
+      continue;
+    }
     const int r0 = c * pl->rows_per_split;
     int nrows = j->seqlen - r0;
     if (nrows > pl->rows_per_split) nrows = pl->rows_per_split;
     scan_workgroup(qf, kh + (long long)r0 * j->row_stride, vh + (long long)r0 * j->row_stride,
-                   j->row_stride, nrows, pl->waves, pl->rows_per_tile, &pm[c], &plv[c],
+                   j->row_stride, nrows, pl->waves, pl->rows_per_tile, 0, 1, 0, &pm[c], &plv[c],
                    po + (long long)c * QD_D);
   }
   merge_head(po, pm, plv, S, oh);
@@ -726,11 +750,17 @@ int qd_oracle_attention_planned(const uint16_t* q, const uint16_t* k, const uint
                                 long long head_stride, const qd_oracle_plan* plan, int nthreads) {
   if (!q || !k || !v || !out || !plan || seqlen < 1 || num_heads < 1) return -1;
   if (plan->rows_per_tile < 1 || plan->waves < 1) return -1;
-  if (plan->variant != 0) {
+  if (plan->variant != 0 && plan->block_rows) {
+    /* blocks of one load round of the workgroup; every split has a block */
+    if (plan->num_splits < 1 || plan->block_rows != plan->waves * 4 * plan->rows_per_tile) return -1;
+    if ((long long)(plan->num_splits - 1) * plan->block_rows >= seqlen) return -1;
+  } else if (plan->variant != 0) {
     if (plan->num_splits < 1 || plan->rows_per_split < 1) return -1;
     /* every split workgroup has rows, and together they cover [0, seqlen) */
     if ((long long)(plan->num_splits - 1) * plan->rows_per_split >= seqlen) return -1;
     if ((long long)plan->num_splits * plan->rows_per_split < seqlen) return -1;
+  } else if (plan->block_rows) {
+    return -1;
   }
   gfx_job j = {q, k, v, out, seqlen, num_heads, row_stride, head_stride, *plan, 0};
   if (nthreads > num_heads) nthreads = num_heads;

@@ -140,6 +140,10 @@ typedef struct {
   int rows_per_split; /* KV rows per split workgroup */
   int rows_per_tile;  /* rows each 16-lane group takes per tile (template U) */
   int waves;          /* wavefronts per scan workgroup */
+  int block_rows;     /* split plans: 0 for contiguous ranges [c * rows_per_split,
+                         ...); else the rows form blocks of block_rows (waves * 4 *
+                         rows_per_tile) dealt to the splits in turn, split c taking
+                         blocks c, c + num_splits, ... */
 } qd_oracle_plan;
 
 /* decode_attention_scan_kernel (+ decode_attention_merge_kernel for split
@@ -148,7 +152,8 @@ typedef struct {
  * tile-wise online softmax, the lane-shuffle and LDS folds, and the 8-slice
  * merge.  Same argument meaning as qd_oracle_decode_attention.  Returns 0, or
  * -1 on invalid arguments (including a split plan that does not cover
- * [0, seqlen) with non-empty workgroups). */
+ * [0, seqlen) with non-empty workgroups, and interleaved blocks other than
+ * one load round of a workgroup). */
 int qd_oracle_attention_planned(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                 uint16_t* out, int seqlen, int num_heads, long long row_stride,
                                 long long head_stride, const qd_oracle_plan* plan, int nthreads);

@@ -266,14 +266,14 @@ def _planner_rules(L, H, cus, variant="auto", requested=0, period=0):
     split."""
     fused_max = 128 if period >= 1 and H % period == 0 else 224
     if variant == "fused" or (variant == "auto" and L <= fused_max):
-        return (0, 1, L, 4, 16)
+        return (0, 1, L, 4, 16, 0)
     if requested > 0:
         s = min(requested, 256)
     else:
         s = max(1, min(cus // H, (L + 15) // 16, 256))
     rows = -(-L // s)
     rows = (rows + 3) & ~3
-    return (1, -(-L // rows), rows, 4 if rows >= 64 else 2, 4)
+    return (1, -(-L // rows), rows, 4 if rows >= 64 else 2, 4, 0)
 
 
 @pytest.mark.parametrize("H", [1, 4, 12, 16, 24, 40])

@@ -12,7 +12,9 @@ output can; the pins are independent of the restatement):
     within 2e-3 of the reference-order oracle; closed forms (L=1 -> V0,
     constant 0x3C inputs -> 0x3C3C, constant V, identical keys, a dominant
     key); layout and head independence bit-exact; rows beyond seqlen unread;
-  * different plans agree within one binary16 ulp of each other.
+  * different plans agree within one binary16 ulp of each other;
+  * interleaved split plans: bit-equal to a contiguous plan over rows reordered
+    by hand, and to the one-split contiguous plan; ragged lengths covered.
 """
 import numpy as np
 import pytest
@@ -74,6 +76,9 @@ PLANS = {
     "split16": lambda L: oracle.split_plan(L, 16),
     "split64w8": lambda L: oracle.split_plan(L, 64, waves=8),
     "split200w16": lambda L: oracle.split_plan(L, 200, waves=16),
+    "inter16w8x2": lambda L: oracle.interleaved_plan(L, 16),
+    "inter5w8x4": lambda L: oracle.interleaved_plan(L, 5, rows_per_tile=4),
+    "inter16w4x4": lambda L: oracle.interleaved_plan(L, 16, rows_per_tile=4, waves=4),
 }
 
 
@@ -174,6 +179,86 @@ def test_plans_agree_within_rounding():
         assert np.all(np.abs(o - outs[0]) <= ulp16(outs[0]))
 
 
+def _split_rows_by_hand(L, block, splits):
+    """Rows of each split of an interleaved plan, listed from its definition:
+    blocks of `block` rows dealt to the splits in turn."""
+    blocks = [list(range(b, min(b + block, L))) for b in range(0, L, block)]
+    return [[r for i in range(c, len(blocks), splits) for r in blocks[i]] for c in range(splits)]
+
+
+@pytest.mark.parametrize("L,splits,tile,waves", [(1024, 4, 2, 8), (8192, 16, 2, 8), (3072, 6, 4, 8),
+                                                 (2048, 16, 4, 4)])
+def test_interleaved_plan_is_a_contiguous_plan_over_permuted_rows(L, splits, tile, waves):
+    """With equal splits, an interleaved plan over the cache must give the bits of a
+    contiguous plan of the same shape over a cache whose rows are reordered so that
+    each split's rows (listed by hand) lie together.  Attention does not depend on
+    row order up to rounding, so float64 parity cannot see a wrong row mapping; this
+    check can (a mapping off by one block, or ignoring the split index, fails it)."""
+    block = waves * 4 * tile
+    assert L % (splits * block) == 0
+    case = AttnCase(L, H=3, seed=L + splits)
+    # Order-sensitive values: keys 0 (every weight exactly 1, so the outputs are
+    # plain fp32 sums of V), V rows of +-2^15 on a random tenth of the rows (as many
+    # + as -) among small values that a big partial sum absorbs: which small values
+    # survive depends on how the rows are grouped and ordered.
+    rng = np.random.default_rng(L * 7 + splits)
+    big = rng.choice(L, size=(L // 20) * 2, replace=False)
+    vh = (rng.integers(1, 9, size=(3, L, 128)) * 2.0 ** -10).astype(np.float16)
+    vh[:, big[: len(big) // 2]] = np.float16(32768.0)
+    vh[:, big[len(big) // 2:]] = np.float16(-32768.0)
+    case.vc = np.ascontiguousarray(vh.transpose(1, 0, 2)).reshape(-1)
+    case.kc = np.zeros_like(case.kc)
+    order = [r for rows in _split_rows_by_hand(L, block, splits) for r in rows]
+    assert sorted(order) == list(range(L))
+    perm = AttnCase(L, H=3, seed=0)
+    kc = case.kc.reshape(L, 3, 128)
+    vc = case.vc.reshape(L, 3, 128)
+    perm.kc = np.ascontiguousarray(kc[order]).reshape(-1)
+    perm.vc = np.ascontiguousarray(vc[order]).reshape(-1)
+    perm.q = case.q
+    inter = oracle.interleaved_plan(L, splits, rows_per_tile=tile, waves=waves)
+    assert (inter.num_splits, inter.rows_per_split, inter.block_rows) == (splits, L // splits, block)
+    contiguous = oracle.Plan(1, splits, L // splits, tile, waves, 0)
+    a = _run(case, inter)
+    b = _run(perm, contiguous)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    # on these values the row grouping shows in the bits: the contiguous plan over
+    # the original rows, and the interleaved plan over rows grouped one block off,
+    # both differ
+    assert not np.array_equal(a.view(np.uint16), _run(case, contiguous).view(np.uint16))
+    shifted = [r for rows in _split_rows_by_hand(L, block, splits)[1:] + _split_rows_by_hand(L, block, splits)[:1]
+               for r in rows]
+    perm.kc = np.ascontiguousarray(kc[shifted]).reshape(-1)
+    perm.vc = np.ascontiguousarray(vc[shifted]).reshape(-1)
+    assert not np.array_equal(a.view(np.uint16), _run(perm, contiguous).view(np.uint16))
+
+
+def test_interleaved_single_split_is_the_contiguous_plan():
+    """One split takes every block in order: the interleaved plan is then the
+    contiguous one-split plan, bit for bit (ragged last block included)."""
+    case = AttnCase(1000, H=2, seed=71)
+    inter = oracle.interleaved_plan(1000, 1)
+    assert (inter.num_splits, inter.rows_per_split) == (1, 1000)
+    a = _run(case, inter)
+    b = _run(case, oracle.Plan(1, 1, 1000, 2, 8, 0))
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
+@pytest.mark.parametrize("L", [65, 127, 1000, 1100, 8191])
+def test_interleaved_ragged_lengths_cover_every_row(L):
+    """Ragged lengths (a short last block, splits with unequal block counts):
+    float64 parity, and a key spike planted in the short last block is found."""
+    case = AttnCase(L, H=2, seed=L)
+    j = L - 1
+    case.Kh[1, j] = (case.q[1].astype(np.float32) * 4).astype(np.float16)
+    case.kc[:] = np.ascontiguousarray(case.Kh.transpose(1, 0, 2)).reshape(-1)
+    ref = case.fp64()
+    for plan in (oracle.interleaved_plan(L, 16), oracle.interleaved_plan(L, 3, rows_per_tile=4)):
+        out = _run(case, plan).astype(np.float64)
+        assert np.all(np.abs(out - ref) <= 0.5 * ulp16(ref) + 1e-5), plan
+        assert np.all(np.abs(out[1] - case.Vh[1, j].astype(np.float64)) <= ulp16(case.Vh[1, j])), plan
+
+
 def test_planned_threads_and_validation():
     case = AttnCase(2000, H=4, seed=66)
     plan = oracle.split_plan(2000, 32)
@@ -185,3 +270,9 @@ def test_planned_threads_and_validation():
         _run(case, oracle.Plan(1, 10, 64, 4, 4))
     with pytest.raises(ValueError):
         _run(case, oracle.Plan(1, 32, 64, 0, 4))
+    with pytest.raises(ValueError):      # interleaved blocks other than one load round
+        _run(case, oracle.Plan(1, 16, 128, 2, 8, 32))
+    with pytest.raises(ValueError):      # a split without a block
+        _run(case, oracle.Plan(1, 40, 64, 2, 8, 64))
+    with pytest.raises(ValueError):      # a fused plan is not interleaved
+        _run(case, oracle.Plan(0, 1, 2000, 4, 16, 64))
