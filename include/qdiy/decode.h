@@ -90,15 +90,6 @@ int qd_ffn_up_swiglu(const uint16_t* x, const uint16_t* norm_w, float eps, const
 int qd_gemm_nt(const uint16_t* x, long long ldx, const uint16_t* w, const uint16_t* residual,
                uint16_t* y, long long ldy, int m, int n, int k, int mode, hipStream_t stream);
 
-/* Whether QD_GEMM_MFMA products of 128 rows and more (qd_gemm_nt and the
- * engine's MFMA prefill) may run in hipBLASLt (1, the default) or only in this
- * library's own matrix-core tiles (0), process-wide; returns the previous
- * setting.  The results of both meet the QD_GEMM_MFMA bound.  No counterpart
- * in the reference: for tests and diagnostics of the hand-written tiles, which
- * also serve when the vendor library is absent or has no kernel for a shape.
- * Set it between calls, not while products run on other threads. */
-int qd_gemm_vendor_enable(int enable);
-
 /* Batched FFN up-projection of m prompt rows on the matrix cores, gate and up
  * GEMMs in one pass with the SwiGLU in the epilogue:
  *   act[i][j] = half(g * (u / (1 + exp(-u)))),  g = half(x[i] . w1[j]),

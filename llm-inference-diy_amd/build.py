@@ -18,7 +18,7 @@ BENCH_LIB = os.path.join(LIB_DIR, "libqdiy_bench.so")
 ENGINE_EXE = os.path.join(LIB_DIR, "qdiy_engine")
 
 SOURCES = ["qd_capi.cpp", "qd_engine.cpp", "qd_attention.hip", "qd_rope_cache.hip", "qd_decode_ops.hip", "qd_prefill.hip",
-           "qd_flash_prefill.hip", "qd_blaslt.cpp"]
+           "qd_flash_prefill.hip"]
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for all device code: plain float code is
@@ -55,8 +55,7 @@ def build(verbose: bool = False) -> str:
     tmp = LIB + ".tmp"
     _run([hipcc(), f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
           "-Wall", "-Wno-unused-result", *DEVICE_FLAGS, "-I", INCLUDE, "-I", CSRC,
-          "-Wl,-soname,libqdiy.so", "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES],
-          "-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"], verbose)
+          "-Wl,-soname,libqdiy.so", "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]], verbose)
     os.replace(tmp, LIB)
     tmp = BENCH_LIB + ".tmp"
     _run([hipcc(), f"--offload-arch={ARCH}", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",

@@ -276,17 +276,6 @@ int prefill_batched(qd_engine* e, const int* tokens, int T, int pos0) {
     he = gemv(e->p_att, H, e->w(f.proj_w), H, H, e->p_x, H, 1);
     if (he == hipSuccess) he = qd::launch_rmsnorm_batched(e->p_x, e->w(f.ln_2), kEps, e->p_xn, H, T, e->stream);
     bool joint = false;                          // gate/up GEMM with the SwiGLU in its epilogue
-    if (he == hipSuccess && e->prefill_mode == QD_GEMM_MFMA && T >= qd::kBlasltMinRows &&
-        f.w2 == f.w1 + (long long)I * H) {
-      // w1 and w2 lie back to back: one plain product of 2 * inter columns
-      // into [g | u] rows (the vendor library from 128 rows up), then the
-      // elementwise SwiGLU, is faster there than the fused tiles.
-      qd::BatchedGemvParams q{e->p_xn, H, e->w(f.w1), 2 * I, H, T, e->p_g, 2LL * I, nullptr};
-      he = qd::launch_gemm_mfma(q, 0, e->stream);
-      if (he == hipSuccess)
-        he = qd::launch_swiglu_batched(e->p_g, e->p_g + I, e->p_act, T, I, 2LL * I, e->stream);
-      joint = true;
-    }
     if (he == hipSuccess && e->prefill_mode == QD_GEMM_MFMA && !joint) {
       qd::BatchedGemvParams q{e->p_xn, H, e->w(f.w1), I, H, T, e->p_act, I, nullptr};
       q.w2 = e->w(f.w2);

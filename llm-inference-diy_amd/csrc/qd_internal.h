@@ -314,24 +314,18 @@ hipError_t launch_gemv_batched(const BatchedGemvParams& p, int epi, hipStream_t 
 // The same product on the matrix cores (fp32 accumulation in the hardware's
 // order, not bit-reproducible on the host); p.k must be a multiple of 64.
 hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream);
-// qd_blaslt.cpp: the same product (epi 0 or 1) through hipBLASLt;
-// hipErrorNotSupported when the library has no kernel for it (nothing ran).
-// launch_gemm_mfma takes this path from kBlasltMinRows rows up, and the engine
-// then runs gate and up as one product of 2 * inter columns.
-constexpr int kBlasltMinRows = 128;
-hipError_t blaslt_gemm_nt(const BatchedGemvParams& p, int epi, hipStream_t stream);
-// The same, allowed below kBlasltMinRows rows to split K over up to 4
-// workgroups per tile when the tile grid leaves CUs idle: fp32 partial sums in
-// `workspace` (kGemmSplitWsBytes suffice for every shape), then one launch
-// folds them in slice order and applies the epilogue.  Otherwise, and without
-// a workspace, it is launch_gemm_mfma.
-constexpr size_t kGemmSplitWsBytes = (size_t)4 << 20;
+// The same, allowed to split K over up to 8 slices when the tile grid leaves
+// CUs idle: fp32 partial sums in `workspace` (as many slices as it holds),
+// then one launch folds them in slice order and applies the epilogue.
+// Otherwise, and without a workspace, it is launch_gemm_mfma.
+constexpr size_t kGemmSplitWsBytes = (size_t)64 << 20;
 hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* workspace,
                                   size_t workspace_bytes, hipStream_t stream);
 // act[t][i] = half(g * (u / (1 + exp(-u)))) with g = half(X W1^T), u = half(X W2^T)
 // (p.w = W1, p.w2 = W2, p.n = inter, p.y = act) in one matrix-core launch, the
-// SwiGLU applied in the GEMM's epilogue: the 128 x 128 tile from 512 tokens
-// (act 8-byte aligned, ldy a multiple of 4), else the 64 x 64 tile.
+// SwiGLU applied in the GEMM's epilogue: from 128 tokens (act 8-byte aligned,
+// ldy a multiple of 4) the 192 x 256 or 128 x 128 ring tile, else the 64 x 64
+// tile.
 // hipErrorNotSupported (nothing launched) unless k is a multiple of 64: the
 // caller then runs the two projections and launch_swiglu_batched.
 hipError_t launch_gemm_mfma_swiglu(const BatchedGemvParams& p, hipStream_t stream);

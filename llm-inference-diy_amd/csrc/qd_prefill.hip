@@ -736,115 +736,200 @@ __global__ __launch_bounds__(256) void splitk_fold_kernel(BatchedGemvParams p, i
   reinterpret_cast<_Float16*>(p.y)[t * p.ldy + n] = y;
 }
 
-// Large-M form of the same product (M >= 512: the matrix-core prefill's 2048-
-// token passes): a 128 x 128 workgroup tile computed as Y^T = W X^T, so the
-// MFMA's A operand is W's rows and B the tokens' rows, and accumulator lane
+constexpr int kGemmXcds = 8;                 // MI355X: workgroups are dealt to 8 XCDs in turn
+constexpr int kRingMinRows = 128;            // the ring tiles from this many tokens
+constexpr int kGemmMaxSplits = 8;            // K slices of a split product
+
+// Large-M product on a ring of direct-to-LDS stages (M >= 128: the matrix-core
+// prefill's passes): a 128 x 128 workgroup tile computed as Y^T = W X^T, so
+// the MFMA's A operand is W's rows and B the tokens' rows and accumulator lane
 // (g = l / 16, c = l % 16) holds rows 4 g .. 4 g + 3 of W for token c: four
 // adjacent outputs of one token, stored as 8 bytes.  Four waves of 64 x 64
-// (4 x 4 MFMA blocks) per workgroup and K tiles of 64 through LDS, the next
-// tile's loads in flight in registers; per 32 of K a wave reads 8 fragments
-// for 16 MFMAs (a 64 x 64 tile does twice the work of a 32 x 32 one per byte
-// of LDS, and a 128 x 128 workgroup twice the work of a 64 x 64 one per byte
-// of L2).  The grid is one-dimensional and its index is remapped so that,
-// with workgroups dealt to the 8 XCDs in turn, XCD x computes a contiguous
-// eighth of W's row tiles for all tokens and its L2 holds only that eighth of
-// W.  Requires y and res 8-byte aligned and ldy a multiple of 4.
-// kEpi 3 is the joint gate/up form: a workgroup takes 64 intermediate rows,
-// its LDS W tile holding those rows of W1 (tile rows 0..63) and of W2 (64..127);
-// wave (wy = w / 2) multiplies gate rows 32 wy .. +32 as its A blocks 0-1 and
-// the same up rows as blocks 2-3, so one lane holds g and u of the same
-// outputs and the epilogue writes act = half(g * (u / (1 + exp(-u)))) on the
-// fp16-rounded g and u, as swiglu_batched_kernel does.
-constexpr int kBt = 128;                     // tokens per workgroup
-constexpr int kBn = 128;                     // rows of W per workgroup
-constexpr int kBk = 64;                      // K per LDS tile
-constexpr int kBLd = kBk + 8;                // LDS row stride in halves
-constexpr int kBStage = kBt * kBk / 8 / 256; // 16-byte chunks per thread per operand (4)
-constexpr int kGemmXcds = 8;                 // MI355X: workgroups are dealt to 8 XCDs in turn
+// (4 x 4 MFMA blocks).  K goes in tiles of 64 through a ring of 5 LDS stages of 32 KB
+// (W tile then X tile, 128-byte rows with their 16-byte chunks swizzled by
+// (r / 2) % 8 as in gemm_nt_mfma_kernel) filled by direct loads
+// (global_load_lds_dwordx4, 8 per thread per stage), 4 tiles in flight
+// beyond the one being read: a register-staged version of this tile, with one
+// tile (~0.2 us of matrix-core work) in flight against an L2/MALL round trip
+// and two barriers per tile, ran the 2048-token QKV product in 72 us.  One
+// barrier per tile here, and the next tile's operand fragments are read from
+// LDS while the matrix cores consume the current tile's (with the reads and
+// the products of a tile in sequence, the kernel ran at ~25% of the matrix
+// cores' rate).  Operand reads are inline assembly with their own waits (see
+// gemm_nt_mfma_kernel).  The grid is
+// one-dimensional and XCD-major: XCD x computes a contiguous eighth of the
+// (W row tile, token tile) pairs, W row tile major, so its L2 holds an eighth
+// of W.  kEpi 0: half(sum); 1: half(R + half(sum)); 2: split K, slice z =
+// blockIdx.y stores its fp32 sums to p.part ([z][t][n], n a multiple of 4)
+// for splitk_fold_kernel; 3: the joint gate/up form
+// (64 intermediate rows per workgroup, W tile rows 0..63 from W1 and 64..127
+// the same rows of W2; wave (wy = w / 2) takes gate rows 32 wy .. +32 as its A
+// blocks 0-1 and the same up rows as blocks 2-3; act = half(g * (u / (1 +
+// exp(-u)))) on the fp16-rounded g and u).  Requires k a multiple of 64, y and
+// res 8-byte aligned and ldy a multiple of 4.
+constexpr int kRgT = 128;                        // tokens per workgroup
+constexpr int kRgN = 128;                        // W rows per workgroup (64 outputs when kEpi == 3)
+constexpr int kRgK = 64;                         // K per stage
+constexpr int kRgOps = kRgN * kRgK / 8 / 256;    // direct loads per thread per operand per stage (4)
+constexpr int kRgGroupN = 4;                     // W row tiles per group of the tile order
+
+struct __align__(16) RingStage {
+  uint16_t w[kRgN * kRgK];
+  uint16_t x[kRgT * kRgK];
+};
 
 template <int kEpi>
-__global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvParams p) {
-  __shared__ __align__(16) uint16_t xs[kBt * kBLd];
-  __shared__ __align__(16) uint16_t ws[kBn * kBLd];
+__global__ __launch_bounds__(256, 1) void gemm_nt_ring128_kernel(BatchedGemvParams p) {
+  __shared__ RingStage s0, s1, s2, s3, s4;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  constexpr int kRows = kEpi == 3 ? kBn / 2 : kBn;   // rows of the output per workgroup
-  const int ttiles = (p.t + kBt - 1) / kBt;
-  const int nwg = ttiles * ((p.n + kRows - 1) / kRows);
-  int pi = blockIdx.x;                         // XCD-major: XCD x takes pi in [x nwg/8, (x+1) nwg/8)
+  constexpr int kRows = kEpi == 3 ? kRgN / 2 : kRgN;   // output rows per workgroup
+  const int ttiles = (p.t + kRgT - 1) / kRgT;
+  const int ntiles = (p.n + kRows - 1) / kRows;
+  const int nwg = ttiles * ntiles;
+  int pi = blockIdx.x;
   if (nwg % kGemmXcds == 0) pi = (pi % kGemmXcds) * (nwg / kGemmXcds) + pi / kGemmXcds;
-  const int n0 = (pi / ttiles) * kRows;
-  const int t0 = (pi % ttiles) * kBt;
-  // staging map: chunk i of this thread is row (tid + 256 i) / (kBk / 8) of
-  // the tile, halves 8 ((tid + 256 i) % (kBk / 8)) .. +8 of its K tile (k is a
-  // multiple of kBk, so every chunk lies inside k)
-  const uint16_t* xg[kBStage];
-  const uint16_t* wg[kBStage];
-  int so[kBStage];
+  // Tile pi in groups of kRgGroupN W row tiles (fewer in the last group) x all
+  // token tiles, W tile fastest: 32 consecutive pi (one XCD's CUs) cover 4 W
+  // tiles x 8 token tiles, so each K slab an XCD fetches into its L2 serves 8
+  // or 4 workgroups (16 and 2 with W tile major order: 26% of L2 requests
+  // missed).
+  const int grp = pi / (kRgGroupN * ttiles);
+  const int gn = min(kRgGroupN, ntiles - grp * kRgGroupN);
+  const int rem = pi - grp * kRgGroupN * ttiles;
+  const int n0 = (grp * kRgGroupN + rem % gn) * kRows;
+  const int t0 = (rem / gn) * kRgT;
+  // kEpi 2 (split K): slice z = blockIdx.y sums K [z kslice, (z + 1) kslice)
+  const int kbeg = kEpi == 2 ? (int)blockIdx.y * p.kslice : 0;
+  const int ktiles = (kEpi == 2 ? min(p.k - kbeg, p.kslice) : p.k) / kRgK;
+
+  // Load i of wave w writes 1 KB at chunk 256 i + 64 w + lane of the stage's
+  // operand: row 32 i + 8 w + lane / 8, position lane % 8, which holds the
+  // row's global chunk (lane % 8) ^ mmswz(row).
+  const uint16_t* wg[kRgOps];
+  const uint16_t* xg[kRgOps];
 #pragma unroll
-  for (int i = 0; i < kBStage; ++i) {
-    const int c = tid + 256 * i;
-    const int r = c / (kBk / 8), col = (c % (kBk / 8)) * 8;
-    so[i] = r * kBLd + col;
-    xg[i] = p.x + (long long)min(t0 + r, p.t - 1) * p.ldx + col;
+  for (int i = 0; i < kRgOps; ++i) {
+    const int row = 32 * i + 8 * wave + (lane >> 3);
+    const int ch = (lane & 7) ^ mmswz(row);
     if constexpr (kEpi == 3)
-      wg[i] = (r < 64 ? p.w : p.w2) + (long long)min(n0 + (r & 63), p.n - 1) * p.k + col;
+      wg[i] = (row < 64 ? p.w : p.w2) + (long long)min(n0 + (row & 63), p.n - 1) * p.k + 8 * ch;
     else
-      wg[i] = p.w + (long long)min(n0 + r, p.n - 1) * p.k + col;
+      wg[i] = p.w + (long long)min(n0 + row, p.n - 1) * p.k + kbeg + 8 * ch;
+    xg[i] = p.x + (long long)min(t0 + row, p.t - 1) * p.ldx + kbeg + 8 * ch;
   }
-  f16x8 xr[kBStage], wr[kBStage];
-  auto fetch = [&](int k0) {
+  auto issue = [&](int kt, RingStage& st) {
+    const long long ko = (long long)min(kt, ktiles - 1) * kRgK;   // tiles past the last repeat it
 #pragma unroll
-    for (int i = 0; i < kBStage; ++i) {
-      xr[i] = *reinterpret_cast<const f16x8*>(xg[i] + k0);
-      wr[i] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(wg[i] + k0));
+    for (int i = 0; i < kRgOps; ++i) {
+      __builtin_amdgcn_global_load_lds(wg[i] + ko, (__attribute__((address_space(3))) void*)&st.w[(256 * i + 64 * wave) * 8],
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(xg[i] + ko, (__attribute__((address_space(3))) void*)&st.x[(256 * i + 64 * wave) * 8],
+                                       16, 0, 0);
     }
   };
-  const int wn = (wave >> 1) * 64, wt = (wave & 1) * 64;
-  const int fr = lane & 15, fk = (lane >> 4) * 8;
+
+  const int wy = wave >> 1, wx = wave & 1;
+  const int fr = lane & 15, fg = lane >> 4;
   f32x4_t acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  const int ktiles = p.k / kBk;
-  fetch(0);
-  for (int kt = 0; kt < ktiles; ++kt) {
-    __syncthreads();                           // every wave is done with the previous tile
+  // Byte offsets within a stage of the lane's fragments for K step ks: A (W)
+  // rows of block i, B (X) tokens of block j; chunk 4 ks + fg of the row.
+  unsigned aoff[2][4], boff[2][4];
 #pragma unroll
-    for (int i = 0; i < kBStage; ++i) {
-      *reinterpret_cast<f16x8*>(&xs[so[i]]) = xr[i];
-      *reinterpret_cast<f16x8*>(&ws[so[i]]) = wr[i];
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ar = (kEpi == 3 ? (i >> 1) * 64 + wy * 32 + 16 * (i & 1) : wy * 64 + 16 * i) + fr;
+      aoff[ks][i] = (unsigned)((ar * kRgK + 8 * ((4 * ks + fg) ^ mmswz(ar))) * 2);
+      const int br = wx * 64 + 16 * i + fr;
+      boff[ks][i] = (unsigned)((kRgN * kRgK + br * kRgK + 8 * ((4 * ks + fg) ^ mmswz(br))) * 2);
     }
-    __syncthreads();
-    if (kt + 1 < ktiles) fetch((kt + 1) * kBk);
+  // Fragments of one K tile: f[ks][i] (A, W rows of block i) and f[ks][4 + j]
+  // (B, tokens of block j) for the two K steps of 32.
+  typedef f16x8 Frags[2][8];
+  auto read_frags = [&](const RingStage& st, Frags& f) {
+    const unsigned base = (unsigned)(size_t)(const __attribute__((address_space(3))) void*)&st;
 #pragma unroll
-    for (int ks = 0; ks < kBk; ks += 32) {
-      f16x8 a[4], b[4];
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int ar = kEpi == 3 ? (i >> 1) * 64 + (wave >> 1) * 32 + 16 * (i & 1) : wn + 16 * i;
-        a[i] = *reinterpret_cast<const f16x8*>(&ws[(ar + fr) * kBLd + ks + fk]);
-        b[i] = *reinterpret_cast<const f16x8*>(&xs[(wt + 16 * i + fr) * kBLd + ks + fk]);
+        asm volatile("ds_read_b128 %0, %1" : "=v"(f[ks][i]) : "v"(base + aoff[ks][i]) : "memory");
+        asm volatile("ds_read_b128 %0, %1" : "=v"(f[ks][4 + i]) : "v"(base + boff[ks][i]) : "memory");
       }
+  };
+  auto mfma_tile = [&](const Frags& f) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-    }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[ks][i], f[ks][4 + j], acc[i][j], 0, 0, 0);
+  };
+  // The fragments' registers are bound to the wait, so no use of them can be
+  // scheduled before it.
+  auto wait_frags = [&](Frags& f, int) {
+    asm volatile("s_waitcnt vmcnt(24) lgkmcnt(0)\n\ts_barrier"
+                 : "+v"(f[0][0]), "+v"(f[0][1]), "+v"(f[0][2]), "+v"(f[0][3]), "+v"(f[0][4]),
+                   "+v"(f[0][5]), "+v"(f[0][6]), "+v"(f[0][7]), "+v"(f[1][0]), "+v"(f[1][1]),
+                   "+v"(f[1][2]), "+v"(f[1][3]), "+v"(f[1][4]), "+v"(f[1][5]), "+v"(f[1][6]),
+                   "+v"(f[1][7])
+                 :
+                 : "memory");
+  };
+  // Tile kt sits in stage kt % 5.  Iteration kt holds tile kt's fragments in
+  // registers (read during iteration kt - 1) and tiles kt + 1 .. kt + 4 in
+  // flight.  Each thread waits for its own loads of tile kt + 1 (three newer
+  // tiles of 8 loads stay in flight) and for its reads of tile kt; after the
+  // barrier tile kt + 1 is whole in LDS and tile kt's stage, which every wave
+  // has read, takes tile kt + 5.  Then tile kt + 1's fragments are read while
+  // the matrix cores consume tile kt's: the LDS reads and the products
+  // overlap.  The barrier is s_barrier alone: __syncthreads' fence would wait
+  // for every load in flight.
+  Frags fa, fb;
+  auto body = [&](int kt, Frags& cur, Frags& nxt, RingStage& own, const RingStage& next) {
+    wait_frags(cur, kt);
+    issue(kt + 5, own);
+    read_frags(next, nxt);
+    mfma_tile(cur);
+  };
+  issue(0, s0);
+  issue(1, s1);
+  issue(2, s2);
+  issue(3, s3);
+  issue(4, s4);
+  asm volatile("s_waitcnt vmcnt(32)\n\ts_barrier" ::: "memory");
+  read_frags(s0, fa);
+  for (int kt = 0; kt < ktiles; kt += 10) {
+    body(kt, fa, fb, s0, s1);
+    if (kt + 1 < ktiles) body(kt + 1, fb, fa, s1, s2);
+    if (kt + 2 < ktiles) body(kt + 2, fa, fb, s2, s3);
+    if (kt + 3 < ktiles) body(kt + 3, fb, fa, s3, s4);
+    if (kt + 4 < ktiles) body(kt + 4, fa, fb, s4, s0);
+    if (kt + 5 < ktiles) body(kt + 5, fb, fa, s0, s1);
+    if (kt + 6 < ktiles) body(kt + 6, fa, fb, s1, s2);
+    if (kt + 7 < ktiles) body(kt + 7, fb, fa, s2, s3);
+    if (kt + 8 < ktiles) body(kt + 8, fa, fb, s3, s4);
+    if (kt + 9 < ktiles) body(kt + 9, fb, fa, s4, s0);
   }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeated tail loads land before the workgroup ends
+
   if constexpr (kEpi == 3) {
     // blocks (i, j) and (i + 2, j), i < 2: gate and up of intermediate rows
-    // n0 + 32 wy + 16 i + 4 (l / 16) + r, token t0 + wt + 16 j + l % 16
+    // n0 + 32 wy + 16 i + 4 (l / 16) + r, token t0 + 64 wx + 16 j + l % 16
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int t = t0 + wt + 16 * j + fr;
+      const int t = t0 + wx * 64 + 16 * j + fr;
       if (t >= p.t) continue;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        const int n = n0 + (wave >> 1) * 32 + 16 * i + (lane >> 4) * 4;
+        const int n = n0 + wy * 32 + 16 * i + fg * 4;
         if (n >= p.n) continue;
         f16x4_t v;
 #pragma unroll
@@ -866,15 +951,19 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvPara
     }
     return;
   }
-  // block (i, j): rows n0 + wn + 16 i + 4 (l / 16) + r of W, token t0 + wt + 16 j + l % 16
+  // block (i, j): rows n0 + 64 wy + 16 i + 4 (l / 16) + r of W, token t0 + 64 wx + 16 j + l % 16
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int t = t0 + wt + 16 * j + fr;
+    const int t = t0 + wx * 64 + 16 * j + fr;
     if (t >= p.t) continue;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int n = n0 + wn + 16 * i + (lane >> 4) * 4;
+      const int n = n0 + wy * 64 + 16 * i + fg * 4;
       if (n >= p.n) continue;
+      if constexpr (kEpi == 2) {   // the slice's fp32 sums, [z][t][n] (n a multiple of 4)
+        *reinterpret_cast<f32x4_t*>(p.part + ((long long)blockIdx.y * p.t + t) * p.n + n) = acc[i][j];
+        continue;
+      }
       _Float16* dst = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
       const _Float16* res = reinterpret_cast<const _Float16*>(p.res) + (long long)t * p.ldy + n;
       if (n + 4 <= p.n) {
@@ -894,6 +983,225 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_mfma128_kernel(BatchedGemvPara
           _Float16 y = to_f16(acc[i][j][r]);
           if constexpr (kEpi == 1) y = (_Float16)((float)res[r] + (float)y);
           dst[r] = y;
+        }
+      }
+    }
+  }
+}
+
+// The same product with a 192-row x 256-token workgroup tile (products whose
+// grid of such tiles still covers the device: QKV and gate/up at 2048 tokens,
+// one and two tiles per CU).  Per K, a 128 x 128 tile moves 64 bytes from L2
+// into LDS and reads 128 from LDS per 2048 flops of its four 64 x 64 waves;
+// at the matrix cores' rate that is the whole measured direct-load rate of a
+// CU (~64 B per clock) and more than its LDS, and the 128 x 128 kernel ran at
+// ~35% of the matrix-core time (rocprofv3: SQ_VALU_MFMA_BUSY_CYCLES against
+// SQ_BUSY_CYCLES).  Here each of the four waves computes 96 W rows x 128
+// tokens (6 x 8 MFMA blocks, 192 accumulator registers): 37 B per clock from
+// L2 and ~110 from LDS at the matrix cores' rate.  K goes in tiles of 32
+// through a ring of 5 stages of 28 KB (W tile 192 x 64 B, then X tile 256 x
+// 64 B; chunk q of row r at q ^ ((r / 4) % 4), so the 16 rows of one fragment
+// read fall on distinct banks), 4 tiles in flight, filled by direct loads (7
+// per thread per stage), the next tile's fragments read from LDS while the
+// matrix cores consume the current one's.  kEpi 0: half(sum); 1: half(R +
+// half(sum)); 3: joint gate/up, 96 outputs per workgroup (W tile rows 0..95
+// from W1, 96..191 the same rows of W2; wave (wy = w / 2) takes gate rows
+// 48 wy + 16 i as its A blocks i < 3 and the same up rows as blocks i + 3).
+constexpr int kR2N = 192;                        // W rows per workgroup (96 outputs when kEpi == 3)
+constexpr int kR2T = 256;                        // tokens per workgroup
+constexpr int kR2K = 32;                         // K per stage
+constexpr int kR2A = kR2N * kR2K / 8 / 64;       // 1 KB direct loads per stage: W (12)
+constexpr int kR2B = kR2T * kR2K / 8 / 64;       // X (16)
+constexpr int kR2Loads = (kR2A + kR2B) / 4;      // per thread per stage (7)
+
+struct __align__(16) Ring2Stage {
+  uint16_t w[kR2N * kR2K];
+  uint16_t x[kR2T * kR2K];
+};
+__device__ __forceinline__ int r2swz(int r) { return (r >> 2) & 3; }
+
+template <int kEpi>
+__global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvParams p) {
+  __shared__ Ring2Stage s0, s1, s2, s3, s4;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  constexpr int kRows = kEpi == 3 ? kR2N / 2 : kR2N;   // output rows per workgroup
+  const int ttiles = (p.t + kR2T - 1) / kR2T;
+  const int ntiles = (p.n + kRows - 1) / kRows;
+  const int nwg = ttiles * ntiles;
+  int pi = blockIdx.x;
+  if (nwg % kGemmXcds == 0) pi = (pi % kGemmXcds) * (nwg / kGemmXcds) + pi / kGemmXcds;
+  const int n0 = (pi / ttiles) * kRows;
+  const int t0 = (pi % ttiles) * kR2T;
+  const int ktiles = p.k / kR2K;
+
+  // Direct load j of this wave is 1 KB load L = wave + 4 j of the stage: W
+  // rows 16 L .. +16 for L < 12, else X rows 16 (L - 12) .. +16; lane l fills
+  // row 16 L' + l / 4, position l % 4, with the row's global chunk
+  // (l % 4) ^ r2swz(row).
+  const uint16_t* src[kR2Loads];
+  unsigned dst[kR2Loads];
+#pragma unroll
+  for (int j = 0; j < kR2Loads; ++j) {
+    const int L = wave + 4 * j;
+    const bool isw = L < kR2A;
+    const int row = 16 * (isw ? L : L - kR2A) + (lane >> 2);
+    const int ch = (lane & 3) ^ r2swz(row);
+    if (isw) {
+      if constexpr (kEpi == 3)
+        src[j] = (row < kRows ? p.w : p.w2) + (long long)min(n0 + row % kRows, p.n - 1) * p.k + 8 * ch;
+      else
+        src[j] = p.w + (long long)min(n0 + row, p.n - 1) * p.k + 8 * ch;
+    } else {
+      src[j] = p.x + (long long)min(t0 + row, p.t - 1) * p.ldx + 8 * ch;
+    }
+    dst[j] = (unsigned)(L * 1024);
+  }
+  auto issue = [&](int kt, Ring2Stage& st) {
+    const long long ko = (long long)min(kt, ktiles - 1) * kR2K;   // tiles past the last repeat it
+    char* base = reinterpret_cast<char*>(&st);
+#pragma unroll
+    for (int j = 0; j < kR2Loads; ++j)
+      __builtin_amdgcn_global_load_lds(src[j] + ko, (__attribute__((address_space(3))) void*)(base + dst[j]), 16, 0, 0);
+  };
+
+  const int wy = wave >> 1, wx = wave & 1;
+  const int fr = lane & 15, fg = lane >> 4;
+  f32x4_t acc[6][8];
+#pragma unroll
+  for (int i = 0; i < 6; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // Byte offsets within a stage of the lane's fragments: A (W) rows of block
+  // i, B (X) tokens of block j; chunk fg of the row.
+  unsigned aoff[6], boff[8];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) {
+    const int ar = (kEpi == 3 ? (i / 3) * kRows + wy * 48 + 16 * (i % 3) : wy * 96 + 16 * i) + fr;
+    aoff[i] = (unsigned)(ar * kR2K * 2 + 16 * (fg ^ r2swz(ar)));
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int br = wx * 128 + 16 * j + fr;
+    boff[j] = (unsigned)(kR2N * kR2K * 2 + br * kR2K * 2 + 16 * (fg ^ r2swz(br)));
+  }
+  typedef f16x8 Frags[14];   // A blocks 0..5, then B blocks 0..7
+  auto read_frags = [&](const Ring2Stage& st, Frags& f) {
+    const unsigned base = (unsigned)(size_t)(const __attribute__((address_space(3))) void*)&st;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) asm volatile("ds_read_b128 %0, %1" : "=v"(f[i]) : "v"(base + aoff[i]) : "memory");
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("ds_read_b128 %0, %1" : "=v"(f[6 + j]) : "v"(base + boff[j]) : "memory");
+  };
+  auto mfma_tile = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[i], f[6 + j], acc[i][j], 0, 0, 0);
+  };
+  // The fragments' registers are bound to the wait, so no use of them can be
+  // scheduled before it.  Tile kt sits in stage kt % 5; iteration kt holds
+  // its fragments (read during iteration kt - 1) and tiles kt + 1 .. kt + 4 in
+  // flight; each thread waits for its loads of tile kt + 1 (three newer tiles
+  // of 7 loads stay in flight) and its reads of tile kt, and after the
+  // barrier tile kt's stage takes tile kt + 5 (see gemm_nt_ring128_kernel).
+  auto wait_frags = [&](Frags& f) {
+    asm volatile("s_waitcnt vmcnt(21) lgkmcnt(0)\n\ts_barrier"
+                 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
+                   "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]),
+                   "+v"(f[12]), "+v"(f[13])
+                 :
+                 : "memory");
+  };
+  Frags fa, fb;
+  auto body = [&](int kt, Frags& cur, Frags& nxt, Ring2Stage& own, const Ring2Stage& next) {
+    wait_frags(cur);
+    issue(kt + 5, own);
+    read_frags(next, nxt);
+    mfma_tile(cur);
+  };
+  issue(0, s0);
+  issue(1, s1);
+  issue(2, s2);
+  issue(3, s3);
+  issue(4, s4);
+  asm volatile("s_waitcnt vmcnt(28)\n\ts_barrier" ::: "memory");
+  read_frags(s0, fa);
+  for (int kt = 0; kt < ktiles; kt += 10) {
+    body(kt, fa, fb, s0, s1);
+    if (kt + 1 < ktiles) body(kt + 1, fb, fa, s1, s2);
+    if (kt + 2 < ktiles) body(kt + 2, fa, fb, s2, s3);
+    if (kt + 3 < ktiles) body(kt + 3, fb, fa, s3, s4);
+    if (kt + 4 < ktiles) body(kt + 4, fa, fb, s4, s0);
+    if (kt + 5 < ktiles) body(kt + 5, fb, fa, s0, s1);
+    if (kt + 6 < ktiles) body(kt + 6, fa, fb, s1, s2);
+    if (kt + 7 < ktiles) body(kt + 7, fb, fa, s2, s3);
+    if (kt + 8 < ktiles) body(kt + 8, fa, fb, s3, s4);
+    if (kt + 9 < ktiles) body(kt + 9, fb, fa, s4, s0);
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");   // tail loads land before the workgroup ends
+
+  if constexpr (kEpi == 3) {
+    // blocks (i, j) and (i + 3, j), i < 3: gate and up of outputs
+    // n0 + 48 wy + 16 i + 4 (l / 16) + r, token t0 + 128 wx + 16 j + l % 16
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int t = t0 + wx * 128 + 16 * j + fr;
+      if (t >= p.t) continue;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        const int n = n0 + wy * 48 + 16 * i + fg * 4;
+        if (n >= p.n) continue;
+        f16x4_t v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float gh = (float)to_f16(acc[i][j][r]);
+          const float uh = (float)to_f16(acc[i + 3][j][r]);
+          const float e = exp2_rep(-uh * kLog2e);
+          v[r] = to_f16(gh * (uh / (1.0f + e)));
+        }
+        _Float16* dstp = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
+        if (n + 4 <= p.n) {
+          *reinterpret_cast<f16x4_t*>(dstp) = v;
+        } else {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (n + r < p.n) dstp[r] = v[r];
+        }
+      }
+    }
+    return;
+  }
+  // block (i, j): rows n0 + 96 wy + 16 i + 4 (l / 16) + r of W, token t0 + 128 wx + 16 j + l % 16
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int t = t0 + wx * 128 + 16 * j + fr;
+    if (t >= p.t) continue;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int n = n0 + wy * 96 + 16 * i + fg * 4;
+      if (n >= p.n) continue;
+      _Float16* dstp = reinterpret_cast<_Float16*>(p.y) + (long long)t * p.ldy + n;
+      const _Float16* res = reinterpret_cast<const _Float16*>(p.res) + (long long)t * p.ldy + n;
+      if (n + 4 <= p.n) {
+        f16x4_t v;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = to_f16(acc[i][j][r]);
+        if constexpr (kEpi == 1) {
+          const f16x4_t rv = *reinterpret_cast<const f16x4_t*>(res);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[r] = (_Float16)((float)rv[r] + (float)v[r]);
+        }
+        *reinterpret_cast<f16x4_t*>(dstp) = v;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          if (n + r >= p.n) break;
+          _Float16 y = to_f16(acc[i][j][r]);
+          if constexpr (kEpi == 1) y = (_Float16)((float)res[r] + (float)y);
+          dstp[r] = y;
         }
       }
     }
@@ -1015,21 +1323,44 @@ hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t*
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream) {
-  if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
-  if (p.t >= kBlasltMinRows) {   // plain products from 128 rows: the vendor library (qd_blaslt.cpp)
-    const hipError_t e = blaslt_gemm_nt(p, epi, stream);
-    if (e != hipErrorNotSupported) return e;
-  }
+// Tile choice of a plain product from kRingMinRows tokens: 192 x 256 where
+// that grid covers every CU (2048-token QKV: 256 tiles), else 128 x 128 where
+// that grid covers at least half of them (a 128 x 128 grid of 192 tiles ran
+// the 512-token QKV product as fast as hipBLASLt), else the 64 x 64 tile.
+enum class GemmTile { k64, k128, k192 };
+
+static GemmTile pick_tile(const BatchedGemvParams& p, int rows_per_out) {
   const bool vec8 = ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) == 0 &&
                     p.ldy % 4 == 0;
-  if (p.t >= 512 && vec8 && p.k % kBk == 0) {
-    const dim3 grid(((p.n + kBn - 1) / kBn) * ((p.t + kBt - 1) / kBt));
-    if (epi == 0)
-      hipLaunchKernelGGL(gemm_nt_mfma128_kernel<0>, grid, dim3(256), 0, stream, p);
-    else
-      hipLaunchKernelGGL(gemm_nt_mfma128_kernel<1>, grid, dim3(256), 0, stream, p);
-    return hipGetLastError();
+  if (p.t < kRingMinRows || !vec8) return GemmTile::k64;
+  const int cus = device_cus();
+  const long long big = (long long)((p.n * rows_per_out + kR2N - 1) / kR2N) * ((p.t + kR2T - 1) / kR2T);
+  if (big >= cus) return GemmTile::k192;
+  const long long mid = (long long)((p.n * rows_per_out + kRgN - 1) / kRgN) * ((p.t + kRgT - 1) / kRgT);
+  return 2 * mid >= cus ? GemmTile::k128 : GemmTile::k64;
+}
+
+hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream) {
+  if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
+  switch (pick_tile(p, 1)) {
+    case GemmTile::k192: {
+      const dim3 grid((unsigned)(((p.n + kR2N - 1) / kR2N) * ((p.t + kR2T - 1) / kR2T)));
+      if (epi == 0)
+        hipLaunchKernelGGL(gemm_nt_ring192_kernel<0>, grid, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL(gemm_nt_ring192_kernel<1>, grid, dim3(256), 0, stream, p);
+      return hipGetLastError();
+    }
+    case GemmTile::k128: {
+      const dim3 grid((unsigned)(((p.n + kRgN - 1) / kRgN) * ((p.t + kRgT - 1) / kRgT)));
+      if (epi == 0)
+        hipLaunchKernelGGL(gemm_nt_ring128_kernel<0>, grid, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL(gemm_nt_ring128_kernel<1>, grid, dim3(256), 0, stream, p);
+      return hipGetLastError();
+    }
+    default:
+      break;
   }
   const dim3 grid((p.n + kMmTile - 1) / kMmTile, (p.t + kMmTile - 1) / kMmTile);
   if (epi == 0)
@@ -1041,34 +1372,60 @@ hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t str
 
 hipError_t launch_gemm_mfma_swiglu(const BatchedGemvParams& p, hipStream_t stream) {
   if (p.k < 64 || p.k % 64 != 0 || p.n < 1 || p.t < 1 || !p.w2) return hipErrorNotSupported;
-  if (p.t >= 512 && p.k % kBk == 0 && !(reinterpret_cast<uintptr_t>(p.y) & 7u) && p.ldy % 4 == 0) {
-    const dim3 grid(((p.n + kBn / 2 - 1) / (kBn / 2)) * ((p.t + kBt - 1) / kBt));
-    hipLaunchKernelGGL(gemm_nt_mfma128_kernel<3>, grid, dim3(256), 0, stream, p);
-  } else {
-    const dim3 grid((p.n + kMmTile / 2 - 1) / (kMmTile / 2), (p.t + kMmTile - 1) / kMmTile);
-    hipLaunchKernelGGL(gemm_nt_mfma_kernel<3>, grid, dim3(256), 0, stream, p);
+  switch (pick_tile(p, 2)) {   // two W rows (gate and up) per output
+    case GemmTile::k192:
+      hipLaunchKernelGGL(gemm_nt_ring192_kernel<3>,
+                         dim3((unsigned)(((p.n + kR2N / 2 - 1) / (kR2N / 2)) * ((p.t + kR2T - 1) / kR2T))),
+                         dim3(256), 0, stream, p);
+      break;
+    case GemmTile::k128:
+      hipLaunchKernelGGL(gemm_nt_ring128_kernel<3>,
+                         dim3((unsigned)(((p.n + kRgN / 2 - 1) / (kRgN / 2)) * ((p.t + kRgT - 1) / kRgT))),
+                         dim3(256), 0, stream, p);
+      break;
+    default: {
+      const dim3 grid((p.n + kMmTile / 2 - 1) / (kMmTile / 2), (p.t + kMmTile - 1) / kMmTile);
+      hipLaunchKernelGGL(gemm_nt_mfma_kernel<3>, grid, dim3(256), 0, stream, p);
+      break;
+    }
   }
   return hipGetLastError();
 }
 
+// Splits K over up to kGemmMaxSplits slices of whole 64-wide tiles when the
+// product's grid leaves CUs idle and the workspace holds the slices' fp32
+// partials; one launch then adds the slices in order with the epilogue
+// (splitk_fold_kernel).  From kRingMinRows tokens with n a multiple of 4 the
+// slices run on the 128 x 128 ring tile (the 256-token c_proj product: 32
+// tiles of K = 5504), below it on the 64 x 64 tile.
 hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* workspace,
                                   size_t workspace_bytes, hipStream_t stream) {
   if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
-  const long long tiles = (long long)((p.n + kMmTile - 1) / kMmTile) * ((p.t + kMmTile - 1) / kMmTile);
-  // the conditions under which launch_gemm_mfma takes the 64 x 64 tile
-  const bool small = p.t < 512 || ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) ||
-                     p.ldy % 4 || p.k % kBk;
-  int splits = small && workspace && p.t < kBlasltMinRows ? (int)std::min<long long>(4, 256 / tiles) : 1;
+  const GemmTile tile = pick_tile(p, 1);
+  const bool ring = p.t >= kRingMinRows && p.n % 4 == 0 && tile != GemmTile::k192 &&
+                    ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) == 0 &&
+                    p.ldy % 4 == 0;
+  const int tn = ring ? kRgN : kMmTile, tt = ring ? kRgT : kMmTile;
+  const long long tiles = (long long)((p.n + tn - 1) / tn) * ((p.t + tt - 1) / tt);
+  const int cus = device_cus();
+  int splits = 1;
+  if (workspace && tile != GemmTile::k192 && tiles < cus)
+    splits = (int)std::min<long long>(kGemmMaxSplits, (cus + tiles - 1) / tiles);
   if (splits > 1) {
-    // slices of whole K tiles, none empty
+    // slices of whole K tiles, none empty, as many as the workspace holds
+    while (splits > 1 && (size_t)splits * p.t * p.n * sizeof(float) > workspace_bytes) --splits;
     const int kslice = ((p.k + splits - 1) / splits + kMmK - 1) / kMmK * kMmK;
     splits = (p.k + kslice - 1) / kslice;
-    if (splits > 1 && (size_t)splits * p.t * p.n * sizeof(float) <= workspace_bytes) {
+    if (splits > 1) {
       BatchedGemvParams q = p;
       q.part = workspace;
       q.kslice = kslice;
-      const dim3 grid((p.n + kMmTile - 1) / kMmTile, (p.t + kMmTile - 1) / kMmTile, splits);
-      hipLaunchKernelGGL(gemm_nt_mfma_kernel<2>, grid, dim3(256), 0, stream, q);
+      if (ring)
+        hipLaunchKernelGGL(gemm_nt_ring128_kernel<2>, dim3((unsigned)tiles, splits), dim3(256), 0, stream, q);
+      else
+        hipLaunchKernelGGL(gemm_nt_mfma_kernel<2>,
+                           dim3((p.n + kMmTile - 1) / kMmTile, (p.t + kMmTile - 1) / kMmTile, splits),
+                           dim3(256), 0, stream, q);
       hipError_t e = hipGetLastError();
       if (e != hipSuccess) return e;
       const dim3 fgrid((unsigned)(((long long)p.t * p.n + 255) / 256));

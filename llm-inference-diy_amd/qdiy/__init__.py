@@ -37,7 +37,7 @@ EXPORTS = (
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
-    "qd_gemm_nt", "qd_gemm_vendor_enable", "qd_gemm_swiglu", "qd_prefill_attention",
+    "qd_gemm_nt", "qd_gemm_swiglu", "qd_prefill_attention",
     # qdiy/engine.h
     "qd_model_image_bytes", "qd_model_fill_random", "qd_model_write_random", "qd_engine_create",
     "qd_engine_create_from_image", "qd_engine_destroy", "qd_engine_config", "qd_engine_reset",
@@ -126,7 +126,6 @@ def load() -> ctypes.CDLL:
     ip = ctypes.POINTER(ctypes.c_int)
     L.qd_proj_residual.argtypes = [vp, vp, vp, vp, i, i, vp]
     L.qd_gemm_nt.argtypes = [vp, ll, vp, vp, vp, ll, i, i, i, i, vp]
-    L.qd_gemm_vendor_enable.argtypes = [i]
     L.qd_gemm_swiglu.argtypes = [vp, ll, vp, vp, vp, ll, i, i, i, vp]
     L.qd_prefill_attention.argtypes = [vp, vp, ll, vp, vp, vp, ll, i, i, i, i, i, vp]
     L.qd_engine_set_prefill_mode.argtypes = [vp, i]
@@ -413,13 +412,6 @@ def gemm_nt(x: torch.Tensor, w: torch.Tensor, y: torch.Tensor, m: int, n: int, k
                              None if residual is None else _ptr(residual, "residual"), _ptr(y, "y"),
                              ldy, m, n, k, mode, _stream(stream)))
     return y
-
-
-def gemm_vendor_enable(enable: bool) -> bool:
-    """Let GEMM_MFMA products of 128 rows and more run in hipBLASLt (True, the
-    default) or only in this library's own tiles (False), process-wide;
-    returns the previous setting (qd_gemm_vendor_enable)."""
-    return bool(load().qd_gemm_vendor_enable(1 if enable else 0))
 
 
 def gemm_swiglu(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, act: torch.Tensor, m: int,

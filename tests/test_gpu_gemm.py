@@ -65,23 +65,17 @@ def test_exact_mode_is_the_decode_gemv(qdiy, m, n, k, with_res):
         assert _same(got[i], want), f"row {i}"
 
 
-@pytest.fixture(params=[True, False], ids=["vendor", "own_tiles"])
-def vendor(qdiy, request):
-    """GEMM_MFMA products from 128 rows in hipBLASLt (the default), or only in
-    the library's own tiles (the 64 x 64 tile below 512 rows, the 128 x 128
-    tile from 512): the fallback when the vendor library has no kernel."""
-    prev = qdiy.gemm_vendor_enable(request.param)
-    yield request.param
-    qdiy.gemm_vendor_enable(prev)
-
-
 @pytest.mark.parametrize("m,n,k", [(1, 64, 64), (37, 100, 512), (127, 6144, 2048), (256, 2048, 5504),
                                    (200, 5504, 2048),
-                                   # m >= 512 (own tiles: the 128 x 128 tile; ragged m and n, a
-                                   # partial group of four outputs at n = 130)
-                                   (600, 130, 512), (1024, 2048, 5504), (2048, 6144, 2048)])
+                                   # from 128 rows: the 64 x 64 tile where a 128 x 128 grid would
+                                   # leave most CUs idle (ragged m and n, a partial group of four
+                                   # outputs at n = 130), the 128 x 128 ring tile, and the 192 x 256
+                                   # ring tile where its grid covers the CUs (ragged rows of W at
+                                   # n = 6000, ragged tokens at m = 1800)
+                                   (600, 130, 512), (1024, 2048, 5504), (512, 6144, 2048),
+                                   (2048, 6144, 2048), (2048, 6000, 2048), (1800, 6144, 1024)])
 @pytest.mark.parametrize("with_res", [False, True])
-def test_mfma_mode_within_fp32_summation_bound(qdiy, vendor, m, n, k, with_res):
+def test_mfma_mode_within_fp32_summation_bound(qdiy, m, n, k, with_res):
     rng = np.random.default_rng(7 * m + n + k + with_res)
     x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
     y = torch.full((m * n + 64,), 9.0, dtype=torch.float16, device="cuda")
@@ -104,10 +98,12 @@ def test_mfma_mode_within_fp32_summation_bound(qdiy, vendor, m, n, k, with_res):
 
 
 @pytest.mark.parametrize("m,n,k,ldy", [(37, 100, 512, 100), (127, 1368, 2048, 1368),
-                                        # m >= 512: the 128 x 128 tile, a ragged last tile
-                                        # (n = 130, 1000) and a strided output
+                                        # from 128 rows: the 64 x 64 tile (n = 130, a strided
+                                        # output), the 128 x 128 ring tile (a ragged last tile at
+                                        # n = 1000; 512 x 5504), the 192 x 256 ring tile (2048 x
+                                        # 5504: a last tile of 32 of its 96 outputs)
                                         (600, 130, 512, 136), (1000, 1000, 1024, 1000),
-                                        (512, 5504, 2048, 5504)])
+                                        (512, 5504, 2048, 5504), (2048, 5504, 2048, 5504)])
 def test_gemm_swiglu_within_bound(qdiy, m, n, k, ldy):
     """qd_gemm_swiglu: gate and up GEMMs on the matrix cores with the SwiGLU in the
     epilogue.  Each act is half(g * silu(u)) of g and u the fp16 roundings of
@@ -145,10 +141,10 @@ def test_gemm_swiglu_within_bound(qdiy, m, n, k, ldy):
 
 
 @pytest.mark.parametrize("seed", range(16))
-def test_mfma_random_shapes(qdiy, vendor, seed):
-    """Seeded random m (both sides of the 128-row vendor threshold and of the
+def test_mfma_random_shapes(qdiy, seed):
+    """Seeded random m (both sides of the 128-row ring-tile threshold and of the
     64-token tile), n (ragged against 64), k (a multiple of 64 up to 6144, so the
-    K-tile ring wraps several times or runs short of its 8 stages), row strides
+    K-tile rings wrap several times or run short of their stages), row strides
     and the residual form of qd_gemm_nt, then qd_gemm_swiglu at the same m:
     every output within the bounds of the fixed-shape tests."""
     rng = np.random.default_rng(52000 + seed)
@@ -215,10 +211,10 @@ def test_gemm_nt_rejects_bad_arguments(qdiy):
     torch.cuda.synchronize()
 
 
-def test_mfma_large_m_unaligned_output_and_in_place_residual(qdiy, vendor):
-    """m >= 512 with y rows an odd number of elements apart (among the own
-    tiles the 64 x 64 tile takes it) and with the residual added in place (the
-    128 x 128 tile): both within the fp32 summation bound."""
+def test_mfma_large_m_unaligned_output_and_in_place_residual(qdiy):
+    """m >= 512 with y rows an odd number of elements apart (the 64 x 64 tile
+    takes it: the ring tiles store 8 bytes at a time) and with the residual
+    added in place: both within the fp32 summation bound."""
     m, n, k = 640, 96, 256
     rng = np.random.default_rng(3)
     x, W, R = normal_f16(rng, (m, k)), normal_f16(rng, (n, k), 0.02), normal_f16(rng, (m, n))
@@ -242,13 +238,13 @@ def test_mfma_large_m_unaligned_output_and_in_place_residual(qdiy, vendor):
 
 @pytest.mark.parametrize("hidden,inter,n_prompt", [(512, 1368, 100), (512, 1368, 300), (2048, 5504, 300),
                                                   (512, 1408, 700)])
-def test_engine_mfma_prefill(qdiy, vendor, hidden, inter, n_prompt):
+def test_engine_mfma_prefill(qdiy, hidden, inter, n_prompt):
     """MFMA prefill against exact prefill on the same prompt (with c_proj exact
     where inter is not a multiple of 64): the next step's logits agree to the
     fp32-order difference, and plain decode steps are bit-identical in both
-    modes.  From 128 prompt tokens the plain products go to the vendor library
-    (when enabled) and the gate/up product is one 2 * inter column product
-    followed by the elementwise SwiGLU; below, the hand-written tiles run."""
+    modes.  At hidden 2048 and 299 tokens the o_proj and c_proj products have
+    48 tiles of 128 x 128 and run split over K on that tile (engine workspace,
+    then the fold launch); gate/up is one launch with the SwiGLU epilogue."""
     cfg = qdiy.model_cfg(vocab_size=512, hidden_size=hidden, num_layers=2, num_heads=hidden // 128,
                          intermediate_size=inter, max_seqlen=n_prompt + 20)
     img = qdiy.random_model_image(cfg, 41 + hidden, 0.03, nthreads=8)
