@@ -419,17 +419,22 @@ def measure_front(lib, steps: int, warmup: int):
         return e0.elapsed_time(e1) * 1e3 / iters
 
     us_front = timed(steps, 0, WARMUP_FLOOR_S)
-    us_all = timed(steps, 1, 0.0)
+    us_two = timed(steps, 1, 0.0)        # qd_qkv_proj_rope_cache, then qd_decode_attention
+    us_all = timed(steps, 2, 0.0)        # qd_qkv_proj_rope_cache_attention (one launch)
     ctx.close()
     del w, kc, vc
     torch.cuda.empty_cache()
     front_bytes = w_elems * 2 + HID * 2 + 3 * HID * 2 + 2 * HID * 2
     all_bytes = front_bytes + 2 * L * HID * 2 + HID * 2      # config 4 (L=2048): 41,971,712 B
     log(f"[bench] config 4 (L=2048, pos 2047): front end {us_front:.2f} us "
-        f"({front_bytes / us_front / 1e3:.0f} GB/s), front end + attention {us_all:.2f} us "
-        f"({all_bytes / us_all / 1e3:.0f} GB/s), {n_layers} layers rotated")
+        f"({front_bytes / us_front / 1e3:.0f} GB/s), front end + attention {us_all:.2f} us in one "
+        f"call ({all_bytes / us_all / 1e3:.0f} GB/s; {us_two:.2f} us as two calls), {n_layers} layers "
+        f"rotated")
     return {"us_front_end": round(us_front, 3), "us_front_end_plus_attention": round(us_all, 3),
+            "entry": "qd_qkv_proj_rope_cache_attention",
+            "us_front_end_plus_attention_two_calls": round(us_two, 3),
             "bytes": all_bytes, "gbps": round(all_bytes / us_all / 1e3, 1),
+            "pct_of_peak": round(100 * all_bytes / us_all / 1e3 / PEAK_GBPS, 1),
             "front_end_gbps": round(front_bytes / us_front / 1e3, 1)}
 
 

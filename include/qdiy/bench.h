@@ -64,6 +64,19 @@ int qd_ctx_set_scan_depth(qd_ctx* ctx, int depth);
  * every call is reported by qd_decode_attention_plan_detail. */
 int qd_ctx_set_split_shape(qd_ctx* ctx, int waves, int rows_per_tile, int interleave);
 
+/* Test hook of qd_qkv_proj_rope_cache_attention's one-launch form: with on
+ * nonzero, every split workgroup computes its head's front end itself, as it
+ * does when the producers' words stay invisible to it (a producer ran on
+ * another XCD).  Outputs are unchanged; 0 (the default) turns it off. */
+int qd_ctx_set_front_local(qd_ctx* ctx, int on);
+
+/* Split workgroups of qd_qkv_proj_rope_cache_attention's one-launch form that
+ * computed their head's front end themselves because the producers' words
+ * stayed invisible to them (summed over heads, over every call; those forced
+ * by qd_ctx_set_front_local are not counted).  0 when the producers and the
+ * splits of each head share an XCD, as the launch arranges.  Synchronous. */
+int qd_ctx_front_misses(const qd_ctx* ctx, unsigned long long* misses);
+
 /* Turns counting of in-kernel merges and their slot reads on (nonzero) or
  * off (the default: the counts are atomics issued after the output, and a
  * kernel ends only when they have completed, so they lengthen a call). */

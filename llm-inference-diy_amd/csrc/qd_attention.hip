@@ -47,10 +47,12 @@
 //     serialised per XCD), more than a second launch.  Both folds perform the
 //     same operations in the same order.
 //   * No MFMA: at q=1 the work is a bandwidth-bound GEMV-like reduction.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 
 #include "qd_device.h"
+#include "qd_front_device.h"
 #include "qd_internal.h"
 
 namespace qd {
@@ -301,22 +303,47 @@ struct ScanLds {
 // states in LDS, max-first: for tid < 128, (M, L, O) is the workgroup's
 // partial for dim tid (M and L the same in every thread).  Ends with the LDS
 // reads of the fold; a caller that reuses `lds` synchronises first.
+// Fold each wave's four groups with lane shuffles and the NW wave states in
+// LDS, max-first: for tid < 128, (M, L, O) is the workgroup's partial for dim
+// tid (M and L the same in every thread).  Ends with the LDS reads of the
+// fold; a caller that reuses `lds` synchronises first.
+template <int NW>
+__device__ __forceinline__ void fold_waves(GroupState& st, ScanLds<NW>& lds, float& M, float& L,
+                                           float& O);
+
 template <int NW, int U, int D = 1, bool kInter = false>
-__device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q, int h, int r0,
-                                          int nrows, ScanLds<NW>& lds, float& M, float& L,
-                                          float& O, int c = 0) {
+__device__ __forceinline__ void scan_fold_q(const AttnParams& p, const f16x8 qv, int h, int r0,
+                                            int nrows, ScanLds<NW>& lds, float& M, float& L,
+                                            float& O, int c = 0) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
   const int g = lane >> 4;
   const int t = lane & 15;
-  const f16x8 qv = *reinterpret_cast<const f16x8*>(q + h * kD + t * 8);
   const long long off = h * p.head_stride + (long long)r0 * p.row_stride;
   GroupState st;
   init_state(st);
   scan_rows<NW, U, D, kInter>(st, reinterpret_cast<const char*>(p.k + off),
                               reinterpret_cast<const char*>(p.v + off), (unsigned)(p.row_stride * 2),
                               nrows, wave, g, t, qv, p.scale_log2, c, p.splits);
+  fold_waves<NW>(st, lds, M, L, O);
+}
+
+template <int NW, int U, int D = 1, bool kInter = false>
+__device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q, int h, int r0,
+                                          int nrows, ScanLds<NW>& lds, float& M, float& L,
+                                          float& O, int c = 0) {
+  const f16x8 qv = *reinterpret_cast<const f16x8*>(q + h * kD + (threadIdx.x & 15) * 8);
+  scan_fold_q<NW, U, D, kInter>(p, qv, h, r0, nrows, lds, M, L, O, c);
+}
+
+template <int NW>
+__device__ __forceinline__ void fold_waves(GroupState& st, ScanLds<NW>& lds, float& M, float& L,
+                                           float& O) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int t = lane & 15;
   wave_merge(st);
   if (lane < 16) {
     *reinterpret_cast<f32x4*>(&lds.so[wave][t * 8]) = f32x4{st.o[0], st.o[1], st.o[2], st.o[3]};
@@ -724,32 +751,24 @@ __device__ __forceinline__ unsigned long long merge_wave(const AttnParams& p, co
   }
 }
 
-// SMAX: a bound on p.splits (16, 32 or 64): the slots each merging wave reads.
-// NW scanning waves (4 or 8); kInter: interleaved blocks of NW * 4 * U rows.
-template <int U, int SMAX, int D = 1, int NW = 4, bool kInter = false>
-__global__ __launch_bounds__(NW * 64) void decode_attention_xmerge_kernel(AttnParams p) {
-  static_assert(SMAX % 4 == 0 && SMAX <= kXMaxSplits, "SMAX: a multiple of 4, at most the slot count");
-  static_assert(NW == 4 || NW == 8, "four or eight waves scan; waves 0 and 1 hold the 128 dims");
-  __shared__ ScanLds<NW> slds;
-  __shared__ unsigned long long s_need[2];   // splits to scan again, per merging wave
+// The end of a split workgroup of an in-kernel-merge plan, after its scan:
+// (M, L, O) its partial (threads tid < 128).  Every split but the head's last
+// publishes its partial as tagged words and ends; the last merges (see
+// decode_attention_xmerge_kernel).  qv: this lane's Q chunk, for scanning
+// splits again.
+template <int U, int SMAX, int D, int NW, bool kInter>
+__device__ __forceinline__ void xmerge_finish(const AttnParams& p, int h, int c, const f16x8 qv,
+                                              float M, float L, float O, ScanLds<NW>& slds,
+                                              unsigned long long (&s_need)[2]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int h = blockIdx.x % p.num_heads;
-  const int c = blockIdx.x / p.num_heads;
   const int splits = p.splits;
   const int merger = splits - 1;                             // the last split, often the shortest
   const float tagf = __uint_as_float(p.tag);
   float2* head_slots = p.xpart + (long long)h * kXMaxSplits * kXSlotWords;
   const char* head = reinterpret_cast<const char*>(head_slots);
-
   constexpr int kBlock = NW * 4 * U;
-  const int r0 = kInter ? 0 : c * p.rows_per_split;
-  float M, L, O;   // valid in threads tid < kD
-  scan_fold<NW, U, D, kInter>(p, p.q, h, r0,
-                              kInter ? interleaved_rows(p.seqlen, kBlock, splits, c)
-                                     : min(p.seqlen - r0, p.rows_per_split),
-                              slds, M, L, O, c);
   if (c != merger) {
     // This split's partial, published as tagged words.
     float2* slot = head_slots + (long long)c * kXSlotWords;
@@ -790,7 +809,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_xmerge_kernel(AttnPa
       if (!((all >> cc) & 1ull)) continue;
       const int rr = kInter ? 0 : cc * p.rows_per_split;
       float Mc, Lc, Oc;
-      scan_fold<NW, U, D, kInter>(p, p.q, h, rr,
+      scan_fold_q<NW, U, D, kInter>(p, qv, h, rr,
                                   kInter ? interleaved_rows(p.seqlen, kBlock, splits, cc)
                                          : min(p.seqlen - rr, p.rows_per_split),
                                   slds, Mc, Lc, Oc, cc);
@@ -812,6 +831,29 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_xmerge_kernel(AttnPa
     if (rescanned)
       __hip_atomic_fetch_add(st + kXStatRescans, rescanned, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+}
+
+// SMAX: a bound on p.splits (16, 32 or 64): the slots each merging wave reads.
+// NW scanning waves (4 or 8); kInter: interleaved blocks of NW * 4 * U rows.
+template <int U, int SMAX, int D = 1, int NW = 4, bool kInter = false>
+__global__ __launch_bounds__(NW * 64) void decode_attention_xmerge_kernel(AttnParams p) {
+  static_assert(SMAX % 4 == 0 && SMAX <= kXMaxSplits, "SMAX: a multiple of 4, at most the slot count");
+  static_assert(NW == 4 || NW == 8, "four or eight waves scan; waves 0 and 1 hold the 128 dims");
+  __shared__ ScanLds<NW> slds;
+  __shared__ unsigned long long s_need[2];   // splits to scan again, per merging wave
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.x % p.num_heads;
+  const int c = blockIdx.x / p.num_heads;
+  const int splits = p.splits;
+  constexpr int kBlock = NW * 4 * U;
+  const int r0 = kInter ? 0 : c * p.rows_per_split;
+  const f16x8 qv = *reinterpret_cast<const f16x8*>(p.q + h * kD + (lane & 15) * 8);
+  float M, L, O;   // valid in threads tid < kD
+  scan_fold_q<NW, U, D, kInter>(p, qv, h, r0,
+                                kInter ? interleaved_rows(p.seqlen, kBlock, splits, c)
+                                       : min(p.seqlen - r0, p.rows_per_split),
+                                slds, M, L, O, c);
+  xmerge_finish<U, SMAX, D, NW, kInter>(p, h, c, qv, M, L, O, slds, s_need);
 }
 
 // Stage 2 of the two-launch path for at most SMAX splits per head: merge_fold's
@@ -844,6 +886,211 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_dim_kern
   if (wave == 0) merge_weights<SMAX>(ml.x, ml.y, lane, splits, s_w, s_l);
   __syncthreads();
   fold_per_dim<SMAX>(s_w, s_l, s_o, splits, reinterpret_cast<_Float16*>(p.out) + h * kD);
+}
+
+// ---------------------------------------------------------------------------
+// The attention front end and attention in one launch (the decode step's
+// qwen_infer.cu:626-678 chain: rmsnorm, QKV hgemv, bias, RoPE + cache append,
+// then Flash-Decoding over pos + 1 rows), for in-kernel-merge split plans.
+//
+// Workgroup w is first a producer -- qkv_front_kernel's work for four
+// rotation pairs of one head -- then a split workgroup of the attention plan
+// (split c = w / H of head w % H).  With dispatch round-robin over the 8 XCDs
+// (workgroup w on XCD w mod 8, probed at context creation) and H a multiple
+// of 8, producer w takes head (w mod 8) + 8 ((w / 8) / 16), so head h's 16
+// producers run on the XCD of its splits: every split reads its head's rotated
+// Q, and the split holding the appended row that row's rotated K and V, from
+// (value, tag) words the producers wrote into that XCD's L2 (as the in-kernel
+// merge hands over partials).  No cache row this call writes is read from the
+// cache: the appended row's loaded lanes are replaced by the tagged values,
+// which are the values the producers store there, so each split's first load
+// round of K and V is issued before its front-end work and overlaps it.  The
+// arithmetic is qkv_front_kernel's and the attention plan's, so every output
+// (qkv, the cache row, out) has the bits of the two launches.  A split that
+// still sees stale words after kFrontPolls reads (a producer ran on another
+// XCD) computes its head's front end itself, in the same arithmetic; the test
+// hook p.force_front_local makes every split do so.
+// ---------------------------------------------------------------------------
+constexpr int kFrontPolls = 1 << 14;
+
+// Replaces the appended row's K and V in tile blk (lanes whose loaded row --
+// clamped to nrows - 1 -- is row `pos` of the layer).
+template <int U>
+__device__ __forceinline__ void patch_tile(KvTile<U>& tl, int blk, int nrows, int g, int r0, int pos,
+                                           const f16x8 kpos, const f16x8 vpos) {
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const bool hit = r0 + min(blk + 4 * u + g, nrows - 1) == pos;
+    tl.k[u] = hit ? kpos : tl.k[u];
+    tl.v[u] = hit ? vpos : tl.v[u];
+  }
+}
+
+__device__ __forceinline__ bool tags_ok(const f32x4 (&a)[4], unsigned tag) {
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) ok = ok && tag_ok(a[k][1], tag) && tag_ok(a[k][3], tag);
+  return ok;
+}
+
+__device__ __forceinline__ f16x8 tagged_values(const f32x4 (&a)[4]) {
+  f16x8 v;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[2 * k] = (_Float16)a[k][0];
+    v[2 * k + 1] = (_Float16)a[k][2];
+  }
+  return v;
+}
+
+template <int NJ, bool kBiasWords, int U, int SMAX, int D>
+__global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, AttnParams p) {
+  constexpr int NW = 4;
+  constexpr int kStep = NW * 4 * U;
+  __shared__ ScanLds<NW> slds;
+  __shared__ unsigned long long s_need[2];
+  __shared__ float s_local[3][kD];   // a split's own front end for its head (fallback)
+  __shared__ int s_flag;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4;
+  const int t = lane & 15;
+  const int H = p.num_heads;
+  const int w = blockIdx.x;
+  const float tagf = __uint_as_float(p.tag);
+  const int pos = p.seqlen - 1;
+  if (tid == 0) s_flag = 0;
+
+  // Attention role: split c of head ha; its first load round (rows below pos
+  // are not written by this call) goes out before the front-end work.
+  const bool att = w < p.splits * H;
+  const int ha = w % H, c = w / H;
+  const int r0 = c * p.rows_per_split;
+  const int nrows = att ? min(p.seqlen - r0, p.rows_per_split) : 0;
+  const bool has_pos = r0 + nrows - 1 == pos;              // the head's last split
+  const long long off = (long long)ha * p.head_stride + (long long)r0 * p.row_stride;
+  const char* kbase = reinterpret_cast<const char*>(p.k + off);
+  const char* vbase = reinterpret_cast<const char*>(p.v + off);
+  const unsigned row_bytes = (unsigned)(p.row_stride * 2);
+  const int blk0 = wave * 4 * U;
+  KvTile<U> tl[D];
+  if (att && blk0 < nrows) {
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      if (d == 0 || blk0 + d * kStep < nrows) load_tile<U>(tl[d], kbase, vbase, row_bytes, blk0 + d * kStep, nrows, g, t);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Producer role: four rotation pairs of head hp, then their tagged words.
+  if (w < H * 16) {
+    const int j = w >> 3;
+    const int hp = (w & 7) + 8 * (j >> 4);
+    const int i = 4 * (j & 15) + wave;
+    const FrontPair o = qkv_front_pair<NJ, kBiasWords>(f, hp, i, lane);
+    if (lane == 0) {
+      float2* ft = p.ftag + (long long)hp * 3 * kD;
+      ft[i] = float2{(float)o.q1, tagf};
+      ft[i + 64] = float2{(float)o.q2, tagf};
+      ft[kD + i] = float2{(float)o.kr1, tagf};
+      ft[kD + i + 64] = float2{(float)o.kr2, tagf};
+      ft[2 * kD + i] = float2{(float)o.v1, tagf};
+      ft[2 * kD + i + 64] = float2{(float)o.v2, tagf};
+    }
+  }
+  if (!att) return;
+
+  // This lane's Q chunk (dims 8t .. 8t + 7) and, in the split holding the
+  // appended row, that row's K and V chunks, from the tagged words.
+  f16x8 qv = {}, kpos = {}, vpos = {};
+  bool timed_out = false;
+  {
+    const f32x4* fq = reinterpret_cast<const f32x4*>(p.ftag + (long long)ha * 3 * kD + 8 * t);
+    const f32x4* fk = fq + kD / 2;
+    const f32x4* fvv = fq + kD;
+    for (int poll = 0;; ++poll) {
+      // The loop stores nothing, so without a compiler barrier the Q loads
+      // would be hoisted out of it and read once.
+      __asm__ volatile("" ::: "memory");
+      f32x4 a[4], b[4], e[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) a[k] = __builtin_nontemporal_load(fq + k);
+      if (has_pos) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          b[k] = __builtin_nontemporal_load(fk + k);
+          e[k] = __builtin_nontemporal_load(fvv + k);
+        }
+      }
+      bool ok = tags_ok(a, p.tag);
+      if (has_pos) ok = ok && tags_ok(b, p.tag) && tags_ok(e, p.tag);
+      if (!__builtin_amdgcn_ballot_w64(!ok) && !p.force_front_local) {
+        qv = tagged_values(a);
+        if (has_pos) {
+          kpos = tagged_values(b);
+          vpos = tagged_values(e);
+        }
+        break;
+      }
+      if (poll >= kFrontPolls || p.force_front_local) {
+        timed_out = true;
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  if (timed_out && lane == 0) s_flag = 1;
+  __syncthreads();
+  if (s_flag && tid == 0 && !p.force_front_local)   // a miss, counted (the hook's are not)
+    __hip_atomic_fetch_add(p.xcnt + ha * kXCounterStride + kXStatFrontMisses, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  if (s_flag) {
+    // The head's front end here (every pair, no stores), wave w taking pairs
+    // w, w + 4, ...; the same arithmetic, so the same values.
+    for (int i = wave; i < 64; i += NW) {
+      const FrontPair o = qkv_front_pair<NJ, kBiasWords, false>(f, ha, i, lane);
+      if (lane == 0) {
+        s_local[0][i] = (float)o.q1;
+        s_local[0][i + 64] = (float)o.q2;
+        s_local[1][i] = (float)o.kr1;
+        s_local[1][i + 64] = (float)o.kr2;
+        s_local[2][i] = (float)o.v1;
+        s_local[2][i + 64] = (float)o.v2;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      qv[e] = (_Float16)s_local[0][8 * t + e];
+      kpos[e] = (_Float16)s_local[1][8 * t + e];
+      vpos[e] = (_Float16)s_local[2][8 * t + e];
+    }
+  }
+
+  // The split's scan: scan_rows' tiles in its order, the first round already
+  // loaded, the appended row's lanes replaced.
+  GroupState st;
+  init_state(st);
+  if (blk0 < nrows) {
+    for (int blk = blk0;; ) {
+      if (has_pos) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) patch_tile<U>(tl[d], blk + d * kStep, nrows, g, r0, pos, kpos, vpos);
+      }
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+        if (d == 0 || blk + d * kStep < nrows) consume_tile<U>(st, tl[d], blk + d * kStep, nrows, g, qv, p.scale_log2);
+      blk += kStep * D;
+      if (blk >= nrows) break;
+#pragma unroll
+      for (int d = 0; d < D; ++d)
+        if (d == 0 || blk + d * kStep < nrows) load_tile<U>(tl[d], kbase, vbase, row_bytes, blk + d * kStep, nrows, g, t);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  float M, L, O;
+  fold_waves<NW>(st, slds, M, L, O);
+  xmerge_finish<U, SMAX, D, NW, false>(p, ha, c, qv, M, L, O, slds, s_need);
 }
 
 }  // namespace
@@ -988,6 +1235,42 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
       hipLaunchKernelGGL(decode_attention_merge_dim_kernel<64>, grid, block, 0, stream, p);
     else
       hipLaunchKernelGGL(decode_attention_merge_kernel<false>, grid, block, 0, stream, p);
+  }
+  return hipGetLastError();
+}
+
+template <int NJ, bool kBiasWords, int SMAX>
+static void launch_qkv_attention_t(const QkvFrontParams& f, const AttnParams& p, const AttnPlan& plan,
+                                   dim3 grid, hipStream_t stream) {
+  if (plan.rows_per_tile == 4) {
+    if (plan.depth == 2)
+      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 4, SMAX, 2>), grid, dim3(256), 0, stream, f, p);
+    else
+      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 4, SMAX, 1>), grid, dim3(256), 0, stream, f, p);
+  } else {
+    if (plan.depth == 2)
+      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 2, SMAX, 2>), grid, dim3(256), 0, stream, f, p);
+    else
+      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 2, SMAX, 1>), grid, dim3(256), 0, stream, f, p);
+  }
+}
+
+hipError_t launch_qkv_attention(const QkvFrontParams& f, const AttnParams& p, const AttnPlan& plan,
+                                hipStream_t stream) {
+  const int H = p.num_heads;
+  if (!plan.xmerge || plan.variant != 1 || plan.waves != 4 || plan.block_rows || !p.xpart ||
+      !p.xcnt || !p.ftag || (H != 8 && H != 16) || f.num_heads != H || f.pos != p.seqlen - 1 ||
+      (plan.depth != 1 && plan.depth != 2) || p.splits > (H == 16 ? 16 : 32) ||
+      std::max(H * 16, p.splits * H) > p.num_cus)
+    return hipErrorInvalidValue;
+  const dim3 grid(std::max(H * 16, p.splits * H));
+  const bool words = (reinterpret_cast<uintptr_t>(f.bias) & 3u) == 0;
+  if (H == 16) {
+    if (words) launch_qkv_attention_t<4, true, 16>(f, p, plan, grid, stream);
+    else launch_qkv_attention_t<4, false, 16>(f, p, plan, grid, stream);
+  } else {
+    if (words) launch_qkv_attention_t<2, true, 32>(f, p, plan, grid, stream);
+    else launch_qkv_attention_t<2, false, 32>(f, p, plan, grid, stream);
   }
   return hipGetLastError();
 }

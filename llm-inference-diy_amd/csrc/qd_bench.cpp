@@ -65,8 +65,9 @@ int qd_bench_decode_step(qd_ctx* ctx, uint16_t* qkv, const uint16_t* bias, uint1
 }
 
 // Config-4 loop: per layer, qd_qkv_proj_rope_cache (GEMV [3*hid][hid] + bias +
-// RoPE + append at pos) and, when with_attention, qd_decode_attention over
-// pos + 1 rows.  Layer l's buffers sit at the given strides from the bases.
+// RoPE + append at pos) and, with with_attention 1, qd_decode_attention over
+// pos + 1 rows; with with_attention 2, both in qd_qkv_proj_rope_cache_attention.
+// Layer l's buffers sit at the given strides from the bases.
 int qd_bench_attn_front(qd_ctx* ctx, const uint16_t* x, const uint16_t* w_qkv, const uint16_t* bias,
                         uint16_t* qkv, uint16_t* k, uint16_t* v, uint16_t* out,
                         long long w_layer_stride, long long kv_layer_stride, int n_layers, int pos,
@@ -79,9 +80,18 @@ int qd_bench_attn_front(qd_ctx* ctx, const uint16_t* x, const uint16_t* w_qkv, c
     uint16_t* ql = qkv + layer * 3 * hid;
     uint16_t* kl = k + layer * kv_layer_stride;
     uint16_t* vl = v + layer * kv_layer_stride;
-    int rc = qd_qkv_proj_rope_cache(ctx, x + layer * hid, nullptr, 1e-6f, w_qkv + layer * w_layer_stride,
-                                    bias + layer * 3 * hid, ql, kl, vl, pos, max_seqlen, num_heads,
-                                    QD_HEAD_DIM, stream);
+    int rc;
+    if (with_attention == 2) {
+      rc = qd_qkv_proj_rope_cache_attention(ctx, x + layer * hid, nullptr, 1e-6f,
+                                            w_qkv + layer * w_layer_stride, bias + layer * 3 * hid, ql,
+                                            kl, vl, out + layer * hid, pos, max_seqlen, num_heads,
+                                            QD_HEAD_DIM, stream);
+      if (rc != QD_OK) return rc;
+      continue;
+    }
+    rc = qd_qkv_proj_rope_cache(ctx, x + layer * hid, nullptr, 1e-6f, w_qkv + layer * w_layer_stride,
+                                bias + layer * 3 * hid, ql, kl, vl, pos, max_seqlen, num_heads,
+                                QD_HEAD_DIM, stream);
     if (rc != QD_OK) return rc;
     if (with_attention) {
       rc = qd_decode_attention(ctx, ql, kl, vl, out + layer * hid, pos + 1, num_heads, QD_HEAD_DIM,

@@ -230,6 +230,8 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.recompute_mask = ctx->recompute_mask;
   p.count_merges = ctx->count_merges;
   p.block_rows = plan.block_rows;
+  p.ftag = ctx->ftag;
+  p.force_front_local = ctx->force_front_local;
   return p;
 }
 
@@ -266,24 +268,32 @@ qd::AttnPlan finish_plan(const qd_ctx* ctx, const qd::AttnPlan& plan_in, int seq
   return plan;
 }
 
+// A fresh tag for a call that merges in the kernel (and its arrival counters'
+// base); tag 0 is never used, and after 2^32 calls, once the tags wrap, the
+// slots and the fused front end's words are cleared so that no stale word can
+// carry the tag of the call that reads it.
+int next_xmerge_tag(qd_ctx* ctx, qd::AttnParams& p, hipStream_t stream) {
+  if (++ctx->xtag == 0u) {
+    hipError_t e = hipMemsetAsync(ctx->xpart, 0,
+                                  (size_t)ctx->cfg.num_heads * qd::kXMaxSplits * qd::kXSlotBytes, stream);
+    if (e == hipSuccess)
+      e = hipMemsetAsync(ctx->ftag, 0, (size_t)ctx->cfg.num_heads * 3 * 128 * sizeof(float2), stream);
+    if (e != hipSuccess) return hip_fail(e, "clearing the in-kernel merge slots");
+    ctx->xtag = 1u;
+  }
+  p.tag = ctx->xtag;
+  p.cnt_base = ctx->xcnt_sum;
+  return QD_OK;
+}
+
 int run_attention(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                   uint16_t* out, int seqlen, const qd::AttnPlan& plan_in, hipStream_t stream,
                   int stages = qd::kStageScan | qd::kStageMerge) {
   const qd::AttnPlan plan = finish_plan(ctx, plan_in, seqlen);
   qd::AttnParams p = make_params(ctx, q, k, v, out, seqlen, plan);
   if (plan.xmerge && (stages & qd::kStageScan)) {
-    // A fresh tag per call; tag 0 is never used, and after 2^32 calls, once
-    // the tags wrap, the slots are cleared so that no stale word can carry the
-    // tag of the call that reads it.
-    if (++ctx->xtag == 0u) {
-      const hipError_t e = hipMemsetAsync(ctx->xpart, 0,
-                                          (size_t)ctx->cfg.num_heads * qd::kXMaxSplits * qd::kXSlotBytes,
-                                          stream);
-      if (e != hipSuccess) return hip_fail(e, "clearing the in-kernel merge slots");
-      ctx->xtag = 1u;
-    }
-    p.tag = ctx->xtag;
-    p.cnt_base = ctx->xcnt_sum;
+    const int rc = next_xmerge_tag(ctx, p, stream);
+    if (rc != QD_OK) return rc;
   }
   hipError_t e = qd::launch_decode_attention(p, plan, stream, stages);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
@@ -381,6 +391,15 @@ int attention_prefill_mfma(qd_ctx* ctx, const uint16_t* q, long long q_stride, c
 
 }  // namespace qd
 
+namespace {
+// The checks and parameters of qd_qkv_proj_rope_cache (QD_OK, or the error
+// with its message).
+int front_params(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_w, float eps,
+                 const uint16_t* w_qkv, const uint16_t* qkv_bias, uint16_t* qkv, uint16_t* k_layer,
+                 uint16_t* v_layer, int pos, int max_seqlen, int num_heads, int head_dim,
+                 qd::QkvFrontParams& p);
+}  // namespace
+
 extern "C" {
 
 int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
@@ -450,12 +469,15 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   // zeroed arrival counters; then the dispatch placement it is fast under.
   const size_t xpart_bytes = H * qd::kXMaxSplits * qd::kXSlotBytes;
   const size_t xcnt_bytes = H * qd::kXCounterStride * sizeof(unsigned);
+  const size_t ftag_bytes = H * 3 * 128 * sizeof(float2);
   if ((e = hipMalloc(&ctx->xpart, xpart_bytes)) != hipSuccess ||
-      (e = hipMalloc(&ctx->xcnt, xcnt_bytes)) != hipSuccess) {
+      (e = hipMalloc(&ctx->xcnt, xcnt_bytes)) != hipSuccess ||
+      (e = hipMalloc(&ctx->ftag, ftag_bytes)) != hipSuccess) {
     int code = hip_fail(e, "hipMalloc of the in-kernel merge scratch");
     return cleanup(code == QD_EHIP ? QD_ENOMEM : code);
   }
-  if ((e = hipMemset(ctx->xcnt, 0, xcnt_bytes)) != hipSuccess)
+  if ((e = hipMemset(ctx->xcnt, 0, xcnt_bytes)) != hipSuccess ||
+      (e = hipMemset(ctx->ftag, 0, ftag_bytes)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMemset of the merge counters"));
   // Which XCD each workgroup runs on, probed into the slot area (cleared
   // afterwards).  Round-robin with period n (workgroup i on XCD (k + i) mod n
@@ -480,6 +502,7 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   ctx->count_merges = 0;
   ctx->scan_depth = 0;
   ctx->shape_waves = ctx->shape_tile = ctx->shape_inter = 0;
+  ctx->force_front_local = 0;
   *out_ctx = ctx;
   return QD_OK;
 }
@@ -496,6 +519,7 @@ int qd_ctx_destroy(qd_ctx* ctx) {
   if (ctx->pf_part_ml) (void)hipFree(ctx->pf_part_ml);
   if (ctx->xpart) (void)hipFree(ctx->xpart);
   if (ctx->xcnt) (void)hipFree(ctx->xcnt);
+  if (ctx->ftag) (void)hipFree(ctx->ftag);
   if (switch_dev) (void)hipSetDevice(dev);
   delete ctx;
   return QD_OK;
@@ -536,6 +560,72 @@ int qd_qkv_proj_rope_cache(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_
                            const uint16_t* w_qkv, const uint16_t* qkv_bias, uint16_t* qkv,
                            uint16_t* k_layer, uint16_t* v_layer, int pos, int max_seqlen,
                            int num_heads, int head_dim, hipStream_t stream) {
+  qd::QkvFrontParams p;
+  const int rc = front_params(ctx, x, norm_w, eps, w_qkv, qkv_bias, qkv, k_layer, v_layer, pos,
+                              max_seqlen, num_heads, head_dim, p);
+  if (rc != QD_OK) return rc;
+  hipError_t e = qd::launch_qkv_front(p, stream);
+  if (e != hipSuccess) return hip_fail(e, "qkv_proj_rope_cache launch");
+  return QD_OK;
+}
+
+constexpr int kFrontFusedMaxRows = 512;
+
+int qd_qkv_proj_rope_cache_attention(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_w,
+                                     float eps, const uint16_t* w_qkv, const uint16_t* qkv_bias,
+                                     uint16_t* qkv, uint16_t* k_layer, uint16_t* v_layer,
+                                     uint16_t* out, int pos, int max_seqlen, int num_heads,
+                                     int head_dim, hipStream_t stream) {
+  qd::QkvFrontParams f;
+  int rc = front_params(ctx, x, norm_w, eps, w_qkv, qkv_bias, qkv, k_layer, v_layer, pos, max_seqlen,
+                        num_heads, head_dim, f);
+  if (rc != QD_OK) return rc;
+  rc = check_attention_args(ctx, qkv, k_layer, v_layer, out, pos + 1, num_heads, head_dim);
+  if (rc != QD_OK) return rc;
+  const int hidden = num_heads * QD_HEAD_DIM;
+  if (qd::overlaps(out, (size_t)hidden * 2, x, (size_t)hidden * 2) ||
+      qd::overlaps(out, (size_t)hidden * 2, w_qkv, (size_t)3 * hidden * hidden * 2))
+    return fail(QD_EINVAL, "out overlaps x or w_qkv");
+  const int seqlen = pos + 1;
+  const qd::AttnPlan plan = finish_plan(ctx, plan_auto(ctx, seqlen), seqlen);
+  // One launch where the plan merges in the kernel with one workgroup per CU,
+  // up to kFrontFusedMaxRows rows (measured on MI355X at 16 heads: 10.98 us
+  // against 11.27 us for the two launches at 256 rows, but 12.47 against 12.29
+  // at 1024 and 14.31 against 13.95 at 2048, where each split's scan waits
+  // for its head's whole front end), and with out apart from qkv (whose rows
+  // the producers store while splits finish); otherwise the two launches,
+  // with the same outputs.
+  const bool fused = seqlen <= kFrontFusedMaxRows && plan.variant == 1 && plan.xmerge && !plan.block_rows &&
+                     (num_heads == 8 || num_heads == 16) &&
+                     std::max(num_heads * 16, plan.splits * num_heads) <= ctx->num_cus &&
+                     !qd::overlaps(out, (size_t)hidden * 2, qkv, (size_t)3 * hidden * 2);
+  if (!fused) {
+    hipError_t e = qd::launch_qkv_front(f, stream);
+    if (e != hipSuccess) return hip_fail(e, "qkv_proj_rope_cache launch");
+    return run_attention(ctx, qkv, k_layer, v_layer, out, seqlen, plan_auto(ctx, seqlen), stream);
+  }
+  qd::AttnParams p = make_params(ctx, qkv, k_layer, v_layer, out, seqlen, plan);
+  rc = next_xmerge_tag(ctx, p, stream);
+  if (rc != QD_OK) return rc;
+  const hipError_t e = qd::launch_qkv_attention(f, p, plan, stream);
+  if (e != hipSuccess) return hip_fail(e, "fused front end + attention launch");
+  ctx->xcnt_sum += (unsigned)(plan.splits - 1);
+  return QD_OK;
+}
+
+int qd_ctx_set_front_local(qd_ctx* ctx, int on) {
+  if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
+  ctx->force_front_local = on != 0;
+  return QD_OK;
+}
+
+}  // extern "C"
+
+namespace {
+int front_params(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_w, float eps,
+                 const uint16_t* w_qkv, const uint16_t* qkv_bias, uint16_t* qkv, uint16_t* k_layer,
+                 uint16_t* v_layer, int pos, int max_seqlen, int num_heads, int head_dim,
+                 qd::QkvFrontParams& p) {
   if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
   if (!x || !w_qkv || !qkv || !k_layer || !v_layer)
     return fail(QD_EINVAL, "x, w_qkv, qkv, k_layer and v_layer must be non-NULL");
@@ -562,7 +652,6 @@ int qd_qkv_proj_rope_cache(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != ctx->device)
     return fail(QD_EINVAL, "current device %d is not the context's device %d", dev, ctx->device);
-  qd::QkvFrontParams p;
   p.x = x;
   p.norm_w = norm_w;
   p.eps = eps;
@@ -576,10 +665,11 @@ int qd_qkv_proj_rope_cache(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_
   p.head_stride = ctx->cfg.kv_head_stride;
   p.pos = pos;
   p.num_heads = num_heads;
-  hipError_t e = qd::launch_qkv_front(p, stream);
-  if (e != hipSuccess) return hip_fail(e, "qkv_proj_rope_cache launch");
   return QD_OK;
 }
+}  // namespace
+
+extern "C" {
 
 int qd_decode_attention_plan(const qd_ctx* ctx, int seqlen, int* variant, int* num_splits) {
   if (!ctx || !variant || !num_splits) return fail(QD_EINVAL, "NULL argument");
@@ -671,6 +761,18 @@ int qd_ctx_xmerge_stats(const qd_ctx* ctx, unsigned long long* merges, unsigned 
   if (merges) *merges = t[0];
   if (reads) *reads = t[1];
   if (rescans) *rescans = t[2];
+  return QD_OK;
+}
+
+int qd_ctx_front_misses(const qd_ctx* ctx, unsigned long long* misses) {
+  if (!ctx || !misses) return fail(QD_EINVAL, "NULL argument");
+  const int H = ctx->cfg.num_heads;
+  std::vector<unsigned> c((size_t)H * qd::kXCounterStride);
+  const hipError_t e = hipMemcpy(c.data(), ctx->xcnt, c.size() * sizeof(unsigned), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_fail(e, "hipMemcpy of the merge counters");
+  unsigned long long t = 0ull;
+  for (int h = 0; h < H; ++h) t += c[(size_t)h * qd::kXCounterStride + qd::kXStatFrontMisses];
+  *misses = t;
   return QD_OK;
 }
 

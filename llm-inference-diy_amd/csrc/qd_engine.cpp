@@ -226,12 +226,10 @@ int run_layers(qd_engine* e, int token, int pos) {
   const uint16_t* xin = e->w(e->lay.wte) + (long long)token * H;   // embedding row (:617)
   for (uint32_t l = 0; l < c.num_layers; ++l) {
     const LayerOff& f = e->lay.layers[l];
-    int rc = qd_qkv_proj_rope_cache(e->attn, xin, e->w(f.ln_1), kEps, e->w(f.qkv_w), e->w(f.qkv_b),
-                                    e->qkv, e->kc(l), e->vc(l), pos, (int)c.max_seqlen, NH,
-                                    QD_HEAD_DIM, e->stream);
-    if (rc == QD_OK)
-      rc = qd_decode_attention(e->attn, e->qkv, e->kc(l), e->vc(l), e->attn_out, pos + 1, NH,
-                               QD_HEAD_DIM, e->stream);
+    // attention front end and attention (one launch where the plan allows)
+    int rc = qd_qkv_proj_rope_cache_attention(e->attn, xin, e->w(f.ln_1), kEps, e->w(f.qkv_w),
+                                              e->w(f.qkv_b), e->qkv, e->kc(l), e->vc(l), e->attn_out,
+                                              pos, (int)c.max_seqlen, NH, QD_HEAD_DIM, e->stream);
     if (rc == QD_OK) rc = qd_proj_residual(e->attn_out, e->w(f.proj_w), xin, e->x, H, H, e->stream);
     if (rc == QD_OK)
       rc = qd_ffn_up_swiglu(e->x, e->w(f.ln_2), kEps, e->w(f.w1), e->w(f.w2), e->act, H, I, e->stream);

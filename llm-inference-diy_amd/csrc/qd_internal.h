@@ -79,6 +79,12 @@ struct AttnParams {
   // splits in turn -- split c scans blocks c, c + splits, ... (see
   // interleaved_rows) -- so that at any time the grid reads one run of rows.
   int block_rows;
+  // Fused front end + attention (qkv_attention_kernel) only: tagged words
+  // [H][3][128] (value, tag) of each head's rotated Q, rotated K row and V row
+  // at position seqlen - 1, and a test hook (nonzero: every split computes its
+  // head's front end itself, as it does when the words stay invisible to it).
+  float2* ftag;
+  int force_front_local;
   // In-kernel merge (decode_attention_xmerge_kernel) only: tagged slots
   // [H][kXMaxSplits][kXSlotWords] (value, tag) words, per-head arrival
   // counters (kXCounterStride apart; every head's counter holds cnt_base when
@@ -96,13 +102,16 @@ struct AttnParams {
 // reads them in one batch of loads); counters 128 bytes apart.  Word 0 of a
 // head's counter block is its arrival counter; words kXStatMerges,
 // kXStatReads and kXStatRescans total its merges, reads of its slots and
-// splits scanned again (qd_ctx_xmerge_stats).
+// splits scanned again (qd_ctx_xmerge_stats); word kXStatFrontMisses the
+// splits of qkv_attention_kernel that computed the head's front end
+// themselves because the producers' words stayed invisible (qd_ctx_front_misses).
 constexpr int kXMaxSplits = 64;
 constexpr int kXCounterStride = 32;
 constexpr int kXSlotBytes = 1152;
 constexpr int kXStatMerges = 1;
 constexpr int kXStatReads = 2;
 constexpr int kXStatRescans = 3;
+constexpr int kXStatFrontMisses = 4;
 
 struct RopeParams {
   uint16_t* qkv;          // [3][H][128]
@@ -269,6 +278,13 @@ constexpr int kStageMerge = 2;
 // kStageScan launches it, kStageMerge alone launches nothing).
 hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hipStream_t stream,
                                    int stages = kStageScan | kStageMerge);
+// The attention front end (f: qkv_front_kernel's work) and an in-kernel-merge
+// split plan's attention over f.pos + 1 rows (p, plan) in one launch, with
+// the outputs of the two separate launches, bit for bit.  Requires plan.xmerge
+// with 4-wave contiguous splits, num_heads 8 or 16 and a grid of at most
+// num_cus workgroups (hipErrorInvalidValue otherwise, nothing launched).
+hipError_t launch_qkv_attention(const QkvFrontParams& f, const AttnParams& p, const AttnPlan& plan,
+                                hipStream_t stream);
 // Writes the XCD index (HW_REG_XCC_ID) of each of `grid` one-wave workgroups
 // to out[0..grid): the dispatch placement the in-kernel merge relies on for
 // speed (every split of a head on one XCD).
@@ -306,6 +322,7 @@ hipError_t launch_proj_residual(const ProjResidualParams& p, hipStream_t stream)
 hipError_t launch_ffn_up(const FfnUpParams& p, hipStream_t stream);
 // lm_head kernel, then the one-workgroup reduction of its keys into *token.
 hipError_t launch_lm_head_argmax(const LmHeadParams& p, int* token, hipStream_t stream);
+
 
 // Prefill kernels (qd_prefill.hip).  epi 0: Y = half(sum); epi 1: Y = half(R + half(sum)).
 hipError_t launch_rmsnorm_batched(const uint16_t* x, const uint16_t* w, float eps, uint16_t* xn,
@@ -381,6 +398,7 @@ struct qd_ctx {
   // test hook of AttnParams.
   float2* xpart;
   unsigned* xcnt;
+  float2* ftag;           // [H][3][128] tagged words of the fused front end + attention
   unsigned xtag;
   unsigned xcnt_sum;      // value of every head's arrival counter between calls
   int num_xcd;
@@ -393,4 +411,5 @@ struct qd_ctx {
   int shape_waves;
   int shape_tile;
   int shape_inter;
+  int force_front_local;  // qd_ctx_set_front_local
 };

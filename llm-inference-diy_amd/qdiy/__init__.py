@@ -33,7 +33,7 @@ EXPORTS = (
     # qdiy/bench.h
     "qd_decode_attention_stage", "qd_ctx_set_merge", "qd_ctx_set_recompute_mask",
     "qd_ctx_xcd_period", "qd_xcd_placement", "qd_ctx_xmerge_stats", "qd_ctx_count_xmerges", "qd_ctx_set_scan_depth",
-    "qd_ctx_set_split_shape",
+    "qd_ctx_set_split_shape", "qd_ctx_set_front_local", "qd_ctx_front_misses", "qd_qkv_proj_rope_cache_attention",
     "qd_max_splits", "qd_last_error", "qd_version",
     # qdiy/decode.h
     "qd_proj_residual", "qd_ffn_up_swiglu", "qd_lm_head_workspace_bytes", "qd_lm_head_argmax",
@@ -106,6 +106,8 @@ def load() -> ctypes.CDLL:
     L.qd_qkv_bias_rope_cache.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
     L.qd_qkv_proj_rope_cache.argtypes = [vp, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp, i, i, i,
                                          i, vp]
+    L.qd_qkv_proj_rope_cache_attention.argtypes = [vp, vp, vp, ctypes.c_float, vp, vp, vp, vp, vp, vp,
+                                                   i, i, i, i, vp]
     L.qd_decode_attention.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     L.qd_decode_attention_fused.argtypes = [vp, vp, vp, vp, vp, i, i, i, vp]
     L.qd_decode_attention_split.argtypes = [vp, vp, vp, vp, vp, i, i, i, i, vp]
@@ -119,6 +121,8 @@ def load() -> ctypes.CDLL:
     L.qd_ctx_count_xmerges.argtypes = [vp, i]
     L.qd_ctx_set_scan_depth.argtypes = [vp, i]
     L.qd_ctx_set_split_shape.argtypes = [vp, i, i, i]
+    L.qd_ctx_set_front_local.argtypes = [vp, i]
+    L.qd_ctx_front_misses.argtypes = [vp, ull_p]
     L.qd_xcd_placement.argtypes = [ctypes.POINTER(ctypes.c_uint), i]
     L.qd_decode_attention_plan.argtypes = [vp, i, ctypes.POINTER(i), ctypes.POINTER(i)]
     L.qd_decode_attention_plan_detail.argtypes = [vp, i, i, i, ctypes.POINTER(AttnPlan)]
@@ -332,6 +336,45 @@ class Context:
                                              _ptr(v_layer, "v_layer", False), pos, max_seqlen, H,
                                              HEAD_DIM, _stream(stream)))
 
+
+    def qkv_proj_rope_cache_attention(self, x: torch.Tensor, norm_w, w_qkv: torch.Tensor, bias,
+                                      qkv: torch.Tensor, k_layer: torch.Tensor,
+                                      v_layer: torch.Tensor, out: torch.Tensor, pos: int,
+                                      eps: float = 1e-6, max_seqlen: int | None = None,
+                                      stream=None) -> None:
+        """qkv_proj_rope_cache at pos, then decode_attention over pos + 1 rows into out
+        (one launch where the plan allows: qd_qkv_proj_rope_cache_attention)."""
+        H = self.num_heads
+        hid = H * HEAD_DIM
+        if x.numel() < hid or qkv.numel() < 3 * hid or w_qkv.numel() < 3 * hid * hid:
+            raise ValueError("x needs H*128, qkv 3*H*128 and w_qkv 3*H*128*H*128 elements")
+        if norm_w is not None and norm_w.numel() < hid:
+            raise ValueError("norm_w needs H*128 elements")
+        if bias is not None and bias.numel() < 3 * hid:
+            raise ValueError("bias needs 3*H*128 elements")
+        if out.numel() < hid:
+            raise ValueError("out needs H*128 elements")
+        if max_seqlen is None:
+            max_seqlen = self.max_seqlen
+        if 0 <= pos < max_seqlen:
+            self._check_cache(k_layer, "k_layer", pos + 1)
+            self._check_cache(v_layer, "v_layer", pos + 1)
+        opt = lambda t, n: None if t is None else _ptr(t, n)
+        _check(load().qd_qkv_proj_rope_cache_attention(
+            self._h, _ptr(x, "x"), opt(norm_w, "norm_w"), eps, _ptr(w_qkv, "w_qkv"), opt(bias, "bias"),
+            _ptr(qkv, "qkv"), _ptr(k_layer, "k_layer", False), _ptr(v_layer, "v_layer", False),
+            _ptr(out, "out"), pos, max_seqlen, H, HEAD_DIM, _stream(stream)))
+
+    def set_front_local(self, on: bool) -> None:
+        """qd_ctx_set_front_local: every split computes its head's front end itself."""
+        _check(load().qd_ctx_set_front_local(self._h, 1 if on else 0))
+
+    def front_misses(self) -> int:
+        """qd_ctx_front_misses: split workgroups of the one-launch front end +
+        attention that computed their head's front end themselves (not forced)."""
+        n = ctypes.c_ulonglong(0)
+        _check(load().qd_ctx_front_misses(self._h, ctypes.byref(n)))
+        return n.value
 
     def qkv_proj_rope_cache(self, x: torch.Tensor, norm_w, w_qkv: torch.Tensor, bias,
                             qkv: torch.Tensor, k_layer: torch.Tensor, v_layer: torch.Tensor,
