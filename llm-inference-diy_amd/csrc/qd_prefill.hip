@@ -566,9 +566,12 @@ struct __align__(16) MmStage {
   uint16_t x[kMmTile * kMmK];
   uint16_t w[kMmTile * kMmK];
 };
-// rows r and r + 8 share banks (128-byte rows): (r / 2) % 8 gives the 16 rows
-// of one operand read 16 distinct (row parity, position) pairs
-__device__ __forceinline__ int mmswz(int r) { return (r >> 1) & 7; }
+// ds_read_b128 is served eight lanes at a time over 32 four-byte banks (128
+// bytes), and every 128-byte row starts on bank 0: r % 8 puts the eight rows of
+// one such group (lanes l % 16 = 8g .. 8g + 7 of an operand read) on distinct
+// 16-byte positions.  (The earlier (r / 2) % 8, right for 64 banks, left rows
+// 2i and 2i + 1 on the same banks.)
+__device__ __forceinline__ int mmswz(int r) { return r & 7; }
 
 template <int kEpi>
 __global__ __launch_bounds__(256) void gemm_nt_mfma_kernel(BatchedGemvParams p) {
@@ -1000,8 +1003,10 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring128_kernel(BatchedGemvPara
 // tokens (6 x 8 MFMA blocks, 192 accumulator registers): 37 B per clock from
 // L2 and ~110 from LDS at the matrix cores' rate.  K goes in tiles of 32
 // through a ring of 5 stages of 28 KB (W tile 192 x 64 B, then X tile 256 x
-// 64 B; chunk q of row r at q ^ ((r / 4) % 4), so the 16 rows of one fragment
-// read fall on distinct banks), 4 tiles in flight, filled by direct loads (7
+// 64 B; chunk q of row r at q ^ ((r / 2) % 4), so the eight rows that one
+// eight-lane group of a fragment read covers -- two per 128-byte bank line --
+// fall on distinct banks: no conflicts in rocprofv3's SQ_LDS_BANK_CONFLICT,
+// against 3.7 M cycles per launch with (r / 4) % 4), 4 tiles in flight, filled by direct loads (7
 // per thread per stage), the next tile's fragments read from LDS while the
 // matrix cores consume the current one's.  kEpi 0: half(sum); 1: half(R +
 // half(sum)); 3: joint gate/up, 96 outputs per workgroup (W tile rows 0..95
@@ -1018,7 +1023,7 @@ struct __align__(16) Ring2Stage {
   uint16_t w[kR2N * kR2K];
   uint16_t x[kR2T * kR2K];
 };
-__device__ __forceinline__ int r2swz(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int r2swz(int r) { return (r >> 1) & 3; }
 
 template <int kEpi>
 __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvParams p) {
