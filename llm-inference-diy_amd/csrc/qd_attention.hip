@@ -329,12 +329,50 @@ __device__ __forceinline__ void scan_fold_q(const AttnParams& p, const f16x8 qv,
   fold_waves<NW>(st, lds, M, L, O);
 }
 
+// scan_fold_q with Q read here, the fold written out (fold_waves' steps).
+// Spelled out rather than calling scan_fold_q: built that way the split scan
+// kernel at L=8192 compiled to a slightly different schedule and ran 0.6 us
+// slower per launch (12.8 against 12.2 us, the same bits).
 template <int NW, int U, int D = 1, bool kInter = false>
 __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q, int h, int r0,
                                           int nrows, ScanLds<NW>& lds, float& M, float& L,
                                           float& O, int c = 0) {
-  const f16x8 qv = *reinterpret_cast<const f16x8*>(q + h * kD + (threadIdx.x & 15) * 8);
-  scan_fold_q<NW, U, D, kInter>(p, qv, h, r0, nrows, lds, M, L, O, c);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
+  const int g = lane >> 4;
+  const int t = lane & 15;
+  const f16x8 qv = *reinterpret_cast<const f16x8*>(q + h * kD + t * 8);
+  const long long off = h * p.head_stride + (long long)r0 * p.row_stride;
+  GroupState st;
+  init_state(st);
+  scan_rows<NW, U, D, kInter>(st, reinterpret_cast<const char*>(p.k + off),
+                              reinterpret_cast<const char*>(p.v + off), (unsigned)(p.row_stride * 2),
+                              nrows, wave, g, t, qv, p.scale_log2, c, p.splits);
+  wave_merge(st);
+  if (lane < 16) {
+    *reinterpret_cast<f32x4*>(&lds.so[wave][t * 8]) = f32x4{st.o[0], st.o[1], st.o[2], st.o[3]};
+    *reinterpret_cast<f32x4*>(&lds.so[wave][t * 8 + 4]) = f32x4{st.o[4], st.o[5], st.o[6], st.o[7]};
+    if (t == 0) {
+      lds.sm[wave] = st.m;
+      lds.sl[wave] = st.l;
+    }
+  }
+  __syncthreads();
+  M = -__builtin_inff();
+  L = 0.0f;
+  O = 0.0f;
+  if (tid < kD) {
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, lds.sm[w]);
+    const float base = safe_base(M);
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float wt = exp2_rep_nonpos(lds.sm[w] - base);
+      L = __builtin_fmaf(wt, lds.sl[w], L);
+      O = __builtin_fmaf(wt, lds.so[w][tid], O);
+    }
+  }
 }
 
 template <int NW>
@@ -909,7 +947,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_dim_kern
 // (qkv, the cache row, out) has the bits of the two launches.  A split that
 // still sees stale words after kFrontPolls reads (a producer ran on another
 // XCD) computes its head's front end itself, in the same arithmetic; the test
-// hook p.force_front_local makes every split do so.
+// hook fh.force_local makes every split do so.
 // ---------------------------------------------------------------------------
 constexpr int kFrontPolls = 1 << 14;
 
@@ -944,7 +982,7 @@ __device__ __forceinline__ f16x8 tagged_values(const f32x4 (&a)[4]) {
 }
 
 template <int NJ, bool kBiasWords, int U, int SMAX, int D>
-__global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, AttnParams p) {
+__global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, AttnParams p, FrontHandoff fh) {
   constexpr int NW = 4;
   constexpr int kStep = NW * 4 * U;
   __shared__ ScanLds<NW> slds;
@@ -989,7 +1027,7 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
     const int i = 4 * (j & 15) + wave;
     const FrontPair o = qkv_front_pair<NJ, kBiasWords>(f, hp, i, lane);
     if (lane == 0) {
-      float2* ft = p.ftag + (long long)hp * 3 * kD;
+      float2* ft = fh.ftag + (long long)hp * 3 * kD;
       ft[i] = float2{(float)o.q1, tagf};
       ft[i + 64] = float2{(float)o.q2, tagf};
       ft[kD + i] = float2{(float)o.kr1, tagf};
@@ -1005,7 +1043,7 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
   f16x8 qv = {}, kpos = {}, vpos = {};
   bool timed_out = false;
   {
-    const f32x4* fq = reinterpret_cast<const f32x4*>(p.ftag + (long long)ha * 3 * kD + 8 * t);
+    const f32x4* fq = reinterpret_cast<const f32x4*>(fh.ftag + (long long)ha * 3 * kD + 8 * t);
     const f32x4* fk = fq + kD / 2;
     const f32x4* fvv = fq + kD;
     for (int poll = 0;; ++poll) {
@@ -1024,7 +1062,7 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
       }
       bool ok = tags_ok(a, p.tag);
       if (has_pos) ok = ok && tags_ok(b, p.tag) && tags_ok(e, p.tag);
-      if (!__builtin_amdgcn_ballot_w64(!ok) && !p.force_front_local) {
+      if (!__builtin_amdgcn_ballot_w64(!ok) && !fh.force_local) {
         qv = tagged_values(a);
         if (has_pos) {
           kpos = tagged_values(b);
@@ -1032,7 +1070,7 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
         }
         break;
       }
-      if (poll >= kFrontPolls || p.force_front_local) {
+      if (poll >= kFrontPolls || fh.force_local) {
         timed_out = true;
         break;
       }
@@ -1041,7 +1079,7 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
   __syncthreads();
   if (timed_out && lane == 0) s_flag = 1;
   __syncthreads();
-  if (s_flag && tid == 0 && !p.force_front_local)   // a miss, counted (the hook's are not)
+  if (s_flag && tid == 0 && !fh.force_local)   // a miss, counted (the hook's are not)
     __hip_atomic_fetch_add(p.xcnt + ha * kXCounterStride + kXStatFrontMisses, 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
   if (s_flag) {
@@ -1240,37 +1278,39 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
 }
 
 template <int NJ, bool kBiasWords, int SMAX>
-static void launch_qkv_attention_t(const QkvFrontParams& f, const AttnParams& p, const AttnPlan& plan,
+static void launch_qkv_attention_t(const QkvFrontParams& f, const AttnParams& p, const FrontHandoff& fh,
+                                   const AttnPlan& plan,
                                    dim3 grid, hipStream_t stream) {
   if (plan.rows_per_tile == 4) {
     if (plan.depth == 2)
-      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 4, SMAX, 2>), grid, dim3(256), 0, stream, f, p);
+      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 4, SMAX, 2>), grid, dim3(256), 0, stream, f, p, fh);
     else
-      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 4, SMAX, 1>), grid, dim3(256), 0, stream, f, p);
+      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 4, SMAX, 1>), grid, dim3(256), 0, stream, f, p, fh);
   } else {
     if (plan.depth == 2)
-      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 2, SMAX, 2>), grid, dim3(256), 0, stream, f, p);
+      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 2, SMAX, 2>), grid, dim3(256), 0, stream, f, p, fh);
     else
-      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 2, SMAX, 1>), grid, dim3(256), 0, stream, f, p);
+      hipLaunchKernelGGL((qkv_attention_kernel<NJ, kBiasWords, 2, SMAX, 1>), grid, dim3(256), 0, stream, f, p, fh);
   }
 }
 
-hipError_t launch_qkv_attention(const QkvFrontParams& f, const AttnParams& p, const AttnPlan& plan,
+hipError_t launch_qkv_attention(const QkvFrontParams& f, const AttnParams& p, const FrontHandoff& fh,
+                                const AttnPlan& plan,
                                 hipStream_t stream) {
   const int H = p.num_heads;
   if (!plan.xmerge || plan.variant != 1 || plan.waves != 4 || plan.block_rows || !p.xpart ||
-      !p.xcnt || !p.ftag || (H != 8 && H != 16) || f.num_heads != H || f.pos != p.seqlen - 1 ||
+      !p.xcnt || !fh.ftag || (H != 8 && H != 16) || f.num_heads != H || f.pos != p.seqlen - 1 ||
       (plan.depth != 1 && plan.depth != 2) || p.splits > (H == 16 ? 16 : 32) ||
       std::max(H * 16, p.splits * H) > p.num_cus)
     return hipErrorInvalidValue;
   const dim3 grid(std::max(H * 16, p.splits * H));
   const bool words = (reinterpret_cast<uintptr_t>(f.bias) & 3u) == 0;
   if (H == 16) {
-    if (words) launch_qkv_attention_t<4, true, 16>(f, p, plan, grid, stream);
-    else launch_qkv_attention_t<4, false, 16>(f, p, plan, grid, stream);
+    if (words) launch_qkv_attention_t<4, true, 16>(f, p, fh, plan, grid, stream);
+    else launch_qkv_attention_t<4, false, 16>(f, p, fh, plan, grid, stream);
   } else {
-    if (words) launch_qkv_attention_t<2, true, 32>(f, p, plan, grid, stream);
-    else launch_qkv_attention_t<2, false, 32>(f, p, plan, grid, stream);
+    if (words) launch_qkv_attention_t<2, true, 32>(f, p, fh, plan, grid, stream);
+    else launch_qkv_attention_t<2, false, 32>(f, p, fh, plan, grid, stream);
   }
   return hipGetLastError();
 }

@@ -230,8 +230,6 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.recompute_mask = ctx->recompute_mask;
   p.count_merges = ctx->count_merges;
   p.block_rows = plan.block_rows;
-  p.ftag = ctx->ftag;
-  p.force_front_local = ctx->force_front_local;
   return p;
 }
 
@@ -470,12 +468,13 @@ int qd_ctx_create(const qd_cfg* cfg, qd_ctx** out_ctx) {
   const size_t xpart_bytes = H * qd::kXMaxSplits * qd::kXSlotBytes;
   const size_t xcnt_bytes = H * qd::kXCounterStride * sizeof(unsigned);
   const size_t ftag_bytes = H * 3 * 128 * sizeof(float2);
-  if ((e = hipMalloc(&ctx->xpart, xpart_bytes)) != hipSuccess ||
-      (e = hipMalloc(&ctx->xcnt, xcnt_bytes)) != hipSuccess ||
-      (e = hipMalloc(&ctx->ftag, ftag_bytes)) != hipSuccess) {
+  // The fused front end's tagged words follow the slots in their allocation.
+  if ((e = hipMalloc(&ctx->xpart, xpart_bytes + ftag_bytes)) != hipSuccess ||
+      (e = hipMalloc(&ctx->xcnt, xcnt_bytes)) != hipSuccess) {
     int code = hip_fail(e, "hipMalloc of the in-kernel merge scratch");
     return cleanup(code == QD_EHIP ? QD_ENOMEM : code);
   }
+  ctx->ftag = reinterpret_cast<float2*>(reinterpret_cast<char*>(ctx->xpart) + xpart_bytes);
   if ((e = hipMemset(ctx->xcnt, 0, xcnt_bytes)) != hipSuccess ||
       (e = hipMemset(ctx->ftag, 0, ftag_bytes)) != hipSuccess)
     return cleanup(hip_fail(e, "hipMemset of the merge counters"));
@@ -519,7 +518,6 @@ int qd_ctx_destroy(qd_ctx* ctx) {
   if (ctx->pf_part_ml) (void)hipFree(ctx->pf_part_ml);
   if (ctx->xpart) (void)hipFree(ctx->xpart);
   if (ctx->xcnt) (void)hipFree(ctx->xcnt);
-  if (ctx->ftag) (void)hipFree(ctx->ftag);
   if (switch_dev) (void)hipSetDevice(dev);
   delete ctx;
   return QD_OK;
@@ -607,7 +605,8 @@ int qd_qkv_proj_rope_cache_attention(qd_ctx* ctx, const uint16_t* x, const uint1
   qd::AttnParams p = make_params(ctx, qkv, k_layer, v_layer, out, seqlen, plan);
   rc = next_xmerge_tag(ctx, p, stream);
   if (rc != QD_OK) return rc;
-  const hipError_t e = qd::launch_qkv_attention(f, p, plan, stream);
+  const qd::FrontHandoff fh{ctx->ftag, ctx->force_front_local};
+  const hipError_t e = qd::launch_qkv_attention(f, p, fh, plan, stream);
   if (e != hipSuccess) return hip_fail(e, "fused front end + attention launch");
   ctx->xcnt_sum += (unsigned)(plan.splits - 1);
   return QD_OK;

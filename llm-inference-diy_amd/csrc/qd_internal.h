@@ -79,12 +79,6 @@ struct AttnParams {
   // splits in turn -- split c scans blocks c, c + splits, ... (see
   // interleaved_rows) -- so that at any time the grid reads one run of rows.
   int block_rows;
-  // Fused front end + attention (qkv_attention_kernel) only: tagged words
-  // [H][3][128] (value, tag) of each head's rotated Q, rotated K row and V row
-  // at position seqlen - 1, and a test hook (nonzero: every split computes its
-  // head's front end itself, as it does when the words stay invisible to it).
-  float2* ftag;
-  int force_front_local;
   // In-kernel merge (decode_attention_xmerge_kernel) only: tagged slots
   // [H][kXMaxSplits][kXSlotWords] (value, tag) words, per-head arrival
   // counters (kXCounterStride apart; every head's counter holds cnt_base when
@@ -283,7 +277,17 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
 // the outputs of the two separate launches, bit for bit.  Requires plan.xmerge
 // with 4-wave contiguous splits, num_heads 8 or 16 and a grid of at most
 // num_cus workgroups (hipErrorInvalidValue otherwise, nothing launched).
-hipError_t launch_qkv_attention(const QkvFrontParams& f, const AttnParams& p, const AttnPlan& plan,
+// Fused front end + attention (qkv_attention_kernel) only, kept out of
+// AttnParams, which every attention kernel takes: tagged words [H][3][128]
+// (value, tag) of each head's rotated Q, rotated K row and V row at position
+// seqlen - 1, and a test hook (nonzero: every split computes its head's front
+// end itself, as it does when the words stay invisible to it).
+struct FrontHandoff {
+  float2* ftag;
+  int force_local;
+};
+hipError_t launch_qkv_attention(const QkvFrontParams& f, const AttnParams& p, const FrontHandoff& fh,
+                                const AttnPlan& plan,
                                 hipStream_t stream);
 // Writes the XCD index (HW_REG_XCC_ID) of each of `grid` one-wave workgroups
 // to out[0..grid): the dispatch placement the in-kernel merge relies on for
