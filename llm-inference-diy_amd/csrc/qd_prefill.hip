@@ -750,7 +750,7 @@ constexpr int kGemmMaxSplits = 8;            // K slices of a split product
 // adjacent outputs of one token, stored as 8 bytes.  Four waves of 64 x 64
 // (4 x 4 MFMA blocks).  K goes in tiles of 64 through a ring of 5 LDS stages of 32 KB
 // (W tile then X tile, 128-byte rows with their 16-byte chunks swizzled by
-// (r / 2) % 8 as in gemm_nt_mfma_kernel) filled by direct loads
+// r % 8 as in gemm_nt_mfma_kernel) filled by direct loads
 // (global_load_lds_dwordx4, 8 per thread per stage), 4 tiles in flight
 // beyond the one being read: a register-staged version of this tile, with one
 // tile (~0.2 us of matrix-core work) in flight against an L2/MALL round trip
