@@ -691,8 +691,15 @@ def main() -> int:
             "achieved": round(head["scan_gbps"], 1), "peak": PEAK_GBPS, "unit": "GB/s",
             "frac": round(head["scan_gbps"] / PEAK_GBPS, 4),
             "traffic": traffic.get(HEADLINE_L, {}).get("scan_kernel_traffic_bytes"),
+            "traffic_source": (f"{os.path.relpath(traffic_file(HEADLINE_L), ROOT)}: rocprofv3 --pmc "
+                               f"FETCH_SIZE and WRITE_SIZE runs of bench.py --only scan, scaled by a "
+                               f"copy kernel's counts (not measured in this run)"),
             "algorithmic_bytes_per_launch": scan_bytes(HEADLINE_L),
             "launch_us": round(head["scan_us"], 3),
+            "launch_timing": ("scan-only launches back to back on the same rotated layers "
+                              "(qd_decode_attention_stage); inside the call, after each merge "
+                              "kernel, the same kernel runs ~0.7 us longer per launch in the "
+                              "committed kernel trace"),
             "call_frac": round(head["frac"], 4),
             "per_kernel_trace": "profiles/decode_attention_kernel_trace_L512_to_L32768.md"},
         "cpu_baseline": cpu,
