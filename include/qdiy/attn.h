@@ -145,16 +145,15 @@ int qd_decode_attention_split(qd_ctx* ctx, const uint16_t* q, const uint16_t* k_
  * (:631) -> RoPE + K/V append at pos (:634-642) -> Flash-Decoding over
  * pos + 1 rows (:646-678): qd_qkv_proj_rope_cache followed by
  * qd_decode_attention(q = qkv, seqlen = pos + 1), with those two calls'
- * outputs (qkv, the cache row at pos, out) bit for bit.  Up to 512 rows,
- * where the attention plan merges its splits inside the scan kernel with one
- * workgroup per CU (qd_attn_plan.merge_in_kernel; from 129 rows at 16 heads
- * on MI355X), num_heads is 8 or 16 and out is apart from qkv, it is one
- * launch (longer caches measured faster as two): each
+ * outputs (qkv, the cache row at pos, out) bit for bit.  Where the attention
+ * plan merges its splits inside the scan kernel with one workgroup per CU
+ * (qd_attn_plan.merge_in_kernel; 129 to 3072 rows at 16 heads on MI355X),
+ * num_heads is 8 or 16 and out is apart from qkv, it is one launch: each
  * workgroup computes four rotation pairs of the front end, then its split of
  * the attention, which reads its head's rotated Q (and the appended row's K
  * and V) from the producers of the same XCD without waiting for a kernel
- * boundary, its first K/V loads issued before its front-end work.  Elsewhere
- * it makes the two launches.  Arguments as the two calls; out must not
+ * boundary, its first K/V loads issued behind its front end's weight rows.
+ * Elsewhere it makes the two launches.  Arguments as the two calls; out must not
  * overlap x or w_qkv (QD_EINVAL). */
 int qd_qkv_proj_rope_cache_attention(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_w,
                                      float eps, const uint16_t* w_qkv, const uint16_t* qkv_bias,

@@ -942,8 +942,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_dim_kern
 // merge hands over partials).  No cache row this call writes is read from the
 // cache: the appended row's loaded lanes are replaced by the tagged values,
 // which are the values the producers store there, so each split's first load
-// round of K and V is issued before its front-end work and overlaps it.  The
-// arithmetic is qkv_front_kernel's and the attention plan's, so every output
+// round of K and V is issued with its front-end work (behind the weight rows)
+// and overlaps it.  The arithmetic is qkv_front_kernel's and the attention plan's, so every output
 // (qkv, the cache row, out) has the bits of the two launches.  A split that
 // still sees stale words after kFrontPolls reads (a producer ran on another
 // XCD) computes its head's front end itself, in the same arithmetic; the test
@@ -964,30 +964,13 @@ __device__ __forceinline__ void patch_tile(KvTile<U>& tl, int blk, int nrows, in
   }
 }
 
-__device__ __forceinline__ bool tags_ok(const f32x4 (&a)[4], unsigned tag) {
-  bool ok = true;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) ok = ok && tag_ok(a[k][1], tag) && tag_ok(a[k][3], tag);
-  return ok;
-}
-
-__device__ __forceinline__ f16x8 tagged_values(const f32x4 (&a)[4]) {
-  f16x8 v;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    v[2 * k] = (_Float16)a[k][0];
-    v[2 * k + 1] = (_Float16)a[k][2];
-  }
-  return v;
-}
-
 template <int NJ, bool kBiasWords, int U, int SMAX, int D>
 __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, AttnParams p, FrontHandoff fh) {
   constexpr int NW = 4;
   constexpr int kStep = NW * 4 * U;
   __shared__ ScanLds<NW> slds;
   __shared__ unsigned long long s_need[2];
-  __shared__ float s_local[3][kD];   // a split's own front end for its head (fallback)
+  __shared__ float s_local[3][kD];   // the head's rotated Q, K and V values for the waves
   __shared__ int s_flag;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1000,32 +983,40 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
   const int pos = p.seqlen - 1;
   if (tid == 0) s_flag = 0;
 
-  // Attention role: split c of head ha; its first load round (rows below pos
-  // are not written by this call) goes out before the front-end work.
+  // Attention role: split c of head ha.  Its first load round (rows below pos
+  // are not written by this call) goes out behind the producer's weight rows,
+  // so the front end's bytes are not queued behind the split's.
   const bool att = w < p.splits * H;
   const int ha = w % H, c = w / H;
   const int r0 = c * p.rows_per_split;
   const int nrows = att ? min(p.seqlen - r0, p.rows_per_split) : 0;
   const bool has_pos = r0 + nrows - 1 == pos;              // the head's last split
-  const long long off = (long long)ha * p.head_stride + (long long)r0 * p.row_stride;
+  const long long off = (long long)ha * p.head_stride + (long long)(att ? r0 : 0) * p.row_stride;
   const char* kbase = reinterpret_cast<const char*>(p.k + off);
   const char* vbase = reinterpret_cast<const char*>(p.v + off);
   const unsigned row_bytes = (unsigned)(p.row_stride * 2);
   const int blk0 = wave * 4 * U;
   KvTile<U> tl[D];
-  if (att && blk0 < nrows) {
+  // Every wave issues all D tiles, with rows clamped into its range (a
+  // workgroup without a split reads row 0 of head ha): loads on both sides of
+  // a branch would make the compiler's waits for the weight rows count only
+  // the loads of the shorter side, and so also wait for these.  Tiles past the
+  // range are not consumed.
+  auto first_round = [&]() {
 #pragma unroll
     for (int d = 0; d < D; ++d)
-      if (d == 0 || blk0 + d * kStep < nrows) load_tile<U>(tl[d], kbase, vbase, row_bytes, blk0 + d * kStep, nrows, g, t);
-  }
-  __builtin_amdgcn_sched_barrier(0);
+      load_tile<U>(tl[d], kbase, vbase, row_bytes, blk0 + d * kStep, max(nrows, 1), g, t);
+  };
 
   // Producer role: four rotation pairs of head hp, then their tagged words.
-  if (w < H * 16) {
+  if (w >= H * 16) {
+    first_round();
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
     const int j = w >> 3;
     const int hp = (w & 7) + 8 * (j >> 4);
     const int i = 4 * (j & 15) + wave;
-    const FrontPair o = qkv_front_pair<NJ, kBiasWords>(f, hp, i, lane);
+    const FrontPair o = qkv_front_pair<NJ, kBiasWords>(f, hp, i, lane, first_round);
     if (lane == 0) {
       float2* ft = fh.ftag + (long long)hp * 3 * kD;
       ft[i] = float2{(float)o.q1, tagf};
@@ -1038,46 +1029,45 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
   }
   if (!att) return;
 
-  // This lane's Q chunk (dims 8t .. 8t + 7) and, in the split holding the
-  // appended row, that row's K and V chunks, from the tagged words.
-  f16x8 qv = {}, kpos = {}, vpos = {};
-  bool timed_out = false;
-  {
-    const f32x4* fq = reinterpret_cast<const f32x4*>(fh.ftag + (long long)ha * 3 * kD + 8 * t);
-    const f32x4* fk = fq + kD / 2;
-    const f32x4* fvv = fq + kD;
-    for (int poll = 0;; ++poll) {
-      // The loop stores nothing, so without a compiler barrier the Q loads
-      // would be hoisted out of it and read once.
+  // The head's rotated Q and, in the split holding the appended row, that
+  // row's rotated K and V, from the tagged words into s_local.  Wave 0 polls
+  // (lane l: the words of dims 2l and 2l + 1); the other waves wait at the
+  // barrier, so the workgroup goes on as soon as one read sees the words
+  // (with every wave polling, the last of four reads in flight decided).
+  if (wave == 0 && !fh.force_local) {
+    const f32x4* fq = reinterpret_cast<const f32x4*>(fh.ftag + (long long)ha * 3 * kD) + lane;
+    bool seen = false;
+    for (int poll = 0; poll < kFrontPolls; ++poll) {
+      // The loop stores nothing to memory, so without a compiler barrier the
+      // loads would be hoisted out of it and read once.
       __asm__ volatile("" ::: "memory");
-      f32x4 a[4], b[4], e[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) a[k] = __builtin_nontemporal_load(fq + k);
+      f32x4 r[3];
+      r[0] = __builtin_nontemporal_load(fq);
       if (has_pos) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          b[k] = __builtin_nontemporal_load(fk + k);
-          e[k] = __builtin_nontemporal_load(fvv + k);
-        }
+        r[1] = __builtin_nontemporal_load(fq + kD / 2);
+        r[2] = __builtin_nontemporal_load(fq + kD);
       }
-      bool ok = tags_ok(a, p.tag);
-      if (has_pos) ok = ok && tags_ok(b, p.tag) && tags_ok(e, p.tag);
-      if (!__builtin_amdgcn_ballot_w64(!ok) && !fh.force_local) {
-        qv = tagged_values(a);
+      bool ok = tag_ok(r[0][1], p.tag) && tag_ok(r[0][3], p.tag);
+      if (has_pos)
+        ok = ok && tag_ok(r[1][1], p.tag) && tag_ok(r[1][3], p.tag) && tag_ok(r[2][1], p.tag) &&
+             tag_ok(r[2][3], p.tag);
+      if (!__builtin_amdgcn_ballot_w64(!ok)) {
+        s_local[0][2 * lane] = r[0][0];
+        s_local[0][2 * lane + 1] = r[0][2];
         if (has_pos) {
-          kpos = tagged_values(b);
-          vpos = tagged_values(e);
+#pragma unroll
+          for (int j = 1; j < 3; ++j) {
+            s_local[j][2 * lane] = r[j][0];
+            s_local[j][2 * lane + 1] = r[j][2];
+          }
         }
-        break;
-      }
-      if (poll >= kFrontPolls || fh.force_local) {
-        timed_out = true;
+        seen = true;
         break;
       }
     }
+    if (!seen && lane == 0) s_flag = 1;
   }
-  __syncthreads();
-  if (timed_out && lane == 0) s_flag = 1;
+  if (fh.force_local && tid == 0) s_flag = 1;
   __syncthreads();
   if (s_flag && tid == 0 && !fh.force_local)   // a miss, counted (the hook's are not)
     __hip_atomic_fetch_add(p.xcnt + ha * kXCounterStride + kXStatFrontMisses, 1u, __ATOMIC_RELAXED,
@@ -1097,12 +1087,14 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
       }
     }
     __syncthreads();
+  }
+  // This lane's chunks (dims 8t .. 8t + 7).
+  f16x8 qv, kpos, vpos;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      qv[e] = (_Float16)s_local[0][8 * t + e];
-      kpos[e] = (_Float16)s_local[1][8 * t + e];
-      vpos[e] = (_Float16)s_local[2][8 * t + e];
-    }
+  for (int e = 0; e < 8; ++e) {
+    qv[e] = (_Float16)s_local[0][8 * t + e];
+    kpos[e] = (_Float16)s_local[1][8 * t + e];
+    vpos[e] = (_Float16)s_local[2][8 * t + e];
   }
 
   // The split's scan: scan_rows' tiles in its order, the first round already

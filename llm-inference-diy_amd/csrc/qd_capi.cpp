@@ -567,7 +567,9 @@ int qd_qkv_proj_rope_cache(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_
   return QD_OK;
 }
 
-constexpr int kFrontFusedMaxRows = 512;
+// The fused front end + attention runs where the attention merges in its
+// kernel by default.
+constexpr int kFrontFusedMaxRows = kXMergeMaxRows;
 
 int qd_qkv_proj_rope_cache_attention(qd_ctx* ctx, const uint16_t* x, const uint16_t* norm_w,
                                      float eps, const uint16_t* w_qkv, const uint16_t* qkv_bias,
@@ -587,12 +589,12 @@ int qd_qkv_proj_rope_cache_attention(qd_ctx* ctx, const uint16_t* x, const uint1
   const int seqlen = pos + 1;
   const qd::AttnPlan plan = finish_plan(ctx, plan_auto(ctx, seqlen), seqlen);
   // One launch where the plan merges in the kernel with one workgroup per CU,
-  // up to kFrontFusedMaxRows rows (measured on MI355X at 16 heads: 10.98 us
-  // against 11.27 us for the two launches at 256 rows, but 12.47 against 12.29
-  // at 1024 and 14.31 against 13.95 at 2048, where each split's scan waits
-  // for its head's whole front end), and with out apart from qkv (whose rows
-  // the producers store while splits finish); otherwise the two launches,
-  // with the same outputs.
+  // up to kFrontFusedMaxRows rows (measured on MI355X at 16 heads, cold, per
+  // layer: 9.90 against 11.25 us for the two launches at 256 rows, 10.28
+  // against 11.64 at 512, 11.12 against 12.22 at 1024, 12.94 against 13.94 at
+  // 2048, 14.82 against 15.06 at 3072), and with out apart from qkv (whose
+  // rows the producers store while splits finish); otherwise the two
+  // launches, with the same outputs.
   const bool fused = seqlen <= kFrontFusedMaxRows && plan.variant == 1 && plan.xmerge && !plan.block_rows &&
                      (num_heads == 8 || num_heads == 16) &&
                      std::max(num_heads * 16, plan.splits * num_heads) <= ctx->num_cus &&

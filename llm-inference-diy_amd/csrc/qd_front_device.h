@@ -128,14 +128,22 @@ __device__ __forceinline__ void front_store(const QkvFrontParams& p, int h, int 
 constexpr int qkv_rows_per_phase(int nj) { return nj <= 4 ? 6 : 3; }
 constexpr int kQkvPairsPerBlock = 4;
 
+struct NoLoads {
+  __device__ void operator()() const {}
+};
+
 // One wave's share of the front end (qkv_front_kernel's work for pair (h, i)):
 // rows q(i), q(i+64), k(i), k(i+64), v(i), v(i+64) as six GEMVs in flight,
 // then the bias and rotation (front_finish) and, with kStore, lane 0's stores
 // to qkv and the cache (front_store).  Returns the pair's final values in
 // every lane.  kBiasWords: the bias pointer is 4-byte aligned, so each bias
-// value is read with a scalar load of its 32-bit word.
-template <int NJ, bool kBiasWords, bool kStore = true>
-__device__ __forceinline__ FrontPair qkv_front_pair(const QkvFrontParams& p, int h, int i, int lane) {
+// value is read with a scalar load of its 32-bit word.  after_rows() runs
+// once the weight rows' loads (and the epilogue's operands) are issued: loads
+// it issues go out behind them and stay in flight through the sums (loads
+// complete in issue order).
+template <int NJ, bool kBiasWords, bool kStore = true, class After = NoLoads>
+__device__ __forceinline__ FrontPair qkv_front_pair(const QkvFrontParams& p, int h, int i, int lane,
+                                                    After&& after_rows = After{}) {
   constexpr int RG = qkv_rows_per_phase(NJ);
   const int hidden = NJ * 512;
   // row r: (r >> 1) selects Q, K, V; (r & 1) the rotation half
@@ -152,18 +160,27 @@ __device__ __forceinline__ FrontPair qkv_front_pair(const QkvFrontParams& p, int
   // holding each value, any other 2-byte-aligned one 16 bits at a time into
   // registers that stay untouched until the epilogue.  Either way nothing here
   // waits for the weight stream.
+  // Read through the constant address space: the values are read-only here
+  // and wave-uniform, so they are scalar loads whatever code surrounds them.
+  typedef const __attribute__((address_space(4))) uint64_t ConstU64;
+  typedef const __attribute__((address_space(4))) uint32_t ConstU32;
   uint32_t bias_bits[6] = {};
-  const float2 cs = p.rope_cs[p.pos * 64 + i];
+  const uint64_t cs_bits = *(ConstU64*)(uintptr_t)(p.rope_cs + p.pos * 64 + i);
+  float2 cs;
+  cs.x = __uint_as_float((uint32_t)cs_bits);
+  cs.y = __uint_as_float((uint32_t)(cs_bits >> 32));
   if (p.bias) {
 #pragma unroll
     for (int r = 0; r < 6; ++r) {
       const int idx = (r >> 1) * hidden + h * 128 + i + (r & 1) * 64;
       if constexpr (kBiasWords)
-        bias_bits[r] = (reinterpret_cast<const uint32_t*>(p.bias)[idx >> 1] >> (16 * (idx & 1))) & 0xFFFFu;
+        bias_bits[r] = (((ConstU32*)(uintptr_t)p.bias)[idx >> 1] >> (16 * (idx & 1))) & 0xFFFFu;
       else
         bias_bits[r] = p.bias[idx];
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+  after_rows();
   __builtin_amdgcn_sched_barrier(0);
   if (p.norm_w) normalise<NJ>(xv, nv, p.eps);
   _Float16 y[6];                               // hgemv's half outputs

@@ -1,7 +1,7 @@
 """qd_qkv_proj_rope_cache_attention: the attention front end and decode
 attention of one layer (qwen_infer.cu:626-678) in one call.
 
-Up to 512 rows, where the attention plan merges in the scan kernel (one
+Where the attention plan merges in the scan kernel (up to 3072 rows, one
 workgroup per CU, 8 or 16 heads), the call is one launch in which each workgroup computes its
 share of the QKV GEMV, bias, RoPE and append and then its split of the
 attention, reading its head's rotated Q (and the appended row's K and V)
@@ -83,10 +83,11 @@ def _check_equal(a, b, what):
 @pytest.mark.parametrize("H,seqlen,norm,bias", [
     (16, 129, True, True), (16, 200, True, True), (16, 256, False, True), (16, 300, True, False),
     (16, 512, True, True), (8, 300, True, True),
-    # two launches: an in-kernel-merge plan beyond 512 rows, a fused attention
-    # plan, a two-launch split plan; 8 heads at 2000 rows (32 splits)
     (16, 513, True, True), (16, 1000, True, True), (16, 2048, False, True), (16, 3072, True, True),
-    (16, 100, True, True), (16, 3073, True, True), (8, 2000, True, True)])
+    # 8 heads at 2000 rows: 32 splits, so workgroups 128-255 have no producer role
+    (8, 2000, True, True),
+    # two launches: a fused attention plan, a two-launch split plan
+    (16, 100, True, True), (16, 3073, True, True)])
 def test_one_call_equals_the_two_calls(qdiy, H, seqlen, norm, bias):
     pos = seqlen - 1
     L = Layer(H, seqlen + 3, pos, seed=seqlen * 7 + H, norm=norm, bias=bias)
