@@ -107,6 +107,8 @@ def bench_lib():
     lib.qd_bench_read_ceiling.argtypes = [vp, vp, ll, ll, i, i, i, vp, vp]
     lib.qd_bench_empty.argtypes = [i, i, vp]
     lib.qd_bench_read_sweep.argtypes = [vp, vp, ll, i, i, i, i, i, i, i, i, i, vp, vp]
+    lib.qd_bench_read_merge.argtypes = [vp, vp, ll, i, i, i, i, i, i, i, i, i, vp, vp, ctypes.c_uint,
+                                        vp, vp]
     lib.qd_bench_attn_front.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, ll, ll, i, i, i, i, i, i, vp]
     return lib
 
@@ -230,6 +232,54 @@ def read_sweep(lib, L, n_layers, kc, vc, sh, steps, num_cus):
     return out, best
 
 
+def read_merge_floor(lib, L, n_layers, kc, vc, sh, steps, sweep):
+    """Read-and-merge floor (qd_bench_read_merge): for the sweep's three fastest
+    shapes and the fastest per-head-slice shapes of one workgroup per CU
+    (patterns 1 and 3 at 256 workgroups: one head per workgroup, 16 splits per
+    head, as the attention plans run), the read followed by a 16-partial
+    tagged hand-off to one merging workgroup per head group in the same launch
+    -- what any design that reads the bytes once and merges its splits in the
+    launch could reach with that read.  Returns ({shape: {"read": us,
+    "read_merge": us}}, (best per-head shape, its read_merge us))."""
+    import torch
+
+    slots = torch.zeros(16 * 64 * 144 * 2, dtype=torch.float32, device="cuda")
+    mout = torch.zeros(16 * 128, dtype=torch.float32, device="cuda")
+    stale = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    ranked = sorted(sweep.items(), key=lambda kv: kv[1])
+    names = [k for k, _ in ranked[:3]]
+    for pat in (1, 3):
+        per_head = [k for k, _ in ranked if k.endswith(f"_p{pat}") and "_g256_" in k]
+        names += per_head[:2]
+    tag = [1]
+    out = {}
+    for name in dict.fromkeys(names):
+        t, g, u, pat = (int(x[1:]) for x in name.split("_"))
+
+        def fn(iters):
+            rc = lib.qd_bench_read_merge(kc.data_ptr(), vc.data_ptr(), L * HID * 2, L, HID * 2, H,
+                                         n_layers, t, u, pat, g, iters, slots.data_ptr(), mout.data_ptr(),
+                                         tag[0], stale.data_ptr(), sh)
+            if rc != 0:
+                raise RuntimeError(f"read-merge launch failed ({name}): {rc}")
+            tag[0] += iters
+        fn(max(200, n_layers))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        fn(steps)
+        e1.record(stream)
+        e1.synchronize()
+        out[name] = {"read": sweep[name], "read_merge": round(e0.elapsed_time(e1) * 1e3 / steps, 3)}
+    if int(stale.item()) != 0:
+        raise RuntimeError(f"read-merge floor: {int(stale.item())} merging waves saw stale partials")
+    per_head = {k: v["read_merge"] for k, v in out.items() if "_g256_" in k and k[-2:] in ("p1", "p3")}
+    best = min(per_head.items(), key=lambda kv: kv[1]) if per_head else (None, None)
+    log(f"[bench] read+merge floor L={L}: per-head best {best[0]} {best[1]} us; "
+        + ", ".join(f"{k} {v['read']}/{v['read_merge']}" for k, v in out.items()))
+    return out, best
+
+
 def empty_loop(lib, sh, grid=H):
     """fn(iters): empty kernels of `grid` workgroups, back to back (the dispatch floor)."""
     def fn(iters):
@@ -316,6 +366,7 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     us_cold = timed(steps, cold)
     scan_us = merge_us = ceiling_us = floor_us = None
     sweep, sweep_best = None, (None, None)
+    floor, floor_best = None, (None, None)
     tail = max(20, int(WARMUP_TAIL_S / (us_cold * 1e-6)))
     if detail:
         # the call's kernels on their own, back to back over the same layers
@@ -343,16 +394,18 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
         # reach (last, so that its thousands of launches disturb no other figure)
         num_cus = torch.cuda.get_device_properties(0).multi_processor_count
         sweep, sweep_best = read_sweep(lib, L, n_layers, kc, vc, sh, max(steps, 200), num_cus)
+        floor, floor_best = read_merge_floor(lib, L, n_layers, kc, vc, sh, max(steps, 500), sweep)
     if not torch.isfinite(out).all():
         raise RuntimeError("non-finite attention output")
     d = ctx.plan_detail(L, {0: "auto", 1: "fused", 2: "split"}[variant], splits)
     plan = ("fused" if d.variant == qdiy.FUSED else
             "split+merge-in-kernel" if d.merge_in_kernel else "split", d.num_splits)
     smax = 16 if d.num_splits <= 16 else 32 if d.num_splits <= 32 else 64
-    kernel = (f"decode_attention_xmerge_kernel<{d.rows_per_tile}, {smax}, {d.loads_per_round}>"
-              if d.merge_in_kernel else
+    inter = ", true" if d.block_rows else ""
+    kernel = (f"decode_attention_xmerge_kernel<{d.rows_per_tile}, {smax}, {d.loads_per_round}, "
+              f"{d.waves}{inter}>" if d.merge_in_kernel else
               f"decode_attention_scan_kernel<{d.waves}, {d.rows_per_tile}, "
-              f"{'false' if d.variant == qdiy.FUSED else 'true'}, false, {d.loads_per_round}>")
+              f"{'false' if d.variant == qdiy.FUSED else 'true'}, false, {d.loads_per_round}{inter}>")
     ctx.close()
     del kc, vc
     torch.cuda.empty_cache()
@@ -363,7 +416,8 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
            "warmup_calls": warm_calls, "warmup_ms": round(warm_ms, 1),
            "scan_us": scan_us, "merge_us": merge_us, "read_ceiling_us": ceiling_us,
            "launch_floor_us": floor_us, "read_sweep": sweep, "read_best_shape": sweep_best[0],
-           "read_best_us": sweep_best[1]}
+           "read_best_us": sweep_best[1], "read_merge_floor": floor,
+           "read_merge_floor_best_shape": floor_best[0], "read_merge_floor_best_us": floor_best[1]}
     extra = ""
     if detail:
         res["scan_gbps"] = scan_bytes(L) / (scan_us * 1e-6) / 1e9
@@ -677,6 +731,9 @@ def main() -> int:
             "read_ceiling_best_us": head.get("read_best_us"),
             "read_ceiling_best_shape": head.get("read_best_shape"),
             "read_sweep_L8192": head.get("read_sweep"),
+            "read_merge_floor_L8192": head.get("read_merge_floor"),
+            "read_merge_floor_per_head_best_us": head.get("read_merge_floor_best_us"),
+            "read_merge_floor_per_head_best_shape": head.get("read_merge_floor_best_shape"),
             "empty_kernel_us": per_l("launch_floor_us"),
             "traffic_over_algorithmic": {str(L): t.get("traffic_over_algorithmic")
                                          for L, t in traffic.items()},
@@ -686,8 +743,8 @@ def main() -> int:
         },
         "roofline": None if not detail else {
             "bound": "hbm",
-            "kernel": f"{head['kernel']} (the scan kernel of qd_decode_attention at "
-                      f"L={HEADLINE_L}, plan {head['plan']})",
+            "kernel": f"{head['kernel']} (the {'only' if 'in-kernel' in head['plan'] else 'scan'} "
+                      f"kernel of qd_decode_attention at L={HEADLINE_L}, plan {head['plan']})",
             "achieved": round(head["scan_gbps"], 1), "peak": PEAK_GBPS, "unit": "GB/s",
             "frac": round(head["scan_gbps"] / PEAK_GBPS, 4),
             "traffic": traffic.get(HEADLINE_L, {}).get("scan_kernel_traffic_bytes"),
@@ -696,7 +753,10 @@ def main() -> int:
                                f"copy kernel's counts (not measured in this run)"),
             "algorithmic_bytes_per_launch": scan_bytes(HEADLINE_L),
             "launch_us": round(head["scan_us"], 3),
-            "launch_timing": ("scan-only launches back to back on the same rotated layers "
+            "launch_timing": ("the call's one kernel, back to back on the same rotated layers "
+                              "(qd_decode_attention_stage, scan stage: the whole call for a plan "
+                              "that merges in the scan kernel)" if "in-kernel" in head["plan"] else
+                              "scan-only launches back to back on the same rotated layers "
                               "(qd_decode_attention_stage); inside the call, after each merge "
                               "kernel, the same kernel runs ~0.7 us longer per launch in the "
                               "committed kernel trace"),

@@ -52,7 +52,10 @@ int qd_ctx_set_recompute_mask(qd_ctx* ctx, unsigned mask);
 
 /* Tiles whose loads a wave of a split plan issues before it consumes them
  * (1, 2 or 4; consumed in the same order, so every depth gives the same
- * bits); 0 (the default) lets the planner choose.  For sweeps and tests. */
+ * bits), or QD_SCAN_ROLLING: each wave issues tile i + 1's loads before it
+ * consumes tile i (reported as loads_per_round 0; the same bits too); 0 (the
+ * default) lets the planner choose.  For sweeps and tests. */
+#define QD_SCAN_ROLLING (-1)
 int qd_ctx_set_scan_depth(qd_ctx* ctx, int depth);
 
 /* Shape of the context's split plans, for A/B timing and tests: `waves`

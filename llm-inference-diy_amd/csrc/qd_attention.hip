@@ -232,6 +232,9 @@ __device__ __forceinline__ void consume_tile(GroupState& st, const KvTile<U>& tl
 // for, not the arithmetic.  (Prefetching tile i+1 while consuming tile i was
 // measured: it was slower at L = 8192-32768, where the launch already streams
 // at the box's read ceiling, by 4-8%.)
+// D = 0 is a rolling pipeline instead: the loads of tile i + 1 are issued
+// before tile i is consumed, so a wave's next loads are in flight while it
+// computes (the same tiles consumed in the same order: the same bits).
 template <int NW, int U, int D = 1, bool kInter = false>
 __device__ __forceinline__ void scan_rows(GroupState& st, const char* __restrict__ kbase,
                                           const char* __restrict__ vbase, unsigned row_bytes,
@@ -239,17 +242,46 @@ __device__ __forceinline__ void scan_rows(GroupState& st, const char* __restrict
                                           float scale_log2, int c = 0, int splits = 1) {
   constexpr int kStep = NW * 4 * U;   // rows from one of a wave's tiles to its next
   constexpr int kBlock = kInter ? kStep : 0;
-  for (int blk = wave * 4 * U; blk < nrows; blk += kStep * D) {
-    KvTile<U> tl[D];
+  if constexpr (D == 0) {
+    const int blk0 = wave * 4 * U;
+    if (blk0 >= nrows) return;
+    // Tiles blk0 + i * kStep, i < n.  The loop runs whole pairs with one exit,
+    // so on every edge into it exactly the loads of tile i are pending.
+    const int n = (nrows - blk0 + kStep - 1) / kStep;
+    KvTile<U> a, b;   // ping-pong buffers: no register copies between tiles
+    load_tile<U, kBlock>(a, kbase, vbase, row_bytes, blk0, nrows, g, t, c, splits);
+    int i = 0;
+    for (; i + 2 < n; i += 2) {
+      const int blk = blk0 + i * kStep;
+      load_tile<U, kBlock>(b, kbase, vbase, row_bytes, blk + kStep, nrows, g, t, c, splits);
+      __builtin_amdgcn_sched_barrier(0);
+      consume_tile<U>(st, a, blk, nrows, g, qv, scale_log2);
+      load_tile<U, kBlock>(a, kbase, vbase, row_bytes, blk + 2 * kStep, nrows, g, t, c, splits);
+      __builtin_amdgcn_sched_barrier(0);
+      consume_tile<U>(st, b, blk + kStep, nrows, g, qv, scale_log2);
+    }
+    const int blk = blk0 + i * kStep;
+    if (i + 1 < n) {
+      load_tile<U, kBlock>(b, kbase, vbase, row_bytes, blk + kStep, nrows, g, t, c, splits);
+      __builtin_amdgcn_sched_barrier(0);
+      consume_tile<U>(st, a, blk, nrows, g, qv, scale_log2);
+      consume_tile<U>(st, b, blk + kStep, nrows, g, qv, scale_log2);
+    } else {
+      consume_tile<U>(st, a, blk, nrows, g, qv, scale_log2);
+    }
+  } else {
+    for (int blk = wave * 4 * U; blk < nrows; blk += kStep * D) {
+      KvTile<U> tl[D];
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (d == 0 || blk + d * kStep < nrows)
-        load_tile<U, kBlock>(tl[d], kbase, vbase, row_bytes, blk + d * kStep, nrows, g, t, c, splits);
-    // keep the scheduler from sinking loads next to their uses
-    __builtin_amdgcn_sched_barrier(0);
+      for (int d = 0; d < D; ++d)
+        if (d == 0 || blk + d * kStep < nrows)
+          load_tile<U, kBlock>(tl[d], kbase, vbase, row_bytes, blk + d * kStep, nrows, g, t, c, splits);
+      // keep the scheduler from sinking loads next to their uses
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      if (d == 0 || blk + d * kStep < nrows) consume_tile<U>(st, tl[d], blk + d * kStep, nrows, g, qv, scale_log2);
+      for (int d = 0; d < D; ++d)
+        if (d == 0 || blk + d * kStep < nrows) consume_tile<U>(st, tl[d], blk + d * kStep, nrows, g, qv, scale_log2);
+    }
   }
 }
 
@@ -336,7 +368,7 @@ __device__ __forceinline__ void scan_fold_q(const AttnParams& p, const f16x8 qv,
 template <int NW, int U, int D = 1, bool kInter = false>
 __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q, int h, int r0,
                                           int nrows, ScanLds<NW>& lds, float& M, float& L,
-                                          float& O, int c = 0) {
+                                          float& O, int c, int splits) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar loop control
@@ -348,7 +380,7 @@ __device__ __forceinline__ void scan_fold(const AttnParams& p, const uint16_t* q
   init_state(st);
   scan_rows<NW, U, D, kInter>(st, reinterpret_cast<const char*>(p.k + off),
                               reinterpret_cast<const char*>(p.v + off), (unsigned)(p.row_stride * 2),
-                              nrows, wave, g, t, qv, p.scale_log2, c, p.splits);
+                              nrows, wave, g, t, qv, p.scale_log2, c, splits);
   wave_merge(st);
   if (lane < 16) {
     *reinterpret_cast<f32x4*>(&lds.so[wave][t * 8]) = f32x4{st.o[0], st.o[1], st.o[2], st.o[3]};
@@ -410,7 +442,7 @@ __device__ __forceinline__ void fold_waves(GroupState& st, ScanLds<NW>& lds, flo
 
 template <int NW, int U, bool kSplit, bool kBatch = false, int D = 1, bool kInter = false>
 __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnParams p) {
-  static_assert(!(kBatch && kInter), "batched queries plan contiguous splits");
+  static_assert(!(kBatch && kInter), "batched queries choose their row mapping per query");
   __shared__ ScanLds<NW> lds;
   const int tid = threadIdx.x;
   const int h = blockIdx.x % p.num_heads;
@@ -419,15 +451,31 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
   const int seqlen = p.seqlen + b;
   int rows_per_split = kSplit ? p.rows_per_split : seqlen;
   int splits = p.splits;
-  if constexpr (kBatch) {
-    auto_split(seqlen, p.num_cus, p.num_heads, &splits, &rows_per_split);
-    if (c >= splits) return;                  // workgroup-uniform: this query has fewer splits
-  }
-  const int r0 = kInter ? 0 : c * rows_per_split;
-  const int nrows = kInter ? interleaved_rows(seqlen, NW * 4 * U, splits, c)
-                           : min(seqlen - r0, rows_per_split);
   float M, L, O;
-  scan_fold<NW, U, D, kInter>(p, p.q + b * p.q_batch_stride, h, r0, nrows, lds, M, L, O, c);
+  if constexpr (kBatch) {
+    int block;
+    auto_plan(seqlen, p.num_cus, p.num_heads, p.long_inter != 0, &splits, &rows_per_split, &block);
+    if (c >= splits) return;                  // workgroup-uniform: this query has fewer splits
+    if constexpr (NW * 4 * U == kLongBlockRows) {
+      if (block) {                            // a long query: interleaved blocks, as decode plans it
+        scan_fold<NW, U, D, true>(p, p.q + b * p.q_batch_stride, h, 0,
+                                  interleaved_rows(seqlen, block, splits, c), lds, M, L, O, c, splits);
+      } else {
+        const int r0 = c * rows_per_split;
+        scan_fold<NW, U, D, false>(p, p.q + b * p.q_batch_stride, h, r0,
+                                   min(seqlen - r0, rows_per_split), lds, M, L, O, c, splits);
+      }
+    } else {
+      const int r0 = c * rows_per_split;     // no long query plans these tiles
+      scan_fold<NW, U, D, false>(p, p.q + b * p.q_batch_stride, h, r0,
+                                 min(seqlen - r0, rows_per_split), lds, M, L, O, c, splits);
+    }
+  } else {
+    const int r0 = kInter ? 0 : c * rows_per_split;
+    const int nrows = kInter ? interleaved_rows(seqlen, NW * 4 * U, splits, c)
+                             : min(seqlen - r0, rows_per_split);
+    scan_fold<NW, U, D, kInter>(p, p.q + b * p.q_batch_stride, h, r0, nrows, lds, M, L, O, c, splits);
+  }
   if (tid < kD) {
     if constexpr (kSplit) {
       const long long slot = kBatch ? ((long long)b * p.num_heads + h) * p.split_stride + c
@@ -547,8 +595,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_attention_merge_kernel(A
   _Float16* out = reinterpret_cast<_Float16*>(p.out);
   if constexpr (kBatch) {
     const int b = blockIdx.y;
-    int rows;
-    auto_split(p.seqlen + b, p.num_cus, p.num_heads, &splits, &rows);
+    int rows, block;
+    auto_plan(p.seqlen + b, p.num_cus, p.num_heads, p.long_inter != 0, &splits, &rows, &block);
     first = ((long long)b * p.num_heads + h) * p.split_stride;
     out += b * p.out_batch_stride;
   }
@@ -1128,6 +1176,13 @@ __global__ __launch_bounds__(256) void qkv_attention_kernel(QkvFrontParams f, At
 template <int NW, bool kSplit>
 static void launch_scan(const AttnParams& p, int rows_per_tile, int depth, dim3 grid, hipStream_t stream) {
   if constexpr (NW == 4 && kSplit) {   // deeper load rounds: split plans of 4-wave workgroups
+    if (depth == 0) {
+      if (rows_per_tile == 4)
+        hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, false, 0>), grid, dim3(256), 0, stream, p);
+      else
+        hipLaunchKernelGGL((decode_attention_scan_kernel<4, 2, true, false, 0>), grid, dim3(256), 0, stream, p);
+      return;
+    }
     if (depth == 4) {
       if (rows_per_tile == 4)
         hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, false, 4>), grid, dim3(256), 0, stream, p);
@@ -1161,22 +1216,27 @@ static void launch_xmerge_d(const AttnParams& p, int rows_per_tile, dim3 grid, h
     hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, SMAX, D>), grid, dim3(kMergeThreads), 0, stream, p);
 }
 
-// Interleaved-block split plans merged in the kernel: NW waves, U rows per tile.
-template <int SMAX>
+// Interleaved-block split plans merged in the kernel: NW waves, U rows per tile
+// (D: 1, or 0 for the rolling pipeline).
+template <int SMAX, int D>
 static void launch_xmerge_inter(const AttnParams& p, int waves, int rows_per_tile, dim3 grid,
                                 hipStream_t stream) {
   if (waves == 8 && rows_per_tile == 2)
-    hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, SMAX, 1, 8, true>), grid, dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, SMAX, D, 8, true>), grid, dim3(512), 0, stream, p);
   else if (waves == 8)
-    hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, 1, 8, true>), grid, dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, D, 8, true>), grid, dim3(512), 0, stream, p);
   else
-    hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, 1, 4, true>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, D, 4, true>), grid, dim3(256), 0, stream, p);
 }
 
 template <int SMAX>
 static void launch_xmerge(const AttnParams& p, const AttnPlan& plan, dim3 grid, hipStream_t stream) {
-  if (plan.block_rows)
-    launch_xmerge_inter<SMAX>(p, plan.waves, plan.rows_per_tile, grid, stream);
+  if (plan.block_rows && plan.depth == 0)
+    launch_xmerge_inter<SMAX, 0>(p, plan.waves, plan.rows_per_tile, grid, stream);
+  else if (plan.block_rows)
+    launch_xmerge_inter<SMAX, 1>(p, plan.waves, plan.rows_per_tile, grid, stream);
+  else if (plan.depth == 0)
+    launch_xmerge_d<SMAX, 0>(p, plan.rows_per_tile, grid, stream);
   else if (plan.depth == 4)
     launch_xmerge_d<SMAX, 4>(p, plan.rows_per_tile, grid, stream);
   else if (plan.depth == 2)
@@ -1185,15 +1245,16 @@ static void launch_xmerge(const AttnParams& p, const AttnPlan& plan, dim3 grid, 
     launch_xmerge_d<SMAX, 1>(p, plan.rows_per_tile, grid, stream);
 }
 
-// Scan-only launch of an interleaved-block split plan.
+// Scan-only launch of an interleaved-block split plan (D: 1, or 0 rolling).
+template <int D>
 static void launch_scan_inter(const AttnParams& p, int waves, int rows_per_tile, dim3 grid,
                               hipStream_t stream) {
   if (waves == 8 && rows_per_tile == 2)
-    hipLaunchKernelGGL((decode_attention_scan_kernel<8, 2, true, false, 1, true>), grid, dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((decode_attention_scan_kernel<8, 2, true, false, D, true>), grid, dim3(512), 0, stream, p);
   else if (waves == 8)
-    hipLaunchKernelGGL((decode_attention_scan_kernel<8, 4, true, false, 1, true>), grid, dim3(512), 0, stream, p);
+    hipLaunchKernelGGL((decode_attention_scan_kernel<8, 4, true, false, D, true>), grid, dim3(512), 0, stream, p);
   else
-    hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, false, 1, true>), grid, dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, false, D, true>), grid, dim3(256), 0, stream, p);
 }
 
 hipError_t launch_decode_attention_fused_batch(const AttnParams& p, int tokens, hipStream_t stream) {
@@ -1242,7 +1303,10 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
     return hipGetLastError();
   }
   if ((stages & kStageScan) && plan.block_rows) {
-    launch_scan_inter(p, plan.waves, plan.rows_per_tile, dim3(p.num_heads * p.splits), stream);
+    if (plan.depth == 0)
+      launch_scan_inter<0>(p, plan.waves, plan.rows_per_tile, dim3(p.num_heads * p.splits), stream);
+    else
+      launch_scan_inter<1>(p, plan.waves, plan.rows_per_tile, dim3(p.num_heads * p.splits), stream);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   } else if (stages & kStageScan) {

@@ -12,6 +12,7 @@
 namespace {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // Workgroup w reads units [w * per_wg, (w + 1) * per_wg) of 16 bytes of K and
 // of V; each thread keeps U units of each in flight, all issued before any is
@@ -67,11 +68,10 @@ __global__ __launch_bounds__(256) void read_ceiling_kernel(const u32x4* __restri
 //     reads the HPW * 256 contiguous bytes of group g in rows [c * rows /
 //     splits, ...); every wave instruction reads 1 KB of one row (four heads'
 //     slices), the workgroup's waves covering a row's HPW / 4 such pieces.
+// The loads of read_sweep_kernel: returns the XOR fold of every unit read.
 template <int NT, int U, int kPattern>
-__global__ __launch_bounds__(NT) void read_sweep_kernel(const u32x4* __restrict__ k,
-                                                        const u32x4* __restrict__ v,
-                                                        unsigned total_units, unsigned row_units,
-                                                        int heads, u32x4* sink) {
+__device__ __forceinline__ u32x4 sweep_body(const u32x4* __restrict__ k, const u32x4* __restrict__ v,
+                                            unsigned total_units, unsigned row_units, int heads) {
   u32x4 acc = {0u, 0u, 0u, 0u};
   const unsigned tid = threadIdx.x;
   if constexpr (kPattern == 0) {
@@ -168,23 +168,115 @@ __global__ __launch_bounds__(NT) void read_sweep_kernel(const u32x4* __restrict_
       for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
     }
   }
+  return acc;
+}
+
+template <int NT, int U, int kPattern>
+__global__ __launch_bounds__(NT) void read_sweep_kernel(const u32x4* __restrict__ k,
+                                                        const u32x4* __restrict__ v,
+                                                        unsigned total_units, unsigned row_units,
+                                                        int heads, u32x4* sink) {
+  const u32x4 acc = sweep_body<NT, U, kPattern>(k, v, total_units, row_units, heads);
   if (acc.x == 0x9E3779B9u && acc.y == 0x7F4A7C15u && acc.z == 0x85EBCA6Bu && acc.w == 0xC2B2AE35u)
     sink[blockIdx.x] = acc;
+}
+
+// Read-and-merge floor: a read-sweep kernel whose workgroups then hand a
+// 130-word partial (a stand-in value per thread, derived from the loaded
+// bytes) to one merging workgroup per group, as the in-kernel merge of a split
+// plan does -- so its time per launch is what any design that reads the bytes
+// once and folds split partials in the same launch could reach with that
+// read pattern.  Workgroup w belongs to hand-off group w % 16 (with
+// round-robin dispatch over 8 XCDs, one XCD per group) as split w / 16; the
+// group's last split merges.  Each other split stores its words as (value,
+// tag) 8-byte words, waits for the stores to be acknowledged and ends; the
+// merger's waves 0 and 1 (dim = thread) read every other split's word of
+// their dim with non-temporal loads until all carry this launch's tag (at
+// most kFloorPolls reads; a merger that gives up counts itself in *stale),
+// add them to their own value and store the sum.  No atomics and no fences on
+// the path, as in the product's in-kernel merge.
+constexpr int kFloorGroups = 16;
+constexpr int kFloorMaxSplits = 64;
+constexpr int kFloorSlotWords = 144;
+constexpr int kFloorPolls = 1 << 14;
+
+// The merging waves' read of one group's other splits (SMAX - 1 at most):
+// lane tid's word of every slot, clamped loads issued before any is used (a
+// clamped duplicate is loaded but not counted); returns whether every counted
+// word carries `tag` in every lane of the wave, and the sum in *sum.
+template <int SMAX>
+__device__ __forceinline__ bool poll_slots(const f32x2* gw, unsigned tid, unsigned others, unsigned tag,
+                                           float own, float* sum) {
+  const unsigned last = others ? others - 1 : 0;
+  f32x2 w[SMAX - 1];
+#pragma unroll
+  for (unsigned cc = 0; cc < SMAX - 1; ++cc)
+    w[cc] = __builtin_nontemporal_load(gw + min(cc, last) * kFloorSlotWords + tid);
+  bool ok = true;
+  float s = own;
+#pragma unroll
+  for (unsigned cc = 0; cc < SMAX - 1; ++cc) {
+    const bool on = cc < others;
+    ok &= !on || __float_as_uint(w[cc][1]) == tag;
+    s += on ? w[cc][0] : 0.0f;
+  }
+  *sum = s;
+  return __builtin_amdgcn_ballot_w64(!ok) == 0ull;
+}
+
+template <int NT, int U, int kPattern, int SMAX>
+__global__ __launch_bounds__(NT) void read_merge_kernel(const u32x4* __restrict__ k,
+                                                        const u32x4* __restrict__ v,
+                                                        unsigned total_units, unsigned row_units,
+                                                        int heads, float2* slots, float* out,
+                                                        unsigned tag, unsigned* stale) {
+  const u32x4 acc = sweep_body<NT, U, kPattern>(k, v, total_units, row_units, heads);
+  const unsigned tid = threadIdx.x;
+  const unsigned g = blockIdx.x % kFloorGroups, c = blockIdx.x / kFloorGroups;
+  const unsigned splits = gridDim.x / kFloorGroups;
+  const float tagf = __uint_as_float(tag);
+  const float val = (float)((acc.x ^ acc.y ^ acc.z ^ acc.w ^ tid) & 0xffffu);
+  float2* gs = slots + (size_t)g * kFloorMaxSplits * kFloorSlotWords;
+  if (c + 1 != splits) {
+    if (tid < 130) gs[c * kFloorSlotWords + tid] = float2{val, tagf};
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+  if (tid >= 128) return;
+  const f32x2* gw = reinterpret_cast<const f32x2*>(gs);
+  float sum = val;
+  bool fresh = splits == 1;
+  for (int r = 0; r < kFloorPolls && !fresh; ++r) {
+    asm volatile("" ::: "memory");   // the loads stay in the loop
+    fresh = poll_slots<SMAX>(gw, tid, splits - 1, tag, val, &sum);
+  }
+  if (!fresh && (tid & 63) == 0) atomicAdd(stale, 1u);
+  out[g * 128 + tid] = sum;
 }
 
 typedef void (*SweepKernel)(const u32x4*, const u32x4*, unsigned, unsigned, int, u32x4*);
 
 // The sweep's shapes: (threads per workgroup, loads per lane per stream).
+typedef void (*MergeKernel)(const u32x4*, const u32x4*, unsigned, unsigned, int, float2*, float*,
+                            unsigned, unsigned*);
+
 struct SweepShape {
   int nt, u;
   SweepKernel fn[7];
+  MergeKernel merge[3][7];   // [SMAX 16, 32, 64][pattern]
 };
+
+#define QD_MERGE_ROW(NT, U, S)                                                                 \
+  { read_merge_kernel<NT, U, 0, S>, read_merge_kernel<NT, U, 1, S>, read_merge_kernel<NT, U, 2, S>,   \
+    read_merge_kernel<NT, U, 3, S>, read_merge_kernel<NT, U, 4, S>, read_merge_kernel<NT, U, 5, S>,   \
+    read_merge_kernel<NT, U, 6, S> }
 
 #define QD_SWEEP_SHAPE(NT, U)                                                               \
   SweepShape {                                                                              \
     NT, U, { read_sweep_kernel<NT, U, 0>, read_sweep_kernel<NT, U, 1>, read_sweep_kernel<NT, U, 2>, \
              read_sweep_kernel<NT, U, 3>, read_sweep_kernel<NT, U, 4>, read_sweep_kernel<NT, U, 5>, \
-             read_sweep_kernel<NT, U, 6> }                                                    \
+             read_sweep_kernel<NT, U, 6> },                                                   \
+    { QD_MERGE_ROW(NT, U, 16), QD_MERGE_ROW(NT, U, 32), QD_MERGE_ROW(NT, U, 64) }            \
   }
 
 const SweepShape kSweepShapes[] = {
@@ -194,10 +286,38 @@ const SweepShape kSweepShapes[] = {
     QD_SWEEP_SHAPE(1024, 4), QD_SWEEP_SHAPE(1024, 8),
 };
 #undef QD_SWEEP_SHAPE
+#undef QD_MERGE_ROW
 
 // Does nothing: back-to-back launches of it time the dispatch floor, the cost
 // any dependent kernel (such as a separate merge launch) pays before its work.
 __global__ __launch_bounds__(256) void empty_kernel() {}
+
+
+// The sweep kernels' shape for (threads, loads), or null for arguments outside
+// what read_sweep_kernel's pattern covers (see qd_bench_read_sweep).
+const SweepShape* sweep_shape(int rows, int row_bytes, int heads, int n_layers, int threads,
+                              int loads, int pattern, int grid, int iters) {
+  if (rows < 1 || row_bytes < 16 || row_bytes % 16 || heads < 1 || n_layers < 1 || grid < 1 ||
+      grid > 65536 || iters < 0 || pattern < 0 || pattern > 6)
+    return nullptr;
+  const long long units = (long long)rows * (row_bytes / 16);
+  if (units > 0xFFFFFFFFLL) return nullptr;
+  const SweepShape* shape = nullptr;
+  for (const SweepShape& s : kSweepShapes)
+    if (s.nt == threads && s.u == loads) shape = &s;
+  if (!shape) return nullptr;
+  if (pattern == 0 && units % grid) return nullptr;
+  if (pattern == 1 && (grid % heads || rows % (grid / heads) || row_bytes / 16 != 16 * heads)) return nullptr;
+  if (pattern == 2 && units % ((long long)threads * loads)) return nullptr;
+  if (pattern == 3 && (grid % heads || row_bytes / 16 != 16 * heads)) return nullptr;
+  if (pattern >= 4) {
+    const int hpw = pattern == 4 ? 4 : pattern == 5 ? 8 : 16;
+    if (heads % hpw || threads / 64 < hpw / 4 || row_bytes / 16 != 16 * heads) return nullptr;
+    const int groups = heads / hpw;
+    if (grid % groups || rows % (grid / groups)) return nullptr;
+  }
+  return shape;
+}
 
 }  // namespace
 
@@ -247,31 +367,50 @@ int qd_bench_empty(int grid, int iters, hipStream_t stream) {
 int qd_bench_read_sweep(const void* k, const void* v, long long layer_stride_bytes, int rows,
                         int row_bytes, int heads, int n_layers, int threads, int loads,
                         int pattern, int grid, int iters, void* sink, hipStream_t stream) {
-  if (!k || !v || !sink || rows < 1 || row_bytes < 16 || row_bytes % 16 || heads < 1 ||
-      n_layers < 1 || grid < 1 || grid > 65536 || iters < 0 || pattern < 0 || pattern > 6)
-    return 1;
-  const long long units = (long long)rows * (row_bytes / 16);
-  if (units > 0xFFFFFFFFLL) return 1;
-  const SweepShape* shape = nullptr;
-  for (const SweepShape& s : kSweepShapes)
-    if (s.nt == threads && s.u == loads) shape = &s;
+  if (!k || !v || !sink) return 1;
+  const SweepShape* shape = sweep_shape(rows, row_bytes, heads, n_layers, threads, loads, pattern, grid, iters);
   if (!shape) return 1;
-  if (pattern == 0 && units % grid) return 1;
-  if (pattern == 1 && (grid % heads || rows % (grid / heads) || row_bytes / 16 != 16 * heads)) return 1;
-  if (pattern == 2 && units % ((long long)threads * loads)) return 1;
-  if (pattern == 3 && (grid % heads || row_bytes / 16 != 16 * heads)) return 1;
-  if (pattern >= 4) {
-    const int hpw = pattern == 4 ? 4 : pattern == 5 ? 8 : 16;
-    if (heads % hpw || threads / 64 < hpw / 4 || row_bytes / 16 != 16 * heads) return 1;
-    const int groups = heads / hpw;
-    if (grid % groups || rows % (grid / groups)) return 1;
-  }
+  const long long units = (long long)rows * (row_bytes / 16);
   for (int it = 0; it < iters; ++it) {
     const long long off = (long long)(it % n_layers) * layer_stride_bytes;
     hipLaunchKernelGGL(shape->fn[pattern], dim3(grid), dim3(threads), 0, stream,
                        reinterpret_cast<const u32x4*>(static_cast<const char*>(k) + off),
                        reinterpret_cast<const u32x4*>(static_cast<const char*>(v) + off),
                        (unsigned)units, (unsigned)(row_bytes / 16), heads, static_cast<u32x4*>(sink));
+    if (hipGetLastError() != hipSuccess) return 2;
+  }
+  return 0;
+}
+
+// `iters` launches of one read-and-merge floor kernel (read_merge_kernel):
+// the read of qd_bench_read_sweep's (threads, loads, pattern, grid) shape,
+// then every workgroup's 130-word partial handed to its group's merger, which
+// stores 128 sums to out[16][128] (floats).  Launch i reads layer i %
+// n_layers and tags its words tag0 + i (tag0 >= 1).  slots: 16 * 64 * 144
+// 8-byte words, zero before the first call (no word carries a launch's tag
+// before that launch writes it); stale: one counter, incremented by each
+// merging wave that gave up waiting (0 when every group's splits ran on its
+// merger's XCD).  grid a multiple of 16 with at most 64 workgroups per group,
+// and the sweep's constraints.  Returns 0, or 1 for arguments outside those.
+int qd_bench_read_merge(const void* k, const void* v, long long layer_stride_bytes, int rows,
+                        int row_bytes, int heads, int n_layers, int threads, int loads,
+                        int pattern, int grid, int iters, void* slots, void* out,
+                        unsigned tag0, void* stale, hipStream_t stream) {
+  if (!k || !v || !slots || !out || !stale || tag0 == 0u) return 1;
+  if (grid % kFloorGroups || grid / kFloorGroups > kFloorMaxSplits) return 1;
+  const SweepShape* shape = sweep_shape(rows, row_bytes, heads, n_layers, threads, loads, pattern, grid, iters);
+  if (!shape) return 1;
+  const long long units = (long long)rows * (row_bytes / 16);
+  for (int it = 0; it < iters; ++it) {
+    const long long off = (long long)(it % n_layers) * layer_stride_bytes;
+    const int per_group = grid / kFloorGroups;
+    const int row = per_group <= 16 ? 0 : per_group <= 32 ? 1 : 2;
+    hipLaunchKernelGGL(shape->merge[row][pattern], dim3(grid), dim3(threads), 0, stream,
+                       reinterpret_cast<const u32x4*>(static_cast<const char*>(k) + off),
+                       reinterpret_cast<const u32x4*>(static_cast<const char*>(v) + off),
+                       (unsigned)units, (unsigned)(row_bytes / 16), heads,
+                       static_cast<float2*>(slots), static_cast<float*>(out), tag0 + (unsigned)it,
+                       static_cast<unsigned*>(stale));
     if (hipGetLastError() != hipSuccess) return 2;
   }
   return 0;

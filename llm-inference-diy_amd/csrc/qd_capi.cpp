@@ -52,11 +52,13 @@ using qd::hip_fail;
 //     32, 16.7 at 64, 17.1 at 24).  Up to kXMergeMaxRows rows the last split
 //     of each head merges in the scan kernel (4.9-5.2 us at 256-512 rows, 5.6
 //     at 768, 6.4-6.7 at 1280-1536, against 6.9-7.4 with a merge kernel; 7.24
-//     against 7.29 at 2048, 8.42 against 8.49 at 3072); beyond, a merge kernel
-//     follows (9.67 against 9.73-9.93 us at 4096, 14.7 against 15.0 at 8192).
+//     against 7.29 at 2048, 8.42 against 8.49 at 3072); beyond, the splits'
+//     rows are dealt to them in interleaved blocks of 64 rows and the merge
+//     stays in the scan kernel (qd::auto_plan), where the context can merge
+//     there; else contiguous ranges and a merge kernel.
 constexpr int kFusedMaxRows = 224;
 constexpr int kFusedMaxRowsX = 128;
-constexpr int kXMergeMaxRows = 3072;
+using qd::kXMergeMaxRows;
 constexpr int kPrefillBatch = 256;   // split-plan prefill queries per batched launch pair
 
 qd::AttnPlan plan_fused(int seqlen) {
@@ -72,10 +74,13 @@ qd::AttnPlan plan_fused(int seqlen) {
   return plan;
 }
 
-qd::AttnPlan plan_split(int num_cus, int num_heads, int seqlen, int requested) {
-  int splits, rows;
+// A split plan: the automatic one (requested <= 0; qd::auto_plan, whose long
+// plans interleave their rows where merges_in_kernel), else `requested` splits
+// over contiguous ranges.
+qd::AttnPlan plan_split(int num_cus, int num_heads, int seqlen, int requested, bool merges_in_kernel) {
+  int splits, rows, block = 0;
   if (requested <= 0) {
-    qd::auto_split(seqlen, num_cus, num_heads, &splits, &rows);
+    qd::auto_plan(seqlen, num_cus, num_heads, merges_in_kernel, &splits, &rows, &block);
   } else {
     splits = std::min(requested, qd::kMaxSplits);
     rows = (seqlen + splits - 1) / splits;
@@ -90,7 +95,7 @@ qd::AttnPlan plan_split(int num_cus, int num_heads, int seqlen, int requested) {
   plan.rows_per_tile = rows >= 64 ? 4 : 2;
   plan.xmerge = 0;
   plan.depth = 1;
-  plan.block_rows = 0;
+  plan.block_rows = block;
   return plan;
 }
 
@@ -113,15 +118,21 @@ qd::AttnPlan reshape_split(const qd::AttnPlan& in, int seqlen, int waves, int ro
   return plan;
 }
 
+// The context's split plan.  Its automatic long plans interleave where the
+// context can merge in the scan kernel at all (ctx->xmerge_ok), whatever the
+// merge mode, so that every mode gives the same bits; a forced shape
+// (qd_ctx_set_split_shape) recasts the contiguous plan.
 qd::AttnPlan plan_split(const qd_ctx* ctx, int seqlen, int requested) {
-  const qd::AttnPlan plan = plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, requested);
-  return ctx->shape_waves ? reshape_split(plan, seqlen, ctx->shape_waves, ctx->shape_tile, ctx->shape_inter)
-                          : plan;
+  if (ctx->shape_waves)
+    return reshape_split(plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, requested, false), seqlen,
+                         ctx->shape_waves, ctx->shape_tile, ctx->shape_inter);
+  return plan_split(ctx->num_cus, ctx->cfg.num_heads, seqlen, requested, ctx->xmerge_ok);
 }
 
 // The automatic plan: fused up to fused_max rows, else the automatic split.
-qd::AttnPlan plan_auto(int num_cus, int num_heads, int seqlen, int fused_max) {
-  return seqlen <= fused_max ? plan_fused(seqlen) : plan_split(num_cus, num_heads, seqlen, 0);
+qd::AttnPlan plan_auto(int num_cus, int num_heads, int seqlen, int fused_max, bool merges_in_kernel) {
+  return seqlen <= fused_max ? plan_fused(seqlen)
+                             : plan_split(num_cus, num_heads, seqlen, 0, merges_in_kernel);
 }
 
 // Round-robin period of workgroup dispatch over the XCDs of `device` (workgroup
@@ -230,6 +241,7 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
   p.recompute_mask = ctx->recompute_mask;
   p.count_merges = ctx->count_merges;
   p.block_rows = plan.block_rows;
+  p.long_inter = ctx->xmerge_ok && !ctx->shape_waves;
   return p;
 }
 
@@ -242,7 +254,7 @@ qd::AttnParams make_params(qd_ctx* ctx, const uint16_t* q, const uint16_t* k, co
 // of loads.
 bool use_xmerge(const qd_ctx* ctx, const qd::AttnPlan& plan, int seqlen) {
   return plan.variant == 1 && xmerge_available(ctx) &&
-         (seqlen <= kXMergeMaxRows || ctx->merge_mode == QD_MERGE_IN_KERNEL) &&
+         (seqlen <= kXMergeMaxRows || plan.block_rows || ctx->merge_mode == QD_MERGE_IN_KERNEL) &&
          (plan.waves == 4 || plan.block_rows) && plan.splits <= qd::kXMaxSplits &&
          (long long)plan.splits * ctx->cfg.num_heads <= ctx->num_cus;
 }
@@ -257,7 +269,9 @@ bool use_xmerge(const qd_ctx* ctx, const qd::AttnPlan& plan, int seqlen) {
 qd::AttnPlan finish_plan(const qd_ctx* ctx, const qd::AttnPlan& plan_in, int seqlen) {
   qd::AttnPlan plan = plan_in;
   plan.xmerge = use_xmerge(ctx, plan, seqlen) ? 1 : 0;
-  if (plan.variant == 1 && plan.waves == 4 && !plan.block_rows) {
+  if (plan.variant == 1 && ctx->scan_depth == QD_SCAN_ROLLING) {
+    plan.depth = 0;
+  } else if (plan.variant == 1 && plan.waves == 4 && !plan.block_rows) {
     const int tiles = (plan.rows_per_split + 16 * plan.rows_per_tile - 1) / (16 * plan.rows_per_tile);
     plan.depth = ctx->scan_depth ? ctx->scan_depth : (plan.xmerge && tiles >= 2 ? 2 : 1);
   } else {
@@ -596,6 +610,7 @@ int qd_qkv_proj_rope_cache_attention(qd_ctx* ctx, const uint16_t* x, const uint1
   // rows the producers store while splits finish); otherwise the two
   // launches, with the same outputs.
   const bool fused = seqlen <= kFrontFusedMaxRows && plan.variant == 1 && plan.xmerge && !plan.block_rows &&
+                     (plan.depth == 1 || plan.depth == 2) &&
                      (num_heads == 8 || num_heads == 16) &&
                      std::max(num_heads * 16, plan.splits * num_heads) <= ctx->num_cus &&
                      !qd::overlaps(out, (size_t)hidden * 2, qkv, (size_t)3 * hidden * 2);
@@ -737,8 +752,8 @@ int qd_ctx_set_recompute_mask(qd_ctx* ctx, unsigned mask) {
 
 int qd_ctx_set_scan_depth(qd_ctx* ctx, int depth) {
   if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
-  if (depth != 0 && depth != 1 && depth != 2 && depth != 4)
-    return fail(QD_EINVAL, "scan depth must be 0, 1, 2 or 4, got %d", depth);
+  if (depth != 0 && depth != 1 && depth != 2 && depth != 4 && depth != QD_SCAN_ROLLING)
+    return fail(QD_EINVAL, "scan depth must be 0, 1, 2, 4 or QD_SCAN_ROLLING, got %d", depth);
   ctx->scan_depth = depth;
   return QD_OK;
 }
@@ -880,7 +895,8 @@ int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, cons
   if (rc != QD_OK) return rc;
   const bool ctx_merges_in_kernel = period > 0 && num_heads % period == 0;
   const qd::AttnPlan plan = plan_auto(num_cus, num_heads, seqlen,
-                                      ctx_merges_in_kernel ? kFusedMaxRowsX : kFusedMaxRows);
+                                      ctx_merges_in_kernel ? kFusedMaxRowsX : kFusedMaxRows,
+                                      ctx_merges_in_kernel);
   const long long slots = (long long)num_heads * plan.splits;
   if (plan.variant == 1 && slots > qd::kStaticScratchSlots)
     return fail(QD_EINVAL,
@@ -912,6 +928,7 @@ int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, cons
   p.recompute_mask = 0u;
   p.count_merges = 0;
   p.block_rows = plan.block_rows;
+  p.long_inter = ctx_merges_in_kernel;
   e = qd::launch_decode_attention(p, plan, stream);
   if (e != hipSuccess) return hip_fail(e, "decode attention launch");
   return QD_OK;

@@ -47,6 +47,7 @@ EXPORTS = (
 
 GEMM_EXACT, GEMM_MFMA = 0, 1      # qd_gemm_nt / qd_prefill_attention / qd_engine_set_prefill_mode modes
 MERGE_AUTO, MERGE_TWO_LAUNCHES, MERGE_IN_KERNEL = 0, 1, 2   # qd_ctx_set_merge modes (qdiy/bench.h)
+SCAN_ROLLING = -1   # qd_ctx_set_scan_depth: tile i + 1's loads issued before tile i is consumed
 
 
 class QdError(RuntimeError):
@@ -232,7 +233,8 @@ class Context:
         _check(load().qd_ctx_set_recompute_mask(self._h, mask & 0xFFFFFFFF))
 
     def set_scan_depth(self, depth: int) -> None:
-        """qd_ctx_set_scan_depth: tiles per load round of split plans (0: planner's)."""
+        """qd_ctx_set_scan_depth: tiles per load round of split plans (0: planner's;
+        SCAN_ROLLING: each wave's next tile in flight while it consumes one)."""
         _check(load().qd_ctx_set_scan_depth(self._h, depth))
 
     def set_split_shape(self, waves: int, rows_per_tile: int, interleave: int) -> None:

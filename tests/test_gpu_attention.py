@@ -256,6 +256,12 @@ def test_invalid_arguments_raise(qdiy):
     g.close()
 
 
+def _interleaved_rows(L, block, splits, c):
+    full, rem = divmod(L, block)
+    nfull = (full - 1 - c) // splits + 1 if full > c else 0
+    return nfull * block + (rem if rem > 0 and full % splits == c else 0)
+
+
 def _planner_rules(L, H, cus, variant="auto", requested=0, period=0):
     """The launch planner as its measured rules state it: fused (one 16-wave
     workgroup per head, 4-row tiles) up to 128 rows where the context merges
@@ -263,8 +269,11 @@ def _planner_rules(L, H, cus, variant="auto", requested=0, period=0):
     divides H), else up to 224; above, one split workgroup per CU in total,
     at most one per 16 rows, at most 256, rows per split rounded up to a
     multiple of 4, no empty workgroups, 4 waves, 4-row tiles from 64 rows per
-    split."""
-    fused_max = 128 if period >= 1 and H % period == 0 else 224
+    split; automatic plans beyond 3072 rows of such a context, with at most 64
+    splits and one workgroup per CU, deal the rows to the splits in blocks of
+    64 (the reported rows per split are split 0's)."""
+    xmerge = period >= 1 and H % period == 0
+    fused_max = 128 if xmerge else 224
     if variant == "fused" or (variant == "auto" and L <= fused_max):
         return (0, 1, L, 4, 16, 0)
     if requested > 0:
@@ -273,7 +282,11 @@ def _planner_rules(L, H, cus, variant="auto", requested=0, period=0):
         s = max(1, min(cus // H, (L + 15) // 16, 256))
     rows = -(-L // s)
     rows = (rows + 3) & ~3
-    return (1, -(-L // rows), rows, 4 if rows >= 64 else 2, 4, 0)
+    splits = -(-L // rows)
+    if requested <= 0 and xmerge and L > 3072 and splits <= 64 and splits * H <= cus:
+        splits = min(splits, -(-L // 64))
+        return (1, splits, _interleaved_rows(L, 64, splits, 0), 4, 4, 64)
+    return (1, splits, rows, 4 if rows >= 64 else 2, 4, 0)
 
 
 @pytest.mark.parametrize("H", [1, 4, 12, 16, 24, 40])
@@ -289,7 +302,8 @@ def test_planner_follows_its_rules(qdiy, H):
             assert ctx.plan_detail(L).as_tuple() == _planner_rules(L, H, cus, period=period), (H, L)
             plan = ctx.plan_detail(L)
             want_in_kernel = int(plan.variant == qdiy.SPLIT and period >= 1 and H % period == 0
-                                 and L <= 3072 and plan.num_splits <= 64 and plan.num_splits * H <= cus)
+                                 and (L <= 3072 or plan.block_rows) and plan.num_splits <= 64
+                                 and plan.num_splits * H <= cus)
             assert plan.merge_in_kernel == want_in_kernel, (H, L)
         for L in (1, 300, 8192):
             assert ctx.plan_detail(L, "fused").as_tuple() == _planner_rules(L, H, cus, "fused"), L

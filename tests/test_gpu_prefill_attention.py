@@ -121,6 +121,8 @@ CASES = [  # H, pos0, T, layout, q_pad, out_pad
     (4, 1000, 256, "engine", 0, 0),
     (12, 31, 17, "head_major", 0, 0),
     (12, 5, 40, "engine", 0, 0),         # 36 workgroups: not a multiple of the 8 XCDs
+    (16, 3040, 70, "engine", 0, 0),      # crosses 3072 rows: long queries deal rows in 64-row blocks
+    (8, 3060, 30, "head_major", 0, 0),
 ]
 
 
@@ -129,7 +131,7 @@ def test_exact_mode_is_decode_attention(qdiy, H, pos0, T, layout, q_pad, out_pad
     pr = Prompt(qdiy, H, pos0, T, seed=H * 7 + pos0 + T, layout=layout, q_pad=q_pad, out_pad=out_pad)
     try:
         got = pr.run(qdiy, qdiy.GEMM_EXACT)
-        edges = {max(0, b - pos0 - d) for b in (128, 224) for d in (0, 1)}
+        edges = {max(0, b - pos0 - d) for b in (128, 224, 3072) for d in (0, 1)}
         ts = sorted(({0, T // 3, T // 2, T - 1} | edges) & set(range(T)))
         want = pr.decode_rows(qdiy, ts)
         for t in ts:
