@@ -62,9 +62,11 @@ int qd_ctx_set_scan_depth(qd_ctx* ctx, int depth);
  * waves per workgroup, `rows_per_tile` rows per 16-lane group per tile, and,
  * with interleave 1, the rows dealt to the splits in blocks of waves * 4 *
  * rows_per_tile (qd_attn_plan.block_rows).  Supported: (8, 2, 1), (8, 4, 1),
- * (4, 4, 1); (0, 0, 0) restores the planner's shape.  Each shape has its own
- * summation order, so its bits differ from the default plan's; the plan of
- * every call is reported by qd_decode_attention_plan_detail. */
+ * (4, 4, 1), (4, 2, 1); (0, 0, 0) restores the planner's shape (whose plans
+ * beyond 3072 rows are themselves interleaved: (4, 2, 1) up to 16384 rows,
+ * (4, 4, 1) beyond, where the context can merge in the scan kernel).  Each
+ * shape has its own summation order, so its bits differ from other shapes';
+ * the plan of every call is reported by qd_decode_attention_plan_detail. */
 int qd_ctx_set_split_shape(qd_ctx* ctx, int waves, int rows_per_tile, int interleave);
 
 /* Test hook of qd_qkv_proj_rope_cache_attention's one-launch form: with on

@@ -456,17 +456,14 @@ __global__ __launch_bounds__(NW * 64) void decode_attention_scan_kernel(AttnPara
     int block;
     auto_plan(seqlen, p.num_cus, p.num_heads, p.long_inter != 0, &splits, &rows_per_split, &block);
     if (c >= splits) return;                  // workgroup-uniform: this query has fewer splits
-    if constexpr (NW * 4 * U == kLongBlockRows) {
-      if (block) {                            // a long query: interleaved blocks, as decode plans it
-        scan_fold<NW, U, D, true>(p, p.q + b * p.q_batch_stride, h, 0,
-                                  interleaved_rows(seqlen, block, splits, c), lds, M, L, O, c, splits);
-      } else {
-        const int r0 = c * rows_per_split;
-        scan_fold<NW, U, D, false>(p, p.q + b * p.q_batch_stride, h, r0,
-                                   min(seqlen - r0, rows_per_split), lds, M, L, O, c, splits);
-      }
+    // A long query deals its rows in interleaved blocks, as decode plans it;
+    // the host launches each query with the tile its plan takes, so such a
+    // query's block is this kernel's load round (NW * 4 * U rows).
+    if (block != 0 && block == NW * 4 * U) {
+      scan_fold<NW, U, D, true>(p, p.q + b * p.q_batch_stride, h, 0,
+                                interleaved_rows(seqlen, block, splits, c), lds, M, L, O, c, splits);
     } else {
-      const int r0 = c * rows_per_split;     // no long query plans these tiles
+      const int r0 = c * rows_per_split;
       scan_fold<NW, U, D, false>(p, p.q + b * p.q_batch_stride, h, r0,
                                  min(seqlen - r0, rows_per_split), lds, M, L, O, c, splits);
     }
@@ -1225,6 +1222,8 @@ static void launch_xmerge_inter(const AttnParams& p, int waves, int rows_per_til
     hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, SMAX, D, 8, true>), grid, dim3(512), 0, stream, p);
   else if (waves == 8)
     hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, D, 8, true>), grid, dim3(512), 0, stream, p);
+  else if (rows_per_tile == 2)
+    hipLaunchKernelGGL((decode_attention_xmerge_kernel<2, SMAX, D, 4, true>), grid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL((decode_attention_xmerge_kernel<4, SMAX, D, 4, true>), grid, dim3(256), 0, stream, p);
 }
@@ -1253,6 +1252,8 @@ static void launch_scan_inter(const AttnParams& p, int waves, int rows_per_tile,
     hipLaunchKernelGGL((decode_attention_scan_kernel<8, 2, true, false, D, true>), grid, dim3(512), 0, stream, p);
   else if (waves == 8)
     hipLaunchKernelGGL((decode_attention_scan_kernel<8, 4, true, false, D, true>), grid, dim3(512), 0, stream, p);
+  else if (rows_per_tile == 2)
+    hipLaunchKernelGGL((decode_attention_scan_kernel<4, 2, true, false, D, true>), grid, dim3(256), 0, stream, p);
   else
     hipLaunchKernelGGL((decode_attention_scan_kernel<4, 4, true, false, D, true>), grid, dim3(256), 0, stream, p);
 }
@@ -1285,8 +1286,8 @@ hipError_t launch_decode_attention(const AttnParams& p, const AttnPlan& plan, hi
   }
   if (plan.block_rows && (plan.block_rows != plan.waves * 4 * plan.rows_per_tile ||
                           p.block_rows != plan.block_rows ||
-                          !((plan.waves == 8 && (plan.rows_per_tile == 2 || plan.rows_per_tile == 4)) ||
-                            (plan.waves == 4 && plan.rows_per_tile == 4))))
+                          !((plan.waves == 8 || plan.waves == 4) &&
+                            (plan.rows_per_tile == 2 || plan.rows_per_tile == 4))))
     return hipErrorInvalidValue;
   if (plan.xmerge) {
     if ((plan.waves != 4 && !plan.block_rows) || p.splits > kXMaxSplits || !p.xpart || !p.xcnt)

@@ -92,7 +92,7 @@ qd::AttnPlan plan_split(int num_cus, int num_heads, int seqlen, int requested, b
   plan.rows_per_split = rows;
   plan.splits = splits;
   plan.waves = 4;
-  plan.rows_per_tile = rows >= 64 ? 4 : 2;
+  plan.rows_per_tile = block ? block / 16 : rows >= 64 ? 4 : 2;   // a block: one 4-wave load round
   plan.xmerge = 0;
   plan.depth = 1;
   plan.block_rows = block;
@@ -266,16 +266,28 @@ bool use_xmerge(const qd_ctx* ctx, const qd::AttnPlan& plan, int seqlen) {
 // 7.15, 1536: 6.81 against 7.25); one otherwise, and always with a merge
 // kernel (two per round was 0.1-0.7 us slower from 2048 rows up; four per
 // round slower everywhere).
+// The planner's depth for a split plan (finish_plan's, and the
+// allocation-free entry point's): 4-wave interleaved plans of 2-row tiles keep
+// the next tile's loads in flight while consuming one (depth 0; 8192 rows:
+// 13.78 against 18.41 us with one tile per round); contiguous 4-wave plans
+// that merge in the kernel load two tiles per round where a wave has two.
+int auto_depth(const qd::AttnPlan& plan, bool xmerge) {
+  if (plan.variant != 1) return 1;
+  if (plan.block_rows) return plan.waves == 4 && plan.rows_per_tile == 2 ? 0 : 1;
+  if (plan.waves != 4) return 1;
+  const int tiles = (plan.rows_per_split + 16 * plan.rows_per_tile - 1) / (16 * plan.rows_per_tile);
+  return xmerge && tiles >= 2 ? 2 : 1;
+}
+
 qd::AttnPlan finish_plan(const qd_ctx* ctx, const qd::AttnPlan& plan_in, int seqlen) {
   qd::AttnPlan plan = plan_in;
   plan.xmerge = use_xmerge(ctx, plan, seqlen) ? 1 : 0;
   if (plan.variant == 1 && ctx->scan_depth == QD_SCAN_ROLLING) {
     plan.depth = 0;
-  } else if (plan.variant == 1 && plan.waves == 4 && !plan.block_rows) {
-    const int tiles = (plan.rows_per_split + 16 * plan.rows_per_tile - 1) / (16 * plan.rows_per_tile);
-    plan.depth = ctx->scan_depth ? ctx->scan_depth : (plan.xmerge && tiles >= 2 ? 2 : 1);
+  } else if (plan.variant == 1 && ctx->scan_depth != 0) {   // forced; interleaved plans: 1 per round
+    plan.depth = plan.waves == 4 && !plan.block_rows ? ctx->scan_depth : 1;
   } else {
-    plan.depth = 1;
+    plan.depth = auto_depth(plan, plan.xmerge != 0);
   }
   return plan;
 }
@@ -725,8 +737,7 @@ int qd_decode_attention_plan_detail(const qd_ctx* ctx, int seqlen, int entry, in
 int qd_ctx_set_split_shape(qd_ctx* ctx, int waves, int rows_per_tile, int interleave) {
   if (!ctx) return fail(QD_EINVAL, "ctx is NULL");
   const bool off = waves == 0 && rows_per_tile == 0 && interleave == 0;
-  const bool ok = (waves == 8 && (rows_per_tile == 2 || rows_per_tile == 4) && interleave == 1) ||
-                  (waves == 4 && rows_per_tile == 4 && interleave == 1);
+  const bool ok = (waves == 8 || waves == 4) && (rows_per_tile == 2 || rows_per_tile == 4) && interleave == 1;
   if (!off && !ok)
     return fail(QD_EINVAL, "split shape (%d waves, %d rows per tile, interleave %d) unsupported",
                 waves, rows_per_tile, interleave);
@@ -894,9 +905,10 @@ int qd_decode_attention_noalloc(const uint16_t* q, const uint16_t* k_layer, cons
   rc = dispatch_period(dev, reinterpret_cast<unsigned*>(scratch_o), &period);
   if (rc != QD_OK) return rc;
   const bool ctx_merges_in_kernel = period > 0 && num_heads % period == 0;
-  const qd::AttnPlan plan = plan_auto(num_cus, num_heads, seqlen,
-                                      ctx_merges_in_kernel ? kFusedMaxRowsX : kFusedMaxRows,
-                                      ctx_merges_in_kernel);
+  qd::AttnPlan plan = plan_auto(num_cus, num_heads, seqlen,
+                                ctx_merges_in_kernel ? kFusedMaxRowsX : kFusedMaxRows,
+                                ctx_merges_in_kernel);
+  plan.depth = auto_depth(plan, false);
   const long long slots = (long long)num_heads * plan.splits;
   if (plan.variant == 1 && slots > qd::kStaticScratchSlots)
     return fail(QD_EINVAL,

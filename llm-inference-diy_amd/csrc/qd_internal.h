@@ -256,34 +256,39 @@ __host__ __device__ inline int interleaved_rows(int seqlen, int block_rows, int 
 // merge in the scan kernel (and longest length the automatic plan merges in
 // the scan kernel with such ranges).
 constexpr int kXMergeMaxRows = 3072;
-// Interleaved block of the long automatic plans: one load round of a 4-wave
-// workgroup of 4-row tiles.
-constexpr int kLongBlockRows = 64;
+// Longest automatic plan of 2-row tiles in 32-row interleaved blocks; longer
+// ones take 4-row tiles in 64-row blocks.  (A block is one load round of a
+// 4-wave workgroup: 4 waves x 4 groups x rows per tile.)
+constexpr int kLongTile2MaxRows = 16384;
 
 // The automatic split plan of a query over seqlen rows: auto_split's split
 // count and rows per split, with the rows in contiguous ranges (*block = 0),
 // or -- beyond kXMergeMaxRows rows, where the caller's split plans can merge
 // in the scan kernel (merges_in_kernel: dispatch round-robin over the XCDs
 // with a period dividing num_heads), with at most kXMaxSplits splits and one
-// workgroup per CU -- dealt to the splits in interleaved blocks of
-// kLongBlockRows rows (*block = kLongBlockRows; *rows then split 0's count,
-// the most).  Interleaved, at any time the grid reads one run of rows, and the
-// merge runs in the scan kernel: measured on MI355X at 16 heads (cold, per
-// call) 9.41 against 9.71 us at 4096 rows, 14.46 against 14.74 at 8192,
-// 18.64 against 18.84 at 12288, 23.44 against 24.00 at 16384, 32.42 against
-// 32.99 at 24576 and 40.79 against 41.54 at 32768 for contiguous ranges and a
-// merge kernel.  The host planner and the batched prefill kernels, which plan
-// every query for itself, both evaluate this one function.
+// workgroup per CU -- dealt to the splits in interleaved blocks of 32 rows
+// (2-row tiles of 4-wave workgroups) up to kLongTile2MaxRows rows and of 64
+// rows (4-row tiles) beyond (*block; *rows then split 0's count, the most).
+// Interleaved, at any time the grid reads one run of rows and the merge runs
+// in the scan kernel; the 2-row plans' waves keep their next tile's loads in
+// flight while they consume one (finish_plan's depth 0).  Measured on MI355X
+// at 16 heads (cold, us per call; contiguous ranges with a merge kernel /
+// 64-row blocks / 32-row blocks rolling): 4096 rows 9.71 / 9.41-9.78 / 9.25,
+// 8192 14.74 / 14.15-14.46 / 13.78, 16384 24.00 / 23.44-23.57 / 23.28, 20480
+// - / 27.44 / 27.92, 32768 41.54 / 40.79-41.80 / 42.68.  The host planner and
+// the batched prefill kernels, which plan every query for itself, both
+// evaluate this one function.
 __host__ __device__ inline void auto_plan(int seqlen, int num_cus, int num_heads, bool merges_in_kernel,
                                           int* splits, int* rows, int* block) {
   auto_split(seqlen, num_cus, num_heads, splits, rows);
   *block = 0;
   if (merges_in_kernel && seqlen > kXMergeMaxRows && *splits <= kXMaxSplits &&
       (long long)*splits * num_heads <= num_cus) {
-    const int nblocks = (seqlen + kLongBlockRows - 1) / kLongBlockRows;
+    const int b = seqlen <= kLongTile2MaxRows ? 32 : 64;
+    const int nblocks = (seqlen + b - 1) / b;
     if (*splits > nblocks) *splits = nblocks;
-    *rows = interleaved_rows(seqlen, kLongBlockRows, *splits, 0);
-    *block = kLongBlockRows;
+    *rows = interleaved_rows(seqlen, b, *splits, 0);
+    *block = b;
   }
 }
 

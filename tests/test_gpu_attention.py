@@ -271,7 +271,8 @@ def _planner_rules(L, H, cus, variant="auto", requested=0, period=0):
     multiple of 4, no empty workgroups, 4 waves, 4-row tiles from 64 rows per
     split; automatic plans beyond 3072 rows of such a context, with at most 64
     splits and one workgroup per CU, deal the rows to the splits in blocks of
-    64 (the reported rows per split are split 0's)."""
+    32 rows of 2-row tiles up to 16384 rows, of 64 rows of 4-row tiles beyond
+    (the reported rows per split are split 0's)."""
     xmerge = period >= 1 and H % period == 0
     fused_max = 128 if xmerge else 224
     if variant == "fused" or (variant == "auto" and L <= fused_max):
@@ -284,8 +285,9 @@ def _planner_rules(L, H, cus, variant="auto", requested=0, period=0):
     rows = (rows + 3) & ~3
     splits = -(-L // rows)
     if requested <= 0 and xmerge and L > 3072 and splits <= 64 and splits * H <= cus:
-        splits = min(splits, -(-L // 64))
-        return (1, splits, _interleaved_rows(L, 64, splits, 0), 4, 4, 64)
+        block = 32 if L <= 16384 else 64
+        splits = min(splits, -(-L // block))
+        return (1, splits, _interleaved_rows(L, block, splits, 0), block // 16, 4, block)
     return (1, splits, rows, 4 if rows >= 64 else 2, 4, 0)
 
 
@@ -295,7 +297,8 @@ def test_planner_follows_its_rules(qdiy, H):
     device's CU count, for automatic, fused and explicit split plans."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     lengths = sorted(set(list(range(1, 300)) + list(range(1000, 1100)) + list(range(2000, 2100)) +
-                         [3071, 3072, 3073, 4095, 4096, 4097, 8191, 8192, 8193, 16384, 32767, 32768]))
+                         [3071, 3072, 3073, 4095, 4096, 4097, 8191, 8192, 8193, 16384, 16385,
+                          32767, 32768]))
     with qdiy.Context(num_heads=H, max_seqlen=32768) as ctx:
         period = ctx.xcd_period()
         for L in lengths:

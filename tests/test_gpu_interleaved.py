@@ -40,7 +40,7 @@ def _attend(ctx, tensors, L, H, variant="auto", splits=0):
     return o[:H * 128].reshape(H, 128)
 
 
-SHAPES = [(8, 2, 1), (8, 4, 1), (4, 4, 1)]
+SHAPES = [(8, 2, 1), (8, 4, 1), (4, 4, 1), (4, 2, 1)]
 
 
 @pytest.mark.parametrize("shape", SHAPES)
@@ -91,7 +91,7 @@ def test_interleaved_rescan_path(qdiy, mask):
 
 def test_split_shape_validation(qdiy):
     with qdiy.Context(num_heads=16, max_seqlen=1024) as ctx:
-        for bad in ((8, 8, 1), (16, 2, 1), (8, 2, 0), (4, 2, 1), (0, 2, 0)):
+        for bad in ((8, 8, 1), (16, 2, 1), (8, 2, 0), (4, 2, 0), (4, 3, 1), (0, 2, 0)):
             with pytest.raises(qdiy.QdError):
                 ctx.set_split_shape(*bad)
         ctx.set_split_shape(8, 2, 1)

@@ -65,13 +65,13 @@ def test_context_finds_round_robin_dispatch(qdiy):
             plan = ctx.plan_detail(L)
             assert plan.merge_in_kernel == in_kernel, L           # 100 rows: fused, nothing to merge
             assert plan.variant == (qdiy.FUSED if L <= 128 else qdiy.SPLIT), L
-            assert plan.block_rows == (64 if L > 3072 else 0), L  # long plans: interleaved blocks
+            assert plan.block_rows == (32 if L > 3072 else 0), L  # long plans: interleaved blocks
         ctx.set_merge(qdiy.MERGE_IN_KERNEL)
         assert ctx.plan_detail(8192).merge_in_kernel == 1
         ctx.set_merge(qdiy.MERGE_TWO_LAUNCHES)
         assert ctx.plan_detail(1024).merge_in_kernel == 0
         assert ctx.plan_detail(8192).merge_in_kernel == 0
-        assert ctx.plan_detail(8192).block_rows == 64           # the same plan: the same bits
+        assert ctx.plan_detail(8192).block_rows == 32           # the same plan: the same bits
         assert ctx.plan_detail(200).variant == qdiy.FUSED       # fused up to 224 rows then
 
 
@@ -204,16 +204,16 @@ def test_stage_hook_with_in_kernel_merge(qdiy):
         assert rc == qdiy.QD_EINVAL
 
 
-@pytest.mark.parametrize("L", [300, 768, 1280, 3000, 8192, 20000])
+@pytest.mark.parametrize("L", [300, 768, 1280, 3000, 8192, 16385, 20000])
 def test_loads_per_round_give_the_same_bits(qdiy, L):
     """A wave may issue the loads of 1, 2 or 4 of its tiles before consuming
     them in order, or keep its next tile's loads in flight while it consumes
     one (QD_SCAN_ROLLING): the arithmetic is the same, so is every output bit,
     with the merge in the kernel or in a merge kernel.  The planner's own
     choice (two tiles per round with the merge in the kernel where a wave of a
-    contiguous plan has two or more; one for interleaved plans, whose waves
-    load one tile per round whatever is forced, rolling aside) is what
-    plan_detail reports."""
+    contiguous plan has two or more; rolling for interleaved 2-row plans, one
+    per round for 4-row ones; interleaved plans load one tile per round
+    whatever depth is forced, rolling aside) is what plan_detail reports."""
     H = 16
     case = AttnCase(L, H=H, seed=L + 1, kscale=0.5)
     t = _upload(case)
@@ -223,7 +223,8 @@ def test_loads_per_round_give_the_same_bits(qdiy, L):
             ctx.set_merge(mode)
             plan = ctx.plan_detail(L)
             tiles = -(-plan.rows_per_split // (16 * plan.rows_per_tile))
-            auto = 2 if plan.merge_in_kernel and tiles >= 2 and not plan.block_rows else 1
+            auto = ((0 if plan.rows_per_tile == 2 else 1) if plan.block_rows else
+                    2 if plan.merge_in_kernel and tiles >= 2 else 1)
             assert plan.loads_per_round == auto, (L, mode, plan.as_tuple(), plan.loads_per_round)
             _same(_attend(ctx, t, L, H), want, f"L={L} mode={mode}, planner's depth {auto}")
             for depth in (1, 2, 4, qdiy.SCAN_ROLLING):
