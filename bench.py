@@ -188,12 +188,14 @@ def read_loop(lib, L, n_layers, kc, vc, sh):
 # 32 or 64 KB per wave at 2, 4, 8, 16; patterns: 0 contiguous per workgroup, 1 the
 # scan's per-head 256-byte slices, 2 grid-strided contiguous chunks, 3 per-head slices
 # with the rows dealt to the splits in blocks of one workgroup load round, 4-6
-# workgroups over 4, 8 or 16 heads reading 1, 2 or 4 KB of each row.
+# workgroups over 4, 8 or 16 heads reading 1, 2 or 4 KB of each row; 7 pattern 3 with each
+# wave's next tile in flight while it folds one.
 SWEEP_SHAPES = [(256, 1), (512, 1), (256, 2), (1024, 1), (512, 2), (256, 4)]
 SWEEP_LOADS = (2, 4, 8, 16)
 SWEEP_PATTERNS = {0: "contiguous", 1: "per-head slices", 2: "grid-strided chunks",
                   3: "per-head slices, split-interleaved blocks", 4: "4-head (1 KB) row slices",
-                  5: "8-head (2 KB) row slices", 6: "whole rows (16 heads)"}
+                  5: "8-head (2 KB) row slices", 6: "whole rows (16 heads)",
+                  7: "per-head slices, split-interleaved blocks, next tile in flight"}
 
 
 def read_sweep(lib, L, n_layers, kc, vc, sh, steps, num_cus):
@@ -235,8 +237,8 @@ def read_sweep(lib, L, n_layers, kc, vc, sh, steps, num_cus):
 def read_merge_floor(lib, L, n_layers, kc, vc, sh, steps, sweep):
     """Read-and-merge floor (qd_bench_read_merge): for the sweep's three fastest
     shapes and the fastest per-head-slice shapes of one workgroup per CU
-    (patterns 1 and 3 at 256 workgroups: one head per workgroup, 16 splits per
-    head, as the attention plans run), the read followed by a 16-partial
+    (patterns 1, 3 and 7 at 256 workgroups: one head per workgroup, 16 splits
+    per head, as the attention plans run), the read followed by a 16-partial
     tagged hand-off to one merging workgroup per head group in the same launch
     -- what any design that reads the bytes once and merges its splits in the
     launch could reach with that read.  Returns ({shape: {"read": us,
@@ -249,7 +251,7 @@ def read_merge_floor(lib, L, n_layers, kc, vc, sh, steps, sweep):
     stream = torch.cuda.current_stream()
     ranked = sorted(sweep.items(), key=lambda kv: kv[1])
     names = [k for k, _ in ranked[:3]]
-    for pat in (1, 3):
+    for pat in (1, 3, 7):
         per_head = [k for k, _ in ranked if k.endswith(f"_p{pat}") and "_g256_" in k]
         names += per_head[:2]
     tag = [1]
@@ -273,7 +275,7 @@ def read_merge_floor(lib, L, n_layers, kc, vc, sh, steps, sweep):
         out[name] = {"read": sweep[name], "read_merge": round(e0.elapsed_time(e1) * 1e3 / steps, 3)}
     if int(stale.item()) != 0:
         raise RuntimeError(f"read-merge floor: {int(stale.item())} merging waves saw stale partials")
-    per_head = {k: v["read_merge"] for k, v in out.items() if "_g256_" in k and k[-2:] in ("p1", "p3")}
+    per_head = {k: v["read_merge"] for k, v in out.items() if "_g256_" in k and k[-2:] in ("p1", "p3", "p7")}
     best = min(per_head.items(), key=lambda kv: kv[1]) if per_head else (None, None)
     log(f"[bench] read+merge floor L={L}: per-head best {best[0]} {best[1]} us; "
         + ", ".join(f"{k} {v['read']}/{v['read_merge']}" for k, v in out.items()))
@@ -749,7 +751,7 @@ def main() -> int:
             "frac": round(head["scan_gbps"] / PEAK_GBPS, 4),
             "traffic": traffic.get(HEADLINE_L, {}).get("scan_kernel_traffic_bytes"),
             "traffic_source": (f"{os.path.relpath(traffic_file(HEADLINE_L), ROOT)}: rocprofv3 --pmc "
-                               f"FETCH_SIZE and WRITE_SIZE runs of bench.py --only scan, scaled by a "
+                               f"FETCH_SIZE and WRITE_SIZE runs of bench.py --only call, scaled by a "
                                f"copy kernel's counts (not measured in this run)"),
             "algorithmic_bytes_per_launch": scan_bytes(HEADLINE_L),
             "launch_us": round(head["scan_us"], 3),

@@ -67,7 +67,9 @@ __global__ __launch_bounds__(256) void read_ceiling_kernel(const u32x4* __restri
 //     workgroup (split c, head group g) with blockIdx.x = c * (heads / HPW) + g
 //     reads the HPW * 256 contiguous bytes of group g in rows [c * rows /
 //     splits, ...); every wave instruction reads 1 KB of one row (four heads'
-//     slices), the workgroup's waves covering a row's HPW / 4 such pieces.
+//     slices), the workgroup's waves covering a row's HPW / 4 such pieces;
+//   kPattern 7: kPattern 3's rows and slices, each wave's next tile in flight
+//     while it folds one (the load order of the rolling attention plans).
 // The loads of read_sweep_kernel: returns the XOR fold of every unit read.
 template <int NT, int U, int kPattern>
 __device__ __forceinline__ u32x4 sweep_body(const u32x4* __restrict__ k, const u32x4* __restrict__ v,
@@ -129,6 +131,51 @@ __device__ __forceinline__ u32x4 sweep_body(const u32x4* __restrict__ k, const u
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
+    }
+  } else if constexpr (kPattern == 7) {
+    // kPattern 3's rows and slices, each wave keeping its next tile's loads in
+    // flight while it folds one (rolling, as the attention plans of 2-row
+    // tiles load).  Tiles of a wave: rows b0 + wave * 4U + 4u + lane / 16 of
+    // blocks b0 = (c + splits * i) * kBlock.
+    const unsigned splits = gridDim.x / heads;
+    const unsigned h = blockIdx.x % heads, c = blockIdx.x / heads;
+    const unsigned rows = total_units / row_units;
+    const unsigned wave = tid >> 6, lane = tid & 63;
+    const unsigned col = h * 16u + (lane & 15u);
+    constexpr unsigned kBlock = (NT / 64) * 4u * U;
+    const unsigned nblk = (rows + kBlock - 1) / kBlock;
+    const unsigned n = nblk > c ? (nblk - 1 - c) / splits + 1 : 0;   // this split's blocks
+    auto load = [&](unsigned i, u32x4 (&a)[U], u32x4 (&b)[U]) {
+      const unsigned rb = (c + splits * i) * kBlock + wave * 4u * U + (lane >> 4);
+#pragma unroll
+      for (int u = 0; u < U; ++u) a[u] = __builtin_nontemporal_load(k + min(rb + 4u * u, rows - 1u) * row_units + col);
+#pragma unroll
+      for (int u = 0; u < U; ++u) b[u] = __builtin_nontemporal_load(v + min(rb + 4u * u, rows - 1u) * row_units + col);
+    };
+    auto fold = [&](const u32x4 (&a)[U], const u32x4 (&b)[U]) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) acc ^= a[u] ^ b[u];
+    };
+    if (n > 0) {
+      u32x4 a0[U], b0[U], a1[U], b1[U];
+      load(0, a0, b0);
+      unsigned i = 0;
+      for (; i + 2 < n; i += 2) {
+        load(i + 1, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(a0, b0);
+        load(i + 2, a0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(a1, b1);
+      }
+      if (i + 1 < n) {
+        load(i + 1, a1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        fold(a0, b0);
+        fold(a1, b1);
+      } else {
+        fold(a0, b0);
+      }
     }
   } else if constexpr (kPattern >= 4) {
     constexpr unsigned kHpw = kPattern == 4 ? 4u : kPattern == 5 ? 8u : 16u;
@@ -262,20 +309,20 @@ typedef void (*MergeKernel)(const u32x4*, const u32x4*, unsigned, unsigned, int,
 
 struct SweepShape {
   int nt, u;
-  SweepKernel fn[7];
-  MergeKernel merge[3][7];   // [SMAX 16, 32, 64][pattern]
+  SweepKernel fn[8];
+  MergeKernel merge[3][8];   // [SMAX 16, 32, 64][pattern]
 };
 
 #define QD_MERGE_ROW(NT, U, S)                                                                 \
   { read_merge_kernel<NT, U, 0, S>, read_merge_kernel<NT, U, 1, S>, read_merge_kernel<NT, U, 2, S>,   \
     read_merge_kernel<NT, U, 3, S>, read_merge_kernel<NT, U, 4, S>, read_merge_kernel<NT, U, 5, S>,   \
-    read_merge_kernel<NT, U, 6, S> }
+    read_merge_kernel<NT, U, 6, S>, read_merge_kernel<NT, U, 7, S> }
 
 #define QD_SWEEP_SHAPE(NT, U)                                                               \
   SweepShape {                                                                              \
     NT, U, { read_sweep_kernel<NT, U, 0>, read_sweep_kernel<NT, U, 1>, read_sweep_kernel<NT, U, 2>, \
              read_sweep_kernel<NT, U, 3>, read_sweep_kernel<NT, U, 4>, read_sweep_kernel<NT, U, 5>, \
-             read_sweep_kernel<NT, U, 6> },                                                   \
+             read_sweep_kernel<NT, U, 6>, read_sweep_kernel<NT, U, 7> },                                                   \
     { QD_MERGE_ROW(NT, U, 16), QD_MERGE_ROW(NT, U, 32), QD_MERGE_ROW(NT, U, 64) }            \
   }
 
@@ -298,7 +345,7 @@ __global__ __launch_bounds__(256) void empty_kernel() {}
 const SweepShape* sweep_shape(int rows, int row_bytes, int heads, int n_layers, int threads,
                               int loads, int pattern, int grid, int iters) {
   if (rows < 1 || row_bytes < 16 || row_bytes % 16 || heads < 1 || n_layers < 1 || grid < 1 ||
-      grid > 65536 || iters < 0 || pattern < 0 || pattern > 6)
+      grid > 65536 || iters < 0 || pattern < 0 || pattern > 7)
     return nullptr;
   const long long units = (long long)rows * (row_bytes / 16);
   if (units > 0xFFFFFFFFLL) return nullptr;
@@ -309,7 +356,7 @@ const SweepShape* sweep_shape(int rows, int row_bytes, int heads, int n_layers, 
   if (pattern == 0 && units % grid) return nullptr;
   if (pattern == 1 && (grid % heads || rows % (grid / heads) || row_bytes / 16 != 16 * heads)) return nullptr;
   if (pattern == 2 && units % ((long long)threads * loads)) return nullptr;
-  if (pattern == 3 && (grid % heads || row_bytes / 16 != 16 * heads)) return nullptr;
+  if ((pattern == 3 || pattern == 7) && (grid % heads || row_bytes / 16 != 16 * heads)) return nullptr;
   if (pattern >= 4) {
     const int hpw = pattern == 4 ? 4 : pattern == 5 ? 8 : 16;
     if (heads % hpw || threads / 64 < hpw / 4 || row_bytes / 16 != 16 * heads) return nullptr;
@@ -358,8 +405,8 @@ int qd_bench_empty(int grid, int iters, hipStream_t stream) {
 // `iters` launches of one read-sweep kernel, launch i reading layer
 // i % n_layers (`rows` rows of row_bytes bytes of K at k + layer *
 // layer_stride_bytes, and of V).  threads in {256, 512, 1024}, loads in
-// {2, 4, 8, 16} (not 16 with 1024 threads), pattern 0-6 (read_sweep_kernel),
-// grid workgroups; patterns 1 and 3 need grid a multiple of heads and 16
+// {2, 4, 8, 16} (not 16 with 1024 threads), pattern 0-7 (read_sweep_kernel),
+// grid workgroups; patterns 1, 3 and 7 need grid a multiple of heads and 16
 // units per head in a row (pattern 1 also rows a multiple of grid / heads;
 // patterns 4-6 heads a multiple of 4, 8, 16 and rows of grid / (heads / 4, 8,
 // 16) splits),
