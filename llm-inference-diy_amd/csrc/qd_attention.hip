@@ -170,6 +170,31 @@ __device__ __forceinline__ void load_tile(KvTile<U>& tl, const char* __restrict_
     tl.v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vbase + (r[u] * row_bytes + t * 16u)));
 }
 
+// load_tile for a tile all of whose rows are valid, at byte offsets from a
+// wave-uniform tile base: lane t of group g reads tbase + off[u], off[u] =
+// (first + 4u + g) * row_bytes + 16 t, the same addresses load_tile forms for
+// such a tile (rows first + 4u + g of the tile's first block row), with the
+// per-row arithmetic moved out of the loop.
+// (The empty asm keeps each offset a 32-bit lane value at its use, so the
+// loads take the saddr form -- scalar tile base + lane offset -- instead of a
+// 64-bit lane address the compiler would otherwise hoist and add per load.)
+template <int U>
+__device__ __forceinline__ void load_tile_at(KvTile<U>& tl, const char* __restrict__ kt,
+                                             const char* __restrict__ vt, const unsigned (&off)[U]) {
+  unsigned o[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    o[u] = off[u];
+    asm volatile("" : "+v"(o[u]));
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    tl.k[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(kt + o[u]));
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    tl.v[u] = __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(vt + o[u]));
+}
+
 // Online-softmax update of a group with one tile: scores s_u (rows >= nrows
 // get -inf), tile max mt = max_u s_u (u ascending), mn = max(m, mt),
 // alpha = exp2(m - mn), l = l*alpha, o = o*alpha, then for u ascending
@@ -245,24 +270,52 @@ __device__ __forceinline__ void scan_rows(GroupState& st, const char* __restrict
   if constexpr (D == 0) {
     const int blk0 = wave * 4 * U;
     if (blk0 >= nrows) return;
-    // Tiles blk0 + i * kStep, i < n.  The loop runs whole pairs with one exit,
-    // so on every edge into it exactly the loads of tile i are pending.
+    // Tiles blk0 + i * kStep, i < n.  Tile i's rows are rows blk0 + 4u + g
+    // past layer row first_row + i * step_rows (interleaved: split c's i-th
+    // block, kStep == kBlock; contiguous: kStep rows on), so every tile loads
+    // from a wave-uniform base with lane offsets fixed for the whole scan: the
+    // saddr form with no per-row arithmetic.  Only the last tile can hold rows
+    // past nrows - 1 (every earlier one ends at blk0 + i * kStep + 4U <=
+    // nrows), and a clamped row lies in its block, so the last tile's offsets
+    // are load_tile's clamp taken once, in the same base: load_tile's
+    // addresses, so the same rows and bits.  (8192 rows: 13.82-13.93 against
+    // 14.03-14.06 us per call with load_tile's per-row addresses; the
+    // one-round-at-a-time loop below ran slower in this form, 8.9 against 8.4
+    // us at 3072 rows and 41.6 against 41.0 at 32768, and keeps load_tile.)
     const int n = (nrows - blk0 + kStep - 1) / kStep;
+    const unsigned step_bytes = (unsigned)(kBlock ? splits * kBlock : kStep) * row_bytes;
+    const unsigned first_bytes = (unsigned)(kBlock ? c * kBlock : 0) * row_bytes;
+    const int lim = nrows - 1 - (n - 1) * kStep;   // the last tile's last valid row
+    unsigned off[U], offl[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      off[u] = (unsigned)(blk0 + 4 * u + g) * row_bytes + (unsigned)t * 16u;
+      offl[u] = (unsigned)min(blk0 + 4 * u + g, lim) * row_bytes + (unsigned)t * 16u;
+    }
+    auto load = [&](KvTile<U>& tl, int i) {
+      const size_t tb = first_bytes + (size_t)i * step_bytes;
+      unsigned o[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) o[u] = i + 1 < n ? off[u] : offl[u];
+      load_tile_at<U>(tl, kbase + tb, vbase + tb, o);
+    };
+    // The loop runs whole pairs with one exit, so on every edge into it
+    // exactly the loads of tile i are pending.
     KvTile<U> a, b;   // ping-pong buffers: no register copies between tiles
-    load_tile<U, kBlock>(a, kbase, vbase, row_bytes, blk0, nrows, g, t, c, splits);
+    load(a, 0);
     int i = 0;
     for (; i + 2 < n; i += 2) {
       const int blk = blk0 + i * kStep;
-      load_tile<U, kBlock>(b, kbase, vbase, row_bytes, blk + kStep, nrows, g, t, c, splits);
+      load(b, i + 1);
       __builtin_amdgcn_sched_barrier(0);
       consume_tile<U>(st, a, blk, nrows, g, qv, scale_log2);
-      load_tile<U, kBlock>(a, kbase, vbase, row_bytes, blk + 2 * kStep, nrows, g, t, c, splits);
+      load(a, i + 2);
       __builtin_amdgcn_sched_barrier(0);
       consume_tile<U>(st, b, blk + kStep, nrows, g, qv, scale_log2);
     }
     const int blk = blk0 + i * kStep;
     if (i + 1 < n) {
-      load_tile<U, kBlock>(b, kbase, vbase, row_bytes, blk + kStep, nrows, g, t, c, splits);
+      load(b, i + 1);
       __builtin_amdgcn_sched_barrier(0);
       consume_tile<U>(st, a, blk, nrows, g, qv, scale_log2);
       consume_tile<U>(st, b, blk + kStep, nrows, g, qv, scale_log2);
