@@ -50,6 +50,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
        python bench.py --only call|scan|merge|read|empty --kv L [--steps K]   (for rocprofv3)
        python bench.py --only prefill --kv T [--steps K]   (MFMA prefill attention of T tokens)
        python bench.py --only sweep --kv L [--steps K]     (read-ceiling sweep over launch shapes)
+       python bench.py --only front [--steps K]            (config 4's three loops, for a profiler)
 """
 from __future__ import annotations
 
@@ -433,6 +434,59 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     return res
 
 
+def front_loops(lib, steps: int, warmup: int):
+    """For a profiler: config 4's three loops (bench.py's config4_front_end), warmup +
+    steps launches each, in order: qd_qkv_proj_rope_cache alone, then followed by
+    qd_decode_attention over 2048 rows (two calls), then qd_qkv_proj_rope_cache_attention
+    (one launch); nothing else is launched after the inputs are made."""
+    import torch
+
+    run, close = _front_setup(lib)
+    for mode in (0, 1, 2):
+        run(warmup + steps, mode)
+        torch.cuda.synchronize()
+    log(f"[bench] profile loops 'front': {warmup + steps} calls each of the front end alone, "
+        f"front end + attention as two calls, and as one call")
+    close()
+
+
+def _front_setup(lib):
+    """Config 4's inputs and a runner run(iters, mode) over the rotated layers (mode 0
+    front end alone, 1 front end then attention as two calls, 2 one call); returns
+    (run, close)."""
+    import torch
+
+    import qdiy
+
+    L, pos = 2048, 2047
+    w_elems = 3 * HID * HID
+    kv_elems = L * HID
+    n_layers = max(3, math.ceil((1 << 30) / (2 * (w_elems + 2 * kv_elems))))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    x = torch.empty(n_layers * HID, dtype=torch.float16, device="cuda").normal_(generator=gen)
+    w = torch.empty(n_layers * w_elems, dtype=torch.float16, device="cuda").normal_(0.0, 0.02, generator=gen)
+    b = torch.empty(n_layers * 3 * HID, dtype=torch.float16, device="cuda").normal_(0.0, 0.02, generator=gen)
+    kc = torch.empty(n_layers * kv_elems, dtype=torch.float16, device="cuda").normal_(generator=gen)
+    vc = torch.empty_like(kc).normal_(generator=gen)
+    qkv = torch.empty(n_layers * 3 * HID, dtype=torch.float16, device="cuda")
+    out = torch.empty(n_layers * HID, dtype=torch.float16, device="cuda")
+    ctx = qdiy.Context(num_heads=H, max_seqlen=L)
+    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def run(iters, mode):
+        rc = lib.qd_bench_attn_front(ctx._h, x.data_ptr(), w.data_ptr(), b.data_ptr(), qkv.data_ptr(),
+                                     kc.data_ptr(), vc.data_ptr(), out.data_ptr(), w_elems, kv_elems,
+                                     n_layers, pos, L, H, iters, mode, sh)
+        if rc != 0:
+            raise RuntimeError(f"front-end bench failed: {qdiy.load().qd_last_error().decode()}")
+
+    def close():
+        ctx.close()
+        torch.cuda.empty_cache()
+    return run, close
+
+
 def measure_front(lib, steps: int, warmup: int):
     """Config 4: QKV GEMV [6144 x 2048] + bias + RoPE at pos 2047 + append, then
     attention over 2048 rows; weights and KV rotate over enough layers (>= 1 GiB)
@@ -623,11 +677,13 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one 256 MiB device copy (known FETCH_SIZE/WRITE_SIZE) and exit")
-    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty", "prefill", "sweep"],
+    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty", "prefill", "sweep", "front"],
                     help="for a profiler: run warmup + steps launches of this loop per --kv length "
                          "(call: qd_decode_attention; scan / merge: that kernel alone; read: the "
                          "read-ceiling kernel; empty: empty kernels; prefill: qd_prefill_attention "
-                         "in the MFMA mode over a --kv-token prompt), print no JSON, and exit")
+                         "in the MFMA mode over a --kv-token prompt; front: config 4's front end "
+                         "alone, with attention as two calls, and as one call), print no JSON, "
+                         "and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -657,6 +713,9 @@ def main() -> int:
     if args.only == "prefill":
         for T in args.kv:
             prefill_attention_loop(T, args.steps, args.warmup)
+        return 0
+    if args.only == "front":
+        front_loops(lib, args.steps, args.warmup)
         return 0
     if args.only == "sweep":
         num_cus = torch.cuda.get_device_properties(0).multi_processor_count
