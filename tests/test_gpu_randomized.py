@@ -87,6 +87,57 @@ def test_attention_random_shapes(qdiy, seed):
     assert np.all(np.abs(got.astype(np.float64) - ref) <= ulp16(ref) + 1e-5), case
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_attention_random_long_lengths(qdiy, seed):
+    """The automatic plan beyond 3072 rows: interleaved blocks (32 rows of 2-row
+    tiles with the next tile in flight up to 16384 rows, 64 rows of 4-row tiles
+    beyond) merged in the scan kernel where the head count is a multiple of the
+    dispatch period, contiguous splits and a merge kernel otherwise (12 heads);
+    random lengths up to 40000 rows, layouts and logit spikes, bit-exact against
+    the oracle's restatement of the plan the library reports."""
+    rng = np.random.default_rng(90000 + seed)
+    H = (8, 16, 24, 12)[int(rng.integers(0, 4))]
+    L = int(rng.integers(3000, 40000))
+    S = L + int(rng.integers(0, 40))
+    layout = ("engine", "head_major", "padded")[int(rng.integers(0, 3))]
+    if layout == "engine":
+        rs, hs = H * D, D
+    elif layout == "head_major":
+        rs, hs = D, S * D
+    else:
+        hs = D + 8 * int(rng.integers(0, 4))
+        rs = (H - 1) * hs + D + 8 * int(rng.integers(0, 33))
+    n = (S - 1) * rs + (H - 1) * hs + D
+    kscale = float(rng.uniform(0.1, 1.5))
+    q = normal_f16(rng, (H, D))
+    k = normal_f16(rng, n, kscale)
+    v = normal_f16(rng, n)
+    if rng.random() < 0.4:                  # rows aligned with q: logit spikes
+        every = int(rng.integers(50, 500))
+        for j in range(int(rng.integers(0, every)), L, every):
+            for h in range(H):
+                k[j * rs + h * hs:j * rs + h * hs + D] = q[h]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    with qdiy.Context(num_heads=H, max_seqlen=S, kv_row_stride=rs, kv_head_stride=hs) as ctx:
+        out = torch.empty(H * D, dtype=torch.float16, device="cuda")
+        ctx.decode_attention(torch.from_numpy(q.reshape(-1)).cuda(), torch.from_numpy(k).cuda(),
+                             torch.from_numpy(v).cuda(), out, L)
+        torch.cuda.synchronize()
+        plan = ctx.plan_detail(L)
+        period = ctx.xcd_period()
+    case = f"H={H} L={L} S={S} {layout} rs={rs} hs={hs} kscale={kscale:.2f} plan={plan.as_tuple()}"
+    print(case, flush=True)
+    if L > 3072 and period >= 1 and H % period == 0 and plan.num_splits * H <= cus:
+        assert plan.block_rows == (32 if L <= 16384 else 64) and plan.merge_in_kernel == 1, case
+    elif L > 3072:
+        assert plan.block_rows == 0 and plan.merge_in_kernel == 0, case
+    got = out.cpu().numpy().reshape(H, D)
+    want = oracle.attention_planned(q, k, v, L, H, rs, hs, oracle.Plan(*plan.as_tuple()), nthreads=8)
+    assert _same(got, want), case
+    ref = _attn_fp64(q, k, v, L, H, rs, hs)
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= ulp16(ref) + 1e-5), case
+
+
 @pytest.mark.parametrize("seed", range(20))
 def test_proj_residual_random_shapes(qdiy, seed):
     rng = np.random.default_rng(71000 + seed)
