@@ -22,19 +22,26 @@ GPU work.  (From an idle GPU, the first 20 calls ran ~8% slower per call than
 the steady state, which a 20-step window would report.)  The warm-up that ran
 is reported in config.warmup_run.
 
-roofline: the dominant kernel of the call, the split scan kernel, timed live
-between two HIP events on the call's stream over `steps` scan-only launches
-(qd_decode_attention_stage) on the same rotated layers; achieved = its
-algorithmic bytes (K and V rows and Q: 8192*L + 4096) / its mean duration per
-launch.  The merge kernel is timed the same way (config.merge_kernel_us).
-config.read_ceiling_us is a load-only kernel over the same layers in the
-scan's launch shape: what one kernel streaming those bytes takes on this box.
-config.empty_kernel_us is an empty kernel of the merge's grid launched back to
-back: the dispatch floor any dependent launch pays.  config.read_sweep_L8192 times
-the same L=8192 bytes read by kernels of 161 other launch shapes (1, 2 or 4 waves
-per SIMD; 8-64 KB in flight per wave; contiguous, grid-strided, per-head and
-head-group access patterns); config.read_ceiling_best_us is the fastest of them:
-what any one-launch design reading those bytes could reach on this box.
+roofline: the dominant kernel of the call -- at every length of the bench on
+MI355X the call's only kernel, the split scan with the merge inside it -- timed
+live between two HIP events on the call's stream over `steps` launches
+(qd_decode_attention_stage, scan stage) on the same rotated layers; achieved =
+its algorithmic bytes (K and V rows and Q: 8192*L + 4096) / its mean duration
+per launch.  config.scan_without_in_kernel_merge_us is the same plan's scan
+kernel alone (a two-launch context's scan stage: plain partials, no merge);
+with a separate merge kernel, config.merge_kernel_us times that kernel.
+config.read_ceiling_us is a load-only kernel over the same layers in a
+one-workgroup-per-CU launch shape: what one kernel streaming those bytes takes on
+this box.  config.empty_kernel_us is an empty kernel of 16 workgroups launched
+back to back: the dispatch floor any dependent launch pays.
+config.read_sweep_L8192 times the same L=8192 bytes read by kernels of other
+launch shapes (1, 2 or 4 waves per SIMD; 8-64 KB in flight per wave;
+contiguous, grid-strided, per-head and head-group access patterns);
+config.read_ceiling_best_us is the fastest of them, and
+config.read_merge_floor_L8192 the fastest of them followed, in the same launch,
+by the tagged hand-off of 16 partials per head group to one merger: what any
+design that reads the bytes once and merges split partials in one launch could
+reach on this box.
 
 The CPU baseline is the repository's C restatement of the reference kernels
 (oracle/) on the host cores of the same box, on a bounded sample of the same
@@ -367,7 +374,7 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
     cold = lambda n: run(n, n_layers)
     warm_calls, warm_ms = warm_up(cold, warmup)
     us_cold = timed(steps, cold)
-    scan_us = merge_us = ceiling_us = floor_us = None
+    scan_us = merge_us = ceiling_us = floor_us = scan_alone_us = None
     sweep, sweep_best = None, (None, None)
     floor, floor_best = None, (None, None)
     tail = max(20, int(WARMUP_TAIL_S / (us_cold * 1e-6)))
@@ -381,6 +388,16 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
         if pd.variant == qdiy.SPLIT and not pd.merge_in_kernel:
             stage(4)(tail)
             merge_us = timed(steps, stage(4))
+        elif pd.variant == qdiy.SPLIT:
+            # the same plan's scan alone (a two-launch context plans the same splits and
+            # writes plain partials): the call's kernel less its in-kernel merge
+            ctx2 = qdiy.Context(num_heads=H, max_seqlen=L)
+            ctx2.set_merge(qdiy.MERGE_TWO_LAUNCHES)
+            if ctx2.plan_detail(L).as_tuple() == pd.as_tuple():
+                s2 = attention_loop(lib, ctx2, L, n_layers, kc, vc, q, out, sh, 3)
+                s2(tail)
+                scan_alone_us = timed(steps, s2)
+            ctx2.close()
         # load-only kernel over the same layers' K and V rows, same launch shape
         read = read_loop(lib, L, n_layers, kc, vc, sh)
         read(tail)
@@ -418,6 +435,7 @@ def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int 
            "layers": n_layers, "plan": f"{plan[0]}x{plan[1]}", "kernel": kernel,
            "warmup_calls": warm_calls, "warmup_ms": round(warm_ms, 1),
            "scan_us": scan_us, "merge_us": merge_us, "read_ceiling_us": ceiling_us,
+           "scan_alone_us": scan_alone_us,
            "launch_floor_us": floor_us, "read_sweep": sweep, "read_best_shape": sweep_best[0],
            "read_best_us": sweep_best[1], "read_merge_floor": floor,
            "read_merge_floor_best_shape": floor_best[0], "read_merge_floor_best_us": floor_best[1]}
@@ -787,6 +805,7 @@ def main() -> int:
             "scan_kernel_us": per_l("scan_us"),
             "scan_kernel_gbps": per_l("scan_gbps", 1),
             "merge_kernel_us": per_l("merge_us"),
+            "scan_without_in_kernel_merge_us": per_l("scan_alone_us"),
             "read_ceiling_us": per_l("read_ceiling_us"),
             "read_ceiling_gbps": per_l("ceiling_gbps", 1),
             "read_ceiling_best_us": head.get("read_best_us"),
