@@ -187,7 +187,7 @@ def _split_rows_by_hand(L, block, splits):
 
 
 @pytest.mark.parametrize("L,splits,tile,waves", [(1024, 4, 2, 8), (8192, 16, 2, 8), (3072, 6, 4, 8),
-                                                 (2048, 16, 4, 4)])
+                                                 (2048, 16, 4, 4), (8192, 16, 2, 4), (32768, 16, 4, 4)])
 def test_interleaved_plan_is_a_contiguous_plan_over_permuted_rows(L, splits, tile, waves):
     """With equal splits, an interleaved plan over the cache must give the bits of a
     contiguous plan of the same shape over a cache whose rows are reordered so that
@@ -253,7 +253,9 @@ def test_interleaved_ragged_lengths_cover_every_row(L):
     case.Kh[1, j] = (case.q[1].astype(np.float32) * 4).astype(np.float16)
     case.kc[:] = np.ascontiguousarray(case.Kh.transpose(1, 0, 2)).reshape(-1)
     ref = case.fp64()
-    for plan in (oracle.interleaved_plan(L, 16), oracle.interleaved_plan(L, 3, rows_per_tile=4)):
+    for plan in (oracle.interleaved_plan(L, 16), oracle.interleaved_plan(L, 3, rows_per_tile=4),
+                 oracle.interleaved_plan(L, 16, rows_per_tile=2, waves=4),
+                 oracle.interleaved_plan(L, 5, rows_per_tile=4, waves=4)):
         out = _run(case, plan).astype(np.float64)
         assert np.all(np.abs(out - ref) <= 0.5 * ulp16(ref) + 1e-5), plan
         assert np.all(np.abs(out[1] - case.Vh[1, j].astype(np.float64)) <= ulp16(case.Vh[1, j])), plan
