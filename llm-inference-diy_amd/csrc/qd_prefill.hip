@@ -992,6 +992,29 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring128_kernel(BatchedGemvPara
   }
 }
 
+// Buffer resource over `bytes` bytes from `base` (raw: no stride, no
+// swizzle; word 3 the data format gfx9 parts take for untyped loads), and the
+// buffer load of 16 bytes per lane into LDS (lane l at lds + 16 l; M0 holds
+// the wave-uniform LDS base) at base + voffset + soffset.  Bytes at or past
+// `bytes` read as zeros.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, unsigned bytes) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  i32x4 r;
+  r[0] = (int)(unsigned)a;
+  r[1] = (int)(unsigned)(a >> 32);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+__device__ void raw_buffer_load_lds(i32x4 rsrc, __attribute__((address_space(3))) unsigned* lds, int size,
+                                    int voffset, int soffset, int offset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.lds");
+__device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, __attribute__((address_space(3))) unsigned* lds,
+                                                  unsigned voffset, int soffset) {
+  raw_buffer_load_lds(rsrc, lds, 16, (int)voffset, soffset, 0, 0);
+}
+
 // The same product with a 192-row x 256-token workgroup tile (products whose
 // grid of such tiles still covers the device: QKV and gate/up at 2048 tokens,
 // one and two tiles per CU).  Per K, a 128 x 128 tile moves 64 bytes from L2
@@ -1001,36 +1024,43 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring128_kernel(BatchedGemvPara
 // ~35% of the matrix-core time (rocprofv3: SQ_VALU_MFMA_BUSY_CYCLES against
 // SQ_BUSY_CYCLES).  Here each of the four waves computes 96 W rows x 128
 // tokens (6 x 8 MFMA blocks, 192 accumulator registers): 37 B per clock from
-// L2 and ~110 from LDS at the matrix cores' rate.  K goes in tiles of 32
-// through a ring of 5 stages of 28 KB (W tile 192 x 64 B, then X tile 256 x
-// 64 B; chunk q of row r at q ^ ((r / 2) % 4), so the eight rows that one
-// eight-lane group of a fragment read covers -- two per 128-byte bank line --
-// fall on distinct banks: no conflicts in rocprofv3's SQ_LDS_BANK_CONFLICT,
-// against 3.7 M cycles per launch with (r / 4) % 4), 4 tiles in flight, filled by direct loads (7
-// per thread per stage), the next tile's fragments read from LDS while the
-// matrix cores consume the current one's.  kEpi 0: half(sum); 1: half(R +
-// half(sum)); 3: joint gate/up, 96 outputs per workgroup (W tile rows 0..95
-// from W1, 96..191 the same rows of W2; wave (wy = w / 2) takes gate rows
-// 48 wy + 16 i as its A blocks i < 3 and the same up rows as blocks i + 3).
+// L2 and ~110 from LDS at the matrix cores' rate.  K goes in tiles of 64
+// through two stages of 56 KB (W tile 192 x 128 B, then X tile 256 x 128 B;
+// chunk q of row r at q ^ (r % 8), so the eight rows that one eight-lane
+// group of a fragment read covers fall on distinct banks), filled by direct
+// loads (14 per thread per stage) whose eight-lane groups each read one whole
+// 128-byte line.  Fragments go in K steps of 32, two per tile: the next
+// step's fragments are read from LDS while the matrix cores consume the
+// current one's, and a stage takes tile kt + 2 as soon as every wave has read
+// tile kt's second step.  (32-wide tiles through a ring of 5 stages of 28 KB,
+// 4 tiles in flight, sent twice the L2 requests for the same bytes, each half
+// a line, and waited twice as long on instructions as hipBLASLt's
+// MT192x256x64.)  kEpi 0: half(sum); 1: half(R + half(sum)); 3: joint
+// gate/up, 96 outputs per workgroup (W tile rows 0..95 from W1, 96..191 the
+// same rows of W2; wave (wy = w / 2) takes gate rows 48 wy + 16 i as its A
+// blocks i < 3 and the same up rows as blocks i + 3).
 constexpr int kR2N = 192;                        // W rows per workgroup (96 outputs when kEpi == 3)
 constexpr int kR2T = 256;                        // tokens per workgroup
-constexpr int kR2K = 32;                         // K per stage
-constexpr int kR2A = kR2N * kR2K / 8 / 64;       // 1 KB direct loads per stage: W (12)
-constexpr int kR2B = kR2T * kR2K / 8 / 64;       // X (16)
-constexpr int kR2Loads = (kR2A + kR2B) / 4;      // per thread per stage (7)
+constexpr int kR2K = 64;                         // K per stage
+constexpr int kR2A = kR2N * kR2K / 8 / 64;       // 1 KB direct loads per stage: W (24)
+constexpr int kR2B = kR2T * kR2K / 8 / 64;       // X (32)
+constexpr int kR2Loads = (kR2A + kR2B) / 4;      // per thread per stage (14)
 
 struct __align__(16) Ring2Stage {
   uint16_t w[kR2N * kR2K];
   uint16_t x[kR2T * kR2K];
 };
-__device__ __forceinline__ int r2swz(int r) { return (r >> 1) & 3; }
+template <int S>
+struct StageIdx {
+  static constexpr int value = S;
+};
 
 template <int kEpi>
 __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvParams p) {
-  __shared__ Ring2Stage s0, s1, s2, s3, s4;
+  __shared__ __align__(128) Ring2Stage st2[2];   // 128-aligned: the step-1 XOR below commutes with the base
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar LDS bases
   constexpr int kRows = kEpi == 3 ? kR2N / 2 : kR2N;   // output rows per workgroup
   const int ttiles = (p.t + kR2T - 1) / kR2T;
   const int ntiles = (p.n + kRows - 1) / kRows;
@@ -1042,33 +1072,43 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
   const int ktiles = p.k / kR2K;
 
   // Direct load j of this wave is 1 KB load L = wave + 4 j of the stage: W
-  // rows 16 L .. +16 for L < 12, else X rows 16 (L - 12) .. +16; lane l fills
-  // row 16 L' + l / 4, position l % 4, with the row's global chunk
-  // (l % 4) ^ r2swz(row).
-  const uint16_t* src[kR2Loads];
-  unsigned dst[kR2Loads];
+  // rows 8 L .. +8 for L < 24, else X rows 8 (L - 24) .. +8; lane l fills row
+  // 8 L' + l / 8, position l % 8, with the row's global chunk (l % 8) ^ (row %
+  // 8): eight lanes read one row's whole 128-byte line.  The loads are buffer
+  // loads over each operand (W or W1, W2, X) with a fixed byte offset per lane
+  // and load and the tile's K offset in a scalar register; rows past the
+  // operand's end lie past its buffer's size and read as zeros (they feed only
+  // outputs that are not stored).
+  const int ch = (lane & 7) ^ ((lane >> 3) & 7);   // row % 8 == (lane / 8) % 8
+  const i32x4 rw = buffer_rsrc(p.w, (unsigned)((long long)p.n * p.k * 2));
+  const i32x4 rw2 = kEpi == 3 ? buffer_rsrc(p.w2, (unsigned)((long long)p.n * p.k * 2)) : rw;
+  const i32x4 rx = buffer_rsrc(p.x, (unsigned)(((long long)(p.t - 1) * p.ldx + p.k) * 2));
+  // Load j reads W (W1, then W2 from j = kR2A / 8 in the gate/up form) for
+  // j < kR2A / 4 and X after, whatever the wave: the operand, and so the
+  // descriptor, is known at compile time (a descriptor chosen at run time is
+  // a vector value, and every load then loops over its distinct values).
+  static_assert(kR2A % 8 == 0 && kR2B % 4 == 0, "loads of one operand per j");
+  unsigned voff[kR2Loads];
 #pragma unroll
   for (int j = 0; j < kR2Loads; ++j) {
     const int L = wave + 4 * j;
-    const bool isw = L < kR2A;
-    const int row = 16 * (isw ? L : L - kR2A) + (lane >> 2);
-    const int ch = (lane & 3) ^ r2swz(row);
-    if (isw) {
-      if constexpr (kEpi == 3)
-        src[j] = (row < kRows ? p.w : p.w2) + (long long)min(n0 + row % kRows, p.n - 1) * p.k + 8 * ch;
-      else
-        src[j] = p.w + (long long)min(n0 + row, p.n - 1) * p.k + 8 * ch;
+    if (j < kR2A / 4) {
+      const int row = 8 * L + (lane >> 3);
+      voff[j] = (unsigned)(n0 + row % kRows) * (unsigned)p.k * 2u + 16u * ch;
     } else {
-      src[j] = p.x + (long long)min(t0 + row, p.t - 1) * p.ldx + 8 * ch;
+      const int row = 8 * (L - kR2A) + (lane >> 3);
+      voff[j] = (unsigned)(t0 + row) * (unsigned)p.ldx * 2u + 16u * ch;
     }
-    dst[j] = (unsigned)(L * 1024);
   }
-  auto issue = [&](int kt, Ring2Stage& st) {
-    const long long ko = (long long)min(kt, ktiles - 1) * kR2K;   // tiles past the last repeat it
-    char* base = reinterpret_cast<char*>(&st);
+  auto issue = [&](int kt, int stage) {
+    char* base = reinterpret_cast<char*>(&st2[stage]);
 #pragma unroll
-    for (int j = 0; j < kR2Loads; ++j)
-      __builtin_amdgcn_global_load_lds(src[j] + ko, (__attribute__((address_space(3))) void*)(base + dst[j]), 16, 0, 0);
+    for (int j = 0; j < kR2Loads; ++j) {
+      const int L = wave + 4 * j;
+      const i32x4 r = j >= kR2A / 4 ? rx : (kEpi == 3 && j >= kR2A / 8) ? rw2 : rw;
+      buffer_load_lds16(r, (__attribute__((address_space(3))) unsigned*)(base + L * 1024), voff[j],
+                        kt * kR2K * 2);
+    }
   };
 
   const int wy = wave >> 1, wx = wave & 1;
@@ -1078,26 +1118,41 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
   for (int i = 0; i < 6; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  // Byte offsets within a stage of the lane's fragments: A (W) rows of block
-  // i, B (X) tokens of block j; chunk fg of the row.
+  // LDS addresses in stage 0 of the lane's fragments for K step 0 of a tile:
+  // A (W) rows of block i, B (X) tokens of block j; chunk fg of the row, at
+  // position fg ^ (row % 8).  Step 1's chunk 4 + fg sits at address ^ 64, and
+  // stage 1 is the read instruction's immediate offset.
+  const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&st2[0];
   unsigned aoff[6], boff[8];
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
     const int ar = (kEpi == 3 ? (i / 3) * kRows + wy * 48 + 16 * (i % 3) : wy * 96 + 16 * i) + fr;
-    aoff[i] = (unsigned)(ar * kR2K * 2 + 16 * (fg ^ r2swz(ar)));
+    aoff[i] = lds0 + (unsigned)(ar * kR2K * 2 + 16 * (fg ^ (ar & 7)));
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int br = wx * 128 + 16 * j + fr;
-    boff[j] = (unsigned)(kR2N * kR2K * 2 + br * kR2K * 2 + 16 * (fg ^ r2swz(br)));
+    boff[j] = lds0 + (unsigned)(kR2N * kR2K * 2 + br * kR2K * 2 + 16 * (fg ^ (br & 7)));
   }
   typedef f16x8 Frags[14];   // A blocks 0..5, then B blocks 0..7
-  auto read_frags = [&](const Ring2Stage& st, Frags& f) {
-    const unsigned base = (unsigned)(size_t)(const __attribute__((address_space(3))) void*)&st;
+  // Step 1's addresses are made opaque where they are formed, so they are
+  // computed at each read rather than kept live across the loop.
+  auto read1 = [&](f16x8& v, unsigned a, auto stage) {
+    if constexpr (decltype(stage)::value == 0)
+      asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
+    else
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"((int)sizeof(Ring2Stage)) : "memory");
+  };
+  auto read_frags = [&](auto stage, int ks, Frags& f) {
 #pragma unroll
-    for (int i = 0; i < 6; ++i) asm volatile("ds_read_b128 %0, %1" : "=v"(f[i]) : "v"(base + aoff[i]) : "memory");
-#pragma unroll
-    for (int j = 0; j < 8; ++j) asm volatile("ds_read_b128 %0, %1" : "=v"(f[6 + j]) : "v"(base + boff[j]) : "memory");
+    for (int i = 0; i < 14; ++i) {
+      unsigned a = i < 6 ? aoff[i] : boff[i - 6];
+      if (ks) {
+        a ^= 64u;
+        asm volatile("" : "+v"(a));
+      }
+      read1(f[i], a, stage);
+    }
   };
   auto mfma_tile = [&](const Frags& f) {
 #pragma unroll
@@ -1106,14 +1161,24 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
       for (int j = 0; j < 8; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[i], f[6 + j], acc[i][j], 0, 0, 0);
   };
-  // The fragments' registers are bound to the wait, so no use of them can be
-  // scheduled before it.  Tile kt sits in stage kt % 5; iteration kt holds
-  // its fragments (read during iteration kt - 1) and tiles kt + 1 .. kt + 4 in
-  // flight; each thread waits for its loads of tile kt + 1 (three newer tiles
-  // of 7 loads stay in flight) and its reads of tile kt, and after the
-  // barrier tile kt's stage takes tile kt + 5 (see gemm_nt_ring128_kernel).
-  auto wait_frags = [&](Frags& f) {
-    asm volatile("s_waitcnt vmcnt(21) lgkmcnt(0)\n\ts_barrier"
+  // The fragments' registers are bound to each wait, so no use of them can be
+  // scheduled before it.  Tile kt sits in stage kt % 2.  Step 0 of tile kt:
+  // wait for the reads of its fragments, read step 1's from the same stage,
+  // multiply.  Step 1: wait for those reads and for this thread's loads of
+  // tile kt + 1 (the only loads in flight), and after the barrier every wave
+  // has read tile kt's stage and every load of tile kt + 1 has landed: the
+  // stage takes tile kt + 2, and tile kt + 1's step-0 fragments are read while
+  // step 1 of tile kt is multiplied.
+  auto wait_reads = [&](Frags& f) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
+                   "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]),
+                   "+v"(f[12]), "+v"(f[13])
+                 :
+                 : "memory");
+  };
+  auto wait_all = [&](Frags& f) {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier"
                  : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
                    "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]),
                    "+v"(f[12]), "+v"(f[13])
@@ -1121,32 +1186,38 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
                  : "memory");
   };
   Frags fa, fb;
-  auto body = [&](int kt, Frags& cur, Frags& nxt, Ring2Stage& own, const Ring2Stage& next) {
-    wait_frags(cur);
-    issue(kt + 5, own);
-    read_frags(next, nxt);
-    mfma_tile(cur);
+  // No branch splits a tile's products (the register allocator then moved
+  // every accumulator at each tile): the last two tiles load the last tile
+  // again into their free stage, and after the last tile the step-0 read of
+  // the other stage only reads LDS that is never used.
+  auto tile = [&](int kt, auto own, auto next) {
+    wait_reads(fa);
+    read_frags(own, 1, fb);
+    mfma_tile(fa);
+    wait_all(fb);
+    issue(min(kt + 2, ktiles - 1), decltype(own)::value);
+    read_frags(next, 0, fa);
+    mfma_tile(fb);
   };
-  issue(0, s0);
-  issue(1, s1);
-  issue(2, s2);
-  issue(3, s3);
-  issue(4, s4);
-  asm volatile("s_waitcnt vmcnt(28)\n\ts_barrier" ::: "memory");
-  read_frags(s0, fa);
-  for (int kt = 0; kt < ktiles; kt += 10) {
-    body(kt, fa, fb, s0, s1);
-    if (kt + 1 < ktiles) body(kt + 1, fb, fa, s1, s2);
-    if (kt + 2 < ktiles) body(kt + 2, fa, fb, s2, s3);
-    if (kt + 3 < ktiles) body(kt + 3, fb, fa, s3, s4);
-    if (kt + 4 < ktiles) body(kt + 4, fa, fb, s4, s0);
-    if (kt + 5 < ktiles) body(kt + 5, fb, fa, s0, s1);
-    if (kt + 6 < ktiles) body(kt + 6, fa, fb, s1, s2);
-    if (kt + 7 < ktiles) body(kt + 7, fb, fa, s2, s3);
-    if (kt + 8 < ktiles) body(kt + 8, fa, fb, s3, s4);
-    if (kt + 9 < ktiles) body(kt + 9, fb, fa, s4, s0);
+  constexpr StageIdx<0> k0{};
+  constexpr StageIdx<1> k1{};
+  issue(0, 0);
+  if (ktiles > 1) {
+    issue(1, 1);
+    asm volatile("s_waitcnt vmcnt(14)\n\ts_barrier" ::: "memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   }
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");   // tail loads land before the workgroup ends
+  read_frags(k0, 0, fa);
+  // Four tiles per trip with guards (two per trip, or a separate odd tile
+  // after the loop, made the allocator move accumulators at every trip).
+  for (int kt = 0; kt < ktiles; kt += 4) {
+    tile(kt, k0, k1);
+    if (kt + 1 < ktiles) tile(kt + 1, k1, k0);
+    if (kt + 2 < ktiles) tile(kt + 2, k0, k1);
+    if (kt + 3 < ktiles) tile(kt + 3, k1, k0);
+  }
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 
   if constexpr (kEpi == 3) {
     // blocks (i, j) and (i + 3, j), i < 3: gate and up of outputs
@@ -1340,7 +1411,10 @@ static GemmTile pick_tile(const BatchedGemvParams& p, int rows_per_out) {
   if (p.t < kRingMinRows || !vec8) return GemmTile::k64;
   const int cus = device_cus();
   const long long big = (long long)((p.n * rows_per_out + kR2N - 1) / kR2N) * ((p.t + kR2T - 1) / kR2T);
-  if (big >= cus) return GemmTile::k192;
+  // the 192 x 256 tile's buffer loads take 32-bit byte offsets up to a tile past each operand's end
+  const bool offsets32 = (long long)(p.n + kR2N) * p.k * 2 < (1LL << 32) &&
+                         (long long)(p.t + kR2T) * p.ldx * 2 < (1LL << 32);
+  if (big >= cus && offsets32) return GemmTile::k192;
   const long long mid = (long long)((p.n * rows_per_out + kRgN - 1) / kRgN) * ((p.t + kRgT - 1) / kRgT);
   return 2 * mid >= cus ? GemmTile::k128 : GemmTile::k64;
 }

@@ -73,7 +73,11 @@ def test_exact_mode_is_the_decode_gemv(qdiy, m, n, k, with_res):
                                    # ring tile where its grid covers the CUs (ragged rows of W at
                                    # n = 6000, ragged tokens at m = 1800)
                                    (600, 130, 512), (1024, 2048, 5504), (512, 6144, 2048),
-                                   (2048, 6144, 2048), (2048, 6000, 2048), (1800, 6144, 1024)])
+                                   (2048, 6144, 2048), (2048, 6000, 2048), (1800, 6144, 1024),
+                                   # the 192 x 256 tile with 1, 2, 3 and 17 K tiles of 64 (its two
+                                   # stages never fill, fill once, or end on an odd tile)
+                                   (2048, 6144, 64), (2048, 6144, 128), (2048, 6000, 192),
+                                   (1800, 6144, 1088)])
 @pytest.mark.parametrize("with_res", [False, True])
 def test_mfma_mode_within_fp32_summation_bound(qdiy, m, n, k, with_res):
     rng = np.random.default_rng(7 * m + n + k + with_res)
@@ -103,7 +107,9 @@ def test_mfma_mode_within_fp32_summation_bound(qdiy, m, n, k, with_res):
                                         # n = 1000; 512 x 5504), the 192 x 256 ring tile (2048 x
                                         # 5504: a last tile of 32 of its 96 outputs)
                                         (600, 130, 512, 136), (1000, 1000, 1024, 1000),
-                                        (512, 5504, 2048, 5504), (2048, 5504, 2048, 5504)])
+                                        (512, 5504, 2048, 5504), (2048, 5504, 2048, 5504),
+                                        # the 192 x 256 tile over 3 K tiles, ragged tokens
+                                        (1900, 5504, 192, 5504)])
 def test_gemm_swiglu_within_bound(qdiy, m, n, k, ldy):
     """qd_gemm_swiglu: gate and up GEMMs on the matrix cores with the SwiGLU in the
     epilogue.  Each act is half(g * silu(u)) of g and u the fp16 roundings of
