@@ -58,6 +58,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-e2e]
        python bench.py --only prefill --kv T [--steps K]   (MFMA prefill attention of T tokens)
        python bench.py --only sweep --kv L [--steps K]     (read-ceiling sweep over launch shapes)
        python bench.py --only front [--steps K]            (config 4's three loops, for a profiler)
+       python bench.py --only gemm --kv T [--gemm qkv,...] [--vendor]   (MFMA prefill products)
 """
 from __future__ import annotations
 
@@ -343,6 +344,75 @@ def prefill_attention_loop(T: int, steps: int, warmup: int):
     torch.cuda.synchronize()
     log(f"[bench] profile loop 'prefill' at T={T}: {warmup + steps} qd_prefill_attention calls (MFMA)")
     ctx.close()
+
+
+def gemm_loops(T: int, steps: int, warmup: int, vendor: bool, which: str):
+    """For a profiler, and as a timing of the MFMA prefill's products: the four
+    products of one Qwen-1.8B-shaped layer at T tokens (QKV 6144 x 2048, gate and up
+    with the SwiGLU 2 x 5504 x 2048, o_proj and c_proj with the residual) through
+    qd_gemm_nt / qd_gemm_swiglu in the MFMA mode, weights of 12 layers rotated, fp16
+    N(0,1) activations and N(0, 0.02) weights; with `vendor`, the same plain products
+    through torch.matmul (hipBLASLt) after each.  `which` is a comma-separated subset
+    of qkv, gateup, oproj, cproj.  Prints one JSON line of us per call (best of three
+    windows of `steps` calls after `warmup`)."""
+    import torch
+
+    import qdiy
+
+    HID, INTER, NL = H * D, 5504, 12
+    dev = torch.device("cuda")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, device=dev, generator=gen) * scale).half()
+
+    def timeit(fn):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(steps):
+                fn(i)
+            e1.record()
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / steps)
+        return round(best, 2)
+
+    x, xi = rnd(T, HID), rnd(T, INTER)
+    res = {"tokens": T}
+    sel = which.split(",")
+    if "qkv" in sel:
+        w = rnd(NL, 3 * HID, HID, scale=0.02)
+        y = torch.empty(T, 3 * HID, dtype=torch.half, device=dev)
+        res["qkv"] = timeit(lambda i: qdiy.gemm_nt(x, w[i % NL], y, T, 3 * HID, HID, mode=qdiy.GEMM_MFMA))
+        if vendor:
+            res["qkv_vendor"] = timeit(lambda i: torch.matmul(x, w[i % NL].t(), out=y))
+        del w, y
+    if "gateup" in sel:
+        w1, w2 = rnd(NL, INTER, HID, scale=0.02), rnd(NL, INTER, HID, scale=0.02)
+        act = torch.empty(T, INTER, dtype=torch.half, device=dev)
+        res["gateup_swiglu"] = timeit(lambda i: qdiy.gemm_swiglu(x, w1[i % NL], w2[i % NL], act, T, INTER, HID))
+        if vendor:
+            w12 = torch.cat([w1, w2], dim=1)
+            yy = torch.empty(T, 2 * INTER, dtype=torch.half, device=dev)
+            res["gateup_vendor_plain"] = timeit(lambda i: torch.matmul(x, w12[i % NL].t(), out=yy))
+            del w12, yy
+        del w1, w2, act
+    for name, k_in, xin in (("oproj", HID, x), ("cproj", INTER, xi)):
+        if name not in sel:
+            continue
+        w = rnd(NL, HID, k_in, scale=0.02)
+        y = rnd(T, HID)
+        res[name + "_residual"] = timeit(
+            lambda i: qdiy.gemm_nt(xin, w[i % NL], y, T, HID, k_in, residual=y, mode=qdiy.GEMM_MFMA))
+        if vendor:
+            res[name + "_vendor"] = timeit(lambda i: torch.matmul(xin, w[i % NL].t(), out=y))
+        del w, y
+    print(json.dumps(res), flush=True)
 
 
 def measure(lib, L: int, steps: int, warmup: int, variant: int = 0, splits: int = 0,
@@ -695,13 +765,19 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="run one 256 MiB device copy (known FETCH_SIZE/WRITE_SIZE) and exit")
-    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty", "prefill", "sweep", "front"],
+    ap.add_argument("--only", choices=["call", "scan", "merge", "read", "empty", "prefill", "sweep", "front",
+                                       "gemm"],
                     help="for a profiler: run warmup + steps launches of this loop per --kv length "
                          "(call: qd_decode_attention; scan / merge: that kernel alone; read: the "
                          "read-ceiling kernel; empty: empty kernels; prefill: qd_prefill_attention "
                          "in the MFMA mode over a --kv-token prompt; front: config 4's front end "
-                         "alone, with attention as two calls, and as one call), print no JSON, "
-                         "and exit")
+                         "alone, with attention as two calls, and as one call; gemm: the MFMA "
+                         "prefill's four products at --kv tokens, see --gemm), print no bench "
+                         "JSON, and exit")
+    ap.add_argument("--gemm", default="qkv,gateup,oproj,cproj",
+                    help="--only gemm: products to run (qkv, gateup, oproj, cproj)")
+    ap.add_argument("--vendor", action="store_true",
+                    help="--only gemm: also time the plain products through torch.matmul (hipBLASLt)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path "
@@ -734,6 +810,10 @@ def main() -> int:
         return 0
     if args.only == "front":
         front_loops(lib, args.steps, args.warmup)
+        return 0
+    if args.only == "gemm":
+        for T in args.kv:
+            gemm_loops(T, args.steps, args.warmup, args.vendor, args.gemm)
         return 0
     if args.only == "sweep":
         num_cus = torch.cuda.get_device_properties(0).multi_processor_count
