@@ -1014,6 +1014,8 @@ __device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, __attribute__((add
                                                   unsigned voffset, int soffset) {
   raw_buffer_load_lds(rsrc, lds, 16, (int)voffset, soffset, 0, 0);
 }
+__device__ i32x4 raw_buffer_load_b128(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
 
 // The same product with a 192-row x 256-token workgroup tile (products whose
 // grid of such tiles still covers the device: QKV and gate/up at 2048 tokens,
@@ -1025,16 +1027,19 @@ __device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, __attribute__((add
 // SQ_BUSY_CYCLES).  Here each of the four waves computes 96 W rows x 128
 // tokens (6 x 8 MFMA blocks, 192 accumulator registers): 37 B per clock from
 // L2 and ~110 from LDS at the matrix cores' rate.  K goes in tiles of 64
-// through two stages of 56 KB (W tile 192 x 128 B, then X tile 256 x 128 B;
-// chunk q of row r at q ^ (r % 8), so the eight rows that one eight-lane
-// group of a fragment read covers fall on distinct banks), filled by direct
-// loads (14 per thread per stage) whose eight-lane groups each read one whole
-// 128-byte line.  Fragments go in K steps of 32, two per tile: the next
-// step's fragments are read from LDS while the matrix cores consume the
-// current one's, and a stage takes tile kt + 2 as soon as every wave has read
-// tile kt's second step.  (32-wide tiles through a ring of 5 stages of 28 KB,
-// 4 tiles in flight, sent twice the L2 requests for the same bytes, each half
-// a line, and waited twice as long on instructions as hipBLASLt's
+// through two stages each for W (192 x 128 B) and X (256 x 128 B); chunk q of
+// row r at q ^ (r % 8), so the eight rows that one eight-lane group of a
+// fragment read covers fall on distinct banks.  Every load is 16 bytes per
+// lane, eight lanes to one row's whole 128-byte line: X's 8 per thread and
+// tile go straight into LDS, W's 6 go through registers and are stored one
+// tile later.  (With both operands on one path the kernel was slower: direct
+// loads alone 6% on gate/up, registers alone 15-20%; the two paths together
+// move more.)  Fragments go in K steps of 32, two per tile: the next step's
+// fragments are read from LDS while the matrix cores consume the current
+// one's, and a stage takes tile kt + 2 as soon as every wave has read tile
+// kt's second step.  (32-wide tiles through a ring of 5 stages of 28 KB, 4
+// tiles in flight, sent twice the L2 requests for the same bytes, each half a
+// line, and waited twice as long on instructions as hipBLASLt's
 // MT192x256x64.)  kEpi 0: half(sum); 1: half(R + half(sum)); 3: joint
 // gate/up, 96 outputs per workgroup (W tile rows 0..95 from W1, 96..191 the
 // same rows of W2; wave (wy = w / 2) takes gate rows 48 wy + 16 i as its A
@@ -1046,10 +1051,6 @@ constexpr int kR2A = kR2N * kR2K / 8 / 64;       // 1 KB direct loads per stage:
 constexpr int kR2B = kR2T * kR2K / 8 / 64;       // X (32)
 constexpr int kR2Loads = (kR2A + kR2B) / 4;      // per thread per stage (14)
 
-struct __align__(16) Ring2Stage {
-  uint16_t w[kR2N * kR2K];
-  uint16_t x[kR2T * kR2K];
-};
 template <int S>
 struct StageIdx {
   static constexpr int value = S;
@@ -1057,7 +1058,10 @@ struct StageIdx {
 
 template <int kEpi>
 __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvParams p) {
-  __shared__ __align__(128) Ring2Stage st2[2];   // 128-aligned: the step-1 XOR below commutes with the base
+  // W and X tiles in two stages each; 128-aligned, so the step-1 XOR below
+  // commutes with every stage base
+  __shared__ __align__(128) uint16_t lw[2][kR2N * kR2K];
+  __shared__ __align__(128) uint16_t lx[2][kR2T * kR2K];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar LDS bases
@@ -1071,9 +1075,9 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
   const int t0 = (pi % ttiles) * kR2T;
   const int ktiles = p.k / kR2K;
 
-  // Direct load j of this wave is 1 KB load L = wave + 4 j of the stage: W
-  // rows 8 L .. +8 for L < 24, else X rows 8 (L - 24) .. +8; lane l fills row
-  // 8 L' + l / 8, position l % 8, with the row's global chunk (l % 8) ^ (row %
+  // Load j of this wave is 1 KB load L = wave + 4 j of a tile: W rows 8 L ..
+  // +8 for L < 24, else X rows 8 (L - 24) .. +8; lane l fills row 8 L' + l / 8
+  // of its stage, position l % 8, with the row's global chunk (l % 8) ^ (row %
   // 8): eight lanes read one row's whole 128-byte line.  The loads are buffer
   // loads over each operand (W or W1, W2, X) with a fixed byte offset per lane
   // and load and the tile's K offset in a scalar register; rows past the
@@ -1100,15 +1104,28 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
       voff[j] = (unsigned)(t0 + row) * (unsigned)p.ldx * 2u + 16u * ch;
     }
   }
-  auto issue = [&](int kt, int stage) {
-    char* base = reinterpret_cast<char*>(&st2[stage]);
+  // W goes through registers (a tile's loads land in wr while the tile before
+  // is multiplied, then are stored to LDS in the same layout); X goes
+  // straight into LDS.
+  i32x4 wr[kR2A / 4];
+  auto load_w = [&](int kt) {
 #pragma unroll
-    for (int j = 0; j < kR2Loads; ++j) {
-      const int L = wave + 4 * j;
-      const i32x4 r = j >= kR2A / 4 ? rx : (kEpi == 3 && j >= kR2A / 8) ? rw2 : rw;
-      buffer_load_lds16(r, (__attribute__((address_space(3))) unsigned*)(base + L * 1024), voff[j],
-                        kt * kR2K * 2);
-    }
+    for (int j = 0; j < kR2A / 4; ++j)
+      wr[j] = raw_buffer_load_b128((kEpi == 3 && j >= kR2A / 8) ? rw2 : rw, (int)voff[j], kt * kR2K * 2, 0);
+  };
+  auto store_w = [&](int stage) {
+    char* base = reinterpret_cast<char*>(lw[stage]);
+#pragma unroll
+    for (int j = 0; j < kR2A / 4; ++j)
+      *reinterpret_cast<__attribute__((address_space(3))) i32x4*>(
+          (__attribute__((address_space(3))) char*)(base + (wave + 4 * j) * 1024 + 16 * lane)) = wr[j];
+  };
+  auto issue_x = [&](int kt, int stage) {
+    char* base = reinterpret_cast<char*>(lx[stage]);
+#pragma unroll
+    for (int j = kR2A / 4; j < kR2Loads; ++j)
+      buffer_load_lds16(rx, (__attribute__((address_space(3))) unsigned*)(base + (wave + 4 * j - kR2A) * 1024),
+                        voff[j], kt * kR2K * 2);
   };
 
   const int wy = wave >> 1, wx = wave & 1;
@@ -1122,28 +1139,33 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
   // A (W) rows of block i, B (X) tokens of block j; chunk fg of the row, at
   // position fg ^ (row % 8).  Step 1's chunk 4 + fg sits at address ^ 64, and
   // stage 1 is the read instruction's immediate offset.
-  const unsigned lds0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&st2[0];
+  const unsigned lw0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&lw[0][0];
+  const unsigned lx0 = (unsigned)(size_t)(__attribute__((address_space(3))) void*)&lx[0][0];
+  constexpr int kWStage = kR2N * kR2K * 2, kXStage = kR2T * kR2K * 2;   // bytes
   unsigned aoff[6], boff[8];
 #pragma unroll
   for (int i = 0; i < 6; ++i) {
     const int ar = (kEpi == 3 ? (i / 3) * kRows + wy * 48 + 16 * (i % 3) : wy * 96 + 16 * i) + fr;
-    aoff[i] = lds0 + (unsigned)(ar * kR2K * 2 + 16 * (fg ^ (ar & 7)));
+    aoff[i] = lw0 + (unsigned)(ar * kR2K * 2 + 16 * (fg ^ (ar & 7)));
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int br = wx * 128 + 16 * j + fr;
-    boff[j] = lds0 + (unsigned)(kR2N * kR2K * 2 + br * kR2K * 2 + 16 * (fg ^ (br & 7)));
+    boff[j] = lx0 + (unsigned)(br * kR2K * 2 + 16 * (fg ^ (br & 7)));
   }
   typedef f16x8 Frags[14];   // A blocks 0..5, then B blocks 0..7
   // Step 1's addresses are made opaque where they are formed, so they are
   // computed at each read rather than kept live across the loop.
-  auto read1 = [&](f16x8& v, unsigned a, auto stage) {
-    if constexpr (decltype(stage)::value == 0)
+  auto read1 = [&](f16x8& v, unsigned a, auto off) {
+    constexpr int o = decltype(off)::value;
+    if constexpr (o == 0)
       asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
     else
-      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"((int)sizeof(Ring2Stage)) : "memory");
+      asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(o) : "memory");
   };
   auto read_frags = [&](auto stage, int ks, Frags& f) {
+    constexpr StageIdx<decltype(stage)::value * kWStage> wo{};
+    constexpr StageIdx<decltype(stage)::value * kXStage> xo{};
 #pragma unroll
     for (int i = 0; i < 14; ++i) {
       unsigned a = i < 6 ? aoff[i] : boff[i - 6];
@@ -1151,7 +1173,10 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
         a ^= 64u;
         asm volatile("" : "+v"(a));
       }
-      read1(f[i], a, stage);
+      if (i < 6)
+        read1(f[i], a, wo);
+      else
+        read1(f[i], a, xo);
     }
   };
   auto mfma_tile = [&](const Frags& f) {
@@ -1178,7 +1203,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
                  : "memory");
   };
   auto wait_all = [&](Frags& f) {
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier"
+    asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier"
                  : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
                    "+v"(f[6]), "+v"(f[7]), "+v"(f[8]), "+v"(f[9]), "+v"(f[10]), "+v"(f[11]),
                    "+v"(f[12]), "+v"(f[13])
@@ -1190,24 +1215,29 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring192_kernel(BatchedGemvPara
   // every accumulator at each tile): the last two tiles load the last tile
   // again into their free stage, and after the last tile the step-0 read of
   // the other stage only reads LDS that is never used.
+  // Step 0 of tile kt also stores W(kt + 1) from wr into the other W stage
+  // (every wave has read tile kt - 1's, which sat there, before the last
+  // barrier) and loads W(kt + 2) into wr; step 1 waits for X(kt + 1), the
+  // newest loads in flight being W(kt + 2)'s 6.
   auto tile = [&](int kt, auto own, auto next) {
     wait_reads(fa);
+    store_w(decltype(next)::value);
+    load_w(min(kt + 2, ktiles - 1));
     read_frags(own, 1, fb);
     mfma_tile(fa);
     wait_all(fb);
-    issue(min(kt + 2, ktiles - 1), decltype(own)::value);
+    issue_x(min(kt + 2, ktiles - 1), decltype(own)::value);
     read_frags(next, 0, fa);
     mfma_tile(fb);
   };
   constexpr StageIdx<0> k0{};
   constexpr StageIdx<1> k1{};
-  issue(0, 0);
-  if (ktiles > 1) {
-    issue(1, 1);
-    asm volatile("s_waitcnt vmcnt(14)\n\ts_barrier" ::: "memory");
-  } else {
-    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-  }
+  load_w(0);
+  issue_x(0, 0);
+  store_w(0);
+  load_w(min(1, ktiles - 1));
+  issue_x(min(1, ktiles - 1), 1);
+  asm volatile("s_waitcnt vmcnt(14) lgkmcnt(0)\n\ts_barrier" ::: "memory");   // W(0) stored, X(0) landed
   read_frags(k0, 0, fa);
   // Four tiles per trip with guards (two per trip, or a separate odd tile
   // after the loop, made the allocator move accumulators at every trip).
