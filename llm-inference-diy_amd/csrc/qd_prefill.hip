@@ -739,6 +739,31 @@ __global__ __launch_bounds__(256) void splitk_fold_kernel(BatchedGemvParams p, i
   reinterpret_cast<_Float16*>(p.y)[t * p.ldy + n] = y;
 }
 
+// Buffer resource over `bytes` bytes from `base` (raw: no stride, no
+// swizzle; word 3 the data format gfx9 parts take for untyped loads), and the
+// buffer load of 16 bytes per lane into LDS (lane l at lds + 16 l; M0 holds
+// the wave-uniform LDS base) at base + voffset + soffset.  Bytes at or past
+// `bytes` read as zeros.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, unsigned bytes) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  i32x4 r;
+  r[0] = (int)(unsigned)a;
+  r[1] = (int)(unsigned)(a >> 32);
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
+}
+__device__ void raw_buffer_load_lds(i32x4 rsrc, __attribute__((address_space(3))) unsigned* lds, int size,
+                                    int voffset, int soffset, int offset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.lds");
+__device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, __attribute__((address_space(3))) unsigned* lds,
+                                                  unsigned voffset, int soffset) {
+  raw_buffer_load_lds(rsrc, lds, 16, (int)voffset, soffset, 0, 0);
+}
+__device__ i32x4 raw_buffer_load_b128(i32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+
 constexpr int kGemmXcds = 8;                 // MI355X: workgroups are dealt to 8 XCDs in turn
 constexpr int kRingMinRows = 128;            // the ring tiles from this many tokens
 constexpr int kGemmMaxSplits = 8;            // K slices of a split product
@@ -786,7 +811,7 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring128_kernel(BatchedGemvPara
   __shared__ RingStage s0, s1, s2, s3, s4;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar LDS bases
   constexpr int kRows = kEpi == 3 ? kRgN / 2 : kRgN;   // output rows per workgroup
   const int ttiles = (p.t + kRgT - 1) / kRgT;
   const int ntiles = (p.n + kRows - 1) / kRows;
@@ -809,27 +834,31 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring128_kernel(BatchedGemvPara
 
   // Load i of wave w writes 1 KB at chunk 256 i + 64 w + lane of the stage's
   // operand: row 32 i + 8 w + lane / 8, position lane % 8, which holds the
-  // row's global chunk (lane % 8) ^ mmswz(row).
-  const uint16_t* wg[kRgOps];
-  const uint16_t* xg[kRgOps];
+  // row's global chunk (lane % 8) ^ mmswz(row).  Buffer loads over each
+  // operand (W or W1 and W2, X): a fixed 32-bit byte offset per lane and load,
+  // the tile's K offset in a scalar register; rows past an operand's end lie
+  // past its buffer's size and read as zeros (they feed only outputs that are
+  // not stored).
+  const int ch = (lane & 7) ^ ((lane >> 3) & 7);   // row % 8 == (lane / 8) % 8
+  const i32x4 rw = buffer_rsrc(p.w, (unsigned)((long long)p.n * p.k * 2));
+  const i32x4 rw2 = kEpi == 3 ? buffer_rsrc(p.w2, (unsigned)((long long)p.n * p.k * 2)) : rw;
+  const i32x4 rx = buffer_rsrc(p.x, (unsigned)(((long long)(p.t - 1) * p.ldx + p.k) * 2));
+  unsigned vw[kRgOps], vx[kRgOps];
 #pragma unroll
   for (int i = 0; i < kRgOps; ++i) {
     const int row = 32 * i + 8 * wave + (lane >> 3);
-    const int ch = (lane & 7) ^ mmswz(row);
-    if constexpr (kEpi == 3)
-      wg[i] = (row < 64 ? p.w : p.w2) + (long long)min(n0 + (row & 63), p.n - 1) * p.k + 8 * ch;
-    else
-      wg[i] = p.w + (long long)min(n0 + row, p.n - 1) * p.k + kbeg + 8 * ch;
-    xg[i] = p.x + (long long)min(t0 + row, p.t - 1) * p.ldx + kbeg + 8 * ch;
+    vw[i] = kEpi == 3 ? (unsigned)(n0 + (row & 63)) * (unsigned)p.k * 2u + 16u * ch
+                      : (unsigned)(n0 + row) * (unsigned)p.k * 2u + (unsigned)kbeg * 2u + 16u * ch;
+    vx[i] = (unsigned)(t0 + row) * (unsigned)p.ldx * 2u + (unsigned)kbeg * 2u + 16u * ch;
   }
   auto issue = [&](int kt, RingStage& st) {
-    const long long ko = (long long)min(kt, ktiles - 1) * kRgK;   // tiles past the last repeat it
+    const int so = min(kt, ktiles - 1) * kRgK * 2;   // tiles past the last repeat it
 #pragma unroll
     for (int i = 0; i < kRgOps; ++i) {
-      __builtin_amdgcn_global_load_lds(wg[i] + ko, (__attribute__((address_space(3))) void*)&st.w[(256 * i + 64 * wave) * 8],
-                                       16, 0, 0);
-      __builtin_amdgcn_global_load_lds(xg[i] + ko, (__attribute__((address_space(3))) void*)&st.x[(256 * i + 64 * wave) * 8],
-                                       16, 0, 0);
+      // rows 64.. of the gate/up form's W tile are W2's (i >= 2)
+      buffer_load_lds16((kEpi == 3 && i >= kRgOps / 2) ? rw2 : rw,
+                        (__attribute__((address_space(3))) unsigned*)&st.w[(256 * i + 64 * wave) * 8], vw[i], so);
+      buffer_load_lds16(rx, (__attribute__((address_space(3))) unsigned*)&st.x[(256 * i + 64 * wave) * 8], vx[i], so);
     }
   };
 
@@ -991,31 +1020,6 @@ __global__ __launch_bounds__(256, 1) void gemm_nt_ring128_kernel(BatchedGemvPara
     }
   }
 }
-
-// Buffer resource over `bytes` bytes from `base` (raw: no stride, no
-// swizzle; word 3 the data format gfx9 parts take for untyped loads), and the
-// buffer load of 16 bytes per lane into LDS (lane l at lds + 16 l; M0 holds
-// the wave-uniform LDS base) at base + voffset + soffset.  Bytes at or past
-// `bytes` read as zeros.
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, unsigned bytes) {
-  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
-  i32x4 r;
-  r[0] = (int)(unsigned)a;
-  r[1] = (int)(unsigned)(a >> 32);
-  r[2] = (int)bytes;
-  r[3] = 0x00020000;
-  return r;
-}
-__device__ void raw_buffer_load_lds(i32x4 rsrc, __attribute__((address_space(3))) unsigned* lds, int size,
-                                    int voffset, int soffset, int offset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.lds");
-__device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, __attribute__((address_space(3))) unsigned* lds,
-                                                  unsigned voffset, int soffset) {
-  raw_buffer_load_lds(rsrc, lds, 16, (int)voffset, soffset, 0, 0);
-}
-__device__ i32x4 raw_buffer_load_b128(i32x4 rsrc, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
 
 // The same product with a 192-row x 256-token workgroup tile (products whose
 // grid of such tiles still covers the device: QKV and gate/up at 2048 tokens,
@@ -1435,6 +1439,11 @@ hipError_t launch_swiglu_batched(const uint16_t* g, const uint16_t* u, uint16_t*
 // the 512-token QKV product as fast as hipBLASLt), else the 64 x 64 tile.
 enum class GemmTile { k64, k128, k192 };
 
+// The 128 x 128 tile's buffer loads take 32-bit byte offsets up to a tile past each operand's end.
+static bool ring128_offsets32(const BatchedGemvParams& p) {
+  return (long long)(p.n + kRgN) * p.k * 2 < (1LL << 32) && (long long)(p.t + kRgT) * p.ldx * 2 < (1LL << 32);
+}
+
 static GemmTile pick_tile(const BatchedGemvParams& p, int rows_per_out) {
   const bool vec8 = ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) == 0 &&
                     p.ldy % 4 == 0;
@@ -1446,7 +1455,7 @@ static GemmTile pick_tile(const BatchedGemvParams& p, int rows_per_out) {
                          (long long)(p.t + kR2T) * p.ldx * 2 < (1LL << 32);
   if (big >= cus && offsets32) return GemmTile::k192;
   const long long mid = (long long)((p.n * rows_per_out + kRgN - 1) / kRgN) * ((p.t + kRgT - 1) / kRgT);
-  return 2 * mid >= cus ? GemmTile::k128 : GemmTile::k64;
+  return 2 * mid >= cus && ring128_offsets32(p) ? GemmTile::k128 : GemmTile::k64;
 }
 
 hipError_t launch_gemm_mfma(const BatchedGemvParams& p, int epi, hipStream_t stream) {
@@ -1511,7 +1520,7 @@ hipError_t launch_gemm_mfma_split(const BatchedGemvParams& p, int epi, float* wo
                                   size_t workspace_bytes, hipStream_t stream) {
   if (p.k < 64 || p.k % 64 != 0 || p.t < 1 || p.n < 1) return hipErrorInvalidValue;
   const GemmTile tile = pick_tile(p, 1);
-  const bool ring = p.t >= kRingMinRows && p.n % 4 == 0 && tile != GemmTile::k192 &&
+  const bool ring = p.t >= kRingMinRows && p.n % 4 == 0 && tile != GemmTile::k192 && ring128_offsets32(p) &&
                     ((reinterpret_cast<uintptr_t>(p.y) | reinterpret_cast<uintptr_t>(p.res)) & 7u) == 0 &&
                     p.ldy % 4 == 0;
   const int tn = ring ? kRgN : kMmTile, tt = ring ? kRgT : kMmTile;
